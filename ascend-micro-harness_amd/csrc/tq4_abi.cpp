@@ -1,0 +1,307 @@
+// tq4_abi.cpp -- the C ABI of libtq4.so (declared in include/tq4.h).
+//
+// Each entry point validates its geometry on the host, the way the
+// reference launchers do (turboquant_reshape_and_cache_a8.cpp:1597-1609,
+// turboquant_paged_decode_attention.cpp:1746-1759), but returns a tq4_status
+// instead of throwing across the C boundary; nothing is launched on a
+// refusal. Launches are asynchronous on the caller's stream.
+#include <hip/hip_runtime.h>
+
+#include "../../include/tq4.h"
+#include "tq4_internal.hpp"
+
+namespace {
+
+constexpr uint32_t kStrip = 16;
+
+bool head_size_ok(uint32_t d) { return d == 64 || d == 128 || d == 256; }
+
+int launched(hipError_t e) { return e == hipSuccess ? TQ4_OK : TQ4_ERR_LAUNCH; }
+
+int writer_checks(const void* key, const void* value, const int8_t* key_cache,
+                  const int8_t* value_cache, const float* scale_cache, const int32_t* slots,
+                  const float* pi_signs, const int32_t* tables, uint32_t num_tokens,
+                  uint32_t num_kv_heads, uint32_t head_size, uint32_t block_size,
+                  uint32_t num_blocks, uint32_t tokens_per_core)
+{
+    if (!head_size_ok(head_size)) return TQ4_ERR_HEAD_SIZE;
+    if (num_kv_heads == 0 || num_blocks == 0 || block_size == 0 || block_size % kStrip)
+        return TQ4_ERR_GEOMETRY;
+    // WholeStrips (turboquant_wave_protocol.hpp:179-185): a partial trailing
+    // strip would be silently dropped, so the geometry is refused.
+    if (tokens_per_core == 0 || tokens_per_core % kStrip || num_tokens % tokens_per_core)
+        return TQ4_ERR_PARTIAL_STRIP;
+    if (num_tokens == 0) return TQ4_OK;
+    if (!key || !value || !key_cache || !value_cache || !scale_cache || !slots)
+        return TQ4_ERR_NULL_POINTER;
+    if (!pi_signs && !tables) return TQ4_ERR_ROTATION;
+    const uint64_t blocks = (uint64_t)(num_tokens / kStrip) * num_kv_heads * 2u;
+    if (blocks > 0x7fffffffull) return TQ4_ERR_RANGE;
+    return TQ4_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* tq4_status_string(int status)
+{
+    switch (status) {
+        case TQ4_OK: return "ok";
+        case TQ4_ERR_NULL_POINTER: return "a required pointer is NULL";
+        case TQ4_ERR_HEAD_SIZE: return "head_size must be 64, 128 or 256";
+        case TQ4_ERR_GEOMETRY: return "invalid geometry (heads, blocks, block_size % 16, GQA group)";
+        case TQ4_ERR_PARTIAL_STRIP:
+            return "num_tokens must be a whole number of tokens_per_core strips (multiple of 16)";
+        case TQ4_ERR_SPLITS: return "num_splits out of range";
+        case TQ4_ERR_WORKSPACE: return "workspace missing or too small";
+        case TQ4_ERR_OUTPUT_STAGE: return "output_stage must be 0, 1 or 2 (2 needs a gate)";
+        case TQ4_ERR_ROTATION: return "neither pi_signs nor tables given";
+        case TQ4_ERR_LAUNCH: return "the HIP runtime refused the launch";
+        case TQ4_ERR_RANGE: return "a size exceeds the kernels' index range";
+        default: return "unknown status";
+    }
+}
+
+uint32_t tq4_version(void) { return (1u << 16) | 0u; }
+
+int tq4_reshape_and_cache_a8(void* stream, const int8_t* key, const int8_t* value,
+                             int8_t* key_cache, int8_t* value_cache, float* scale_cache,
+                             const int32_t* slot_mapping, const float* pi_signs,
+                             const int32_t* tables, uint32_t num_tokens, uint32_t num_kv_heads,
+                             uint32_t head_size, uint32_t block_size, uint32_t num_blocks,
+                             uint32_t tokens_per_core, float inv_sqrt_len,
+                             bool reuse_mode4_flags)
+{
+    (void)reuse_mode4_flags;
+    const int rc = writer_checks(key, value, key_cache, value_cache, scale_cache, slot_mapping,
+                                 pi_signs, tables, num_tokens, num_kv_heads, head_size,
+                                 block_size, num_blocks, tokens_per_core);
+    if (rc != TQ4_OK || num_tokens == 0) return rc;
+    return launched(tq4::launch_strip_writer((hipStream_t)stream, 0, key, value, key_cache,
+                                             value_cache, scale_cache, slot_mapping, pi_signs,
+                                             tables, num_tokens / kStrip, num_kv_heads, head_size,
+                                             block_size, num_blocks, inv_sqrt_len));
+}
+
+int tq4_reshape_and_cache_bf16(void* stream, const uint16_t* key, const uint16_t* value,
+                               int8_t* key_cache, int8_t* value_cache, float* scale_cache,
+                               const int32_t* slot_mapping, const float* pi_signs,
+                               const int32_t* tables, uint32_t num_tokens,
+                               uint32_t num_kv_heads, uint32_t head_size, uint32_t block_size,
+                               uint32_t num_blocks, uint32_t tokens_per_core,
+                               float inv_sqrt_len, bool reuse_mode4_flags)
+{
+    (void)reuse_mode4_flags;
+    const int rc = writer_checks(key, value, key_cache, value_cache, scale_cache, slot_mapping,
+                                 pi_signs, tables, num_tokens, num_kv_heads, head_size,
+                                 block_size, num_blocks, tokens_per_core);
+    if (rc != TQ4_OK || num_tokens == 0) return rc;
+    return launched(tq4::launch_strip_writer((hipStream_t)stream, 1, key, value, key_cache,
+                                             value_cache, scale_cache, slot_mapping, pi_signs,
+                                             tables, num_tokens / kStrip, num_kv_heads, head_size,
+                                             block_size, num_blocks, inv_sqrt_len));
+}
+
+int tq4_reshape_scatter(void* stream, uint32_t block_dim, const uint16_t* key,
+                        const uint16_t* value, int8_t* key_cache, int8_t* value_cache,
+                        float* scale_cache, const int32_t* slot_mapping, const float* pi_signs,
+                        const int32_t* cu_seqlens, int32_t* launch_probe, uint32_t num_requests,
+                        uint32_t num_kv_heads, uint32_t head_size, uint32_t block_size,
+                        uint32_t num_blocks, uint32_t item_begin, uint32_t item_count,
+                        float inv_sqrt_len)
+{
+    if (!head_size_ok(head_size)) return TQ4_ERR_HEAD_SIZE;
+    if (num_kv_heads == 0 || num_blocks == 0 || block_size == 0 || block_size % kStrip)
+        return TQ4_ERR_GEOMETRY;
+    if (item_count == 0 || num_requests == 0) return TQ4_OK;
+    if (!key || !value || !key_cache || !value_cache || !scale_cache || !slot_mapping ||
+        !pi_signs)
+        return TQ4_ERR_NULL_POINTER;
+    uint32_t grid = block_dim == 0 ? item_count : block_dim;
+    if (grid > item_count) grid = item_count;
+    if (grid > 65535u * 16u) grid = 65535u * 16u;
+    return launched(tq4::launch_scatter_writer(
+        (hipStream_t)stream, grid, key, value, key_cache, value_cache, scale_cache, slot_mapping,
+        pi_signs, cu_seqlens, launch_probe, num_requests, num_kv_heads, head_size, block_size,
+        num_blocks, item_begin, item_count, inv_sqrt_len));
+}
+
+size_t tq4_decode_workspace_bytes(uint32_t num_seqs, uint32_t num_heads, uint32_t num_kv_heads,
+                                  uint32_t head_size, uint32_t num_splits)
+{
+    if (num_splits == 0) num_splits = TQ4_MAX_SPLITS;
+    return tq4::decode_records_bytes(num_seqs, num_heads, head_size, num_splits) +
+           (((size_t)num_seqs * num_kv_heads * sizeof(uint32_t) + 255) & ~(size_t)255);
+}
+
+uint32_t tq4_decode_auto_splits(uint32_t num_seqs, uint32_t num_kv_heads,
+                                uint32_t max_blocks_per_seq, uint32_t block_size)
+{
+    // Enough workgroups for every CU several times over (256 CUs), but at
+    // least ~8 strips per workgroup so a split is not all prologue.
+    const uint64_t items = (uint64_t)num_seqs * num_kv_heads;
+    const uint64_t target_wgs = 1024;
+    uint64_t k = items == 0 ? 1 : (target_wgs + items - 1) / items;
+    const uint64_t strips = (uint64_t)max_blocks_per_seq * (block_size / kStrip);
+    uint64_t by_len = strips / 8;
+    if (by_len < 1) by_len = 1;
+    if (k > by_len) k = by_len;
+    if (k > TQ4_MAX_SPLITS) k = TQ4_MAX_SPLITS;
+    if (k < 1) k = 1;
+    return (uint32_t)k;
+}
+
+int tq4_decode_workspace_init(void* stream, void* workspace, size_t workspace_bytes)
+{
+    if (!workspace) return TQ4_ERR_WORKSPACE;
+    return launched(tq4::launch_fill_zero((hipStream_t)stream, workspace, workspace_bytes));
+}
+
+namespace {
+
+int decode_checks(const uint16_t* q, const int8_t* kc, const int8_t* vc, const float* sc,
+                  const int32_t* tables, const int32_t* ctx, const float* pi_signs,
+                  uint32_t num_seqs, uint32_t num_heads, uint32_t num_kv_heads,
+                  uint32_t head_size, uint32_t block_size, uint32_t num_blocks,
+                  uint32_t max_blocks_per_seq, uint32_t flags)
+{
+    if (!head_size_ok(head_size)) return TQ4_ERR_HEAD_SIZE;
+    if (num_seqs == 0 || num_kv_heads == 0 || num_heads == 0 || num_heads % num_kv_heads ||
+        num_heads / num_kv_heads > 16 || block_size == 0 || block_size % kStrip ||
+        num_blocks == 0 || max_blocks_per_seq == 0)
+        return TQ4_ERR_GEOMETRY;
+    if (!q || !kc || !vc || !sc || !tables || !ctx) return TQ4_ERR_NULL_POINTER;
+    if (!(flags & TQ4_DECODE_QUERY_ROTATED) && !pi_signs) return TQ4_ERR_ROTATION;
+    return TQ4_OK;
+}
+
+tq4::DecodeParams make_params(const uint16_t* q, const int8_t* kc, const int8_t* vc,
+                              const float* sc, const int32_t* tables, const int32_t* ctx,
+                              const float* pi_signs, const float* gate, uint32_t num_seqs,
+                              uint32_t num_heads, uint32_t num_kv_heads, uint32_t head_size,
+                              uint32_t block_size, uint32_t num_blocks,
+                              uint32_t max_blocks_per_seq, uint32_t num_splits, float scale,
+                              float inv_sqrt_len, uint32_t output_stage, uint32_t flags)
+{
+    tq4::DecodeParams p{};
+    p.q = q;
+    p.key_cache = kc;
+    p.value_cache = vc;
+    p.scale_cache = sc;
+    p.block_tables = tables;
+    p.context_lens = ctx;
+    p.pi_signs = pi_signs;
+    p.gate = gate;
+    p.B = num_seqs;
+    p.Hq = num_heads;
+    p.Hkv = num_kv_heads;
+    p.G = num_heads / num_kv_heads;
+    p.D = head_size;
+    p.S = block_size;
+    p.P = num_blocks;
+    p.max_blocks = max_blocks_per_seq;
+    p.K = num_splits;
+    p.scale = scale;
+    p.inv_sqrt_len = inv_sqrt_len;
+    p.output_stage = output_stage;
+    p.flags = flags;
+    return p;
+}
+
+}  // namespace
+
+int tq4_paged_decode(void* stream, const uint16_t* q, const int8_t* key_cache,
+                     const int8_t* value_cache, const float* scale_cache,
+                     const int32_t* block_tables, const int32_t* context_lens,
+                     const float* pi_signs, const float* gate, void* workspace,
+                     size_t workspace_bytes, uint16_t* out, uint32_t num_seqs,
+                     uint32_t num_heads, uint32_t num_kv_heads, uint32_t head_size,
+                     uint32_t block_size, uint32_t num_blocks, uint32_t max_blocks_per_seq,
+                     uint32_t num_splits, float scale, float inv_sqrt_len,
+                     uint32_t output_stage, uint32_t flags)
+{
+    int rc = decode_checks(q, key_cache, value_cache, scale_cache, block_tables, context_lens,
+                           pi_signs, num_seqs, num_heads, num_kv_heads, head_size, block_size,
+                           num_blocks, max_blocks_per_seq, flags);
+    if (rc != TQ4_OK) return rc;
+    if (!out) return TQ4_ERR_NULL_POINTER;
+    if (output_stage > 2 || (output_stage == 2 && !gate)) return TQ4_ERR_OUTPUT_STAGE;
+    if (output_stage >= 1 && !pi_signs) return TQ4_ERR_ROTATION;
+    if (num_splits == 0)
+        num_splits = tq4_decode_auto_splits(num_seqs, num_kv_heads, max_blocks_per_seq, block_size);
+    if (num_splits > TQ4_MAX_SPLITS) return TQ4_ERR_SPLITS;
+    if ((uint64_t)num_seqs * num_kv_heads * num_splits > 0x7fffffffull) return TQ4_ERR_RANGE;
+    tq4::DecodeParams p = make_params(q, key_cache, value_cache, scale_cache, block_tables,
+                                      context_lens, pi_signs, gate, num_seqs, num_heads,
+                                      num_kv_heads, head_size, block_size, num_blocks,
+                                      max_blocks_per_seq, num_splits, scale, inv_sqrt_len,
+                                      output_stage, flags);
+    p.out = out;
+    if (num_splits > 1) {
+        const size_t need =
+            tq4_decode_workspace_bytes(num_seqs, num_heads, num_kv_heads, head_size, num_splits);
+        if (!workspace || workspace_bytes < need) return TQ4_ERR_WORKSPACE;
+        p.records = (float*)workspace;
+        // The counters sit at the END of the workspace so their place does not
+        // depend on num_splits: a workspace zeroed once serves every split count.
+        p.counters = (uint32_t*)((char*)workspace + workspace_bytes -
+                                 (((size_t)num_seqs * num_kv_heads * sizeof(uint32_t) + 255) &
+                                  ~(size_t)255));
+    }
+    return launched(tq4::launch_decode((hipStream_t)stream, p, 1));
+}
+
+int tq4_paged_decode_partials(void* stream, const uint16_t* q, const int8_t* key_cache,
+                              const int8_t* value_cache, const float* scale_cache,
+                              const int32_t* block_tables, const int32_t* context_lens,
+                              const float* pi_signs, float* workspace, size_t workspace_bytes,
+                              uint32_t num_seqs, uint32_t num_heads, uint32_t num_kv_heads,
+                              uint32_t head_size, uint32_t block_size, uint32_t num_blocks,
+                              uint32_t max_blocks_per_seq, uint32_t num_splits, float scale,
+                              float inv_sqrt_len, uint32_t flags)
+{
+    int rc = decode_checks(q, key_cache, value_cache, scale_cache, block_tables, context_lens,
+                           pi_signs, num_seqs, num_heads, num_kv_heads, head_size, block_size,
+                           num_blocks, max_blocks_per_seq, flags);
+    if (rc != TQ4_OK) return rc;
+    if (num_splits == 0 || num_splits > TQ4_MAX_SPLITS) return TQ4_ERR_SPLITS;
+    if ((uint64_t)num_seqs * num_kv_heads * num_splits > 0x7fffffffull) return TQ4_ERR_RANGE;
+    if (!workspace ||
+        workspace_bytes < tq4::decode_records_bytes(num_seqs, num_heads, head_size, num_splits))
+        return TQ4_ERR_WORKSPACE;
+    tq4::DecodeParams p = make_params(q, key_cache, value_cache, scale_cache, block_tables,
+                                      context_lens, pi_signs, nullptr, num_seqs, num_heads,
+                                      num_kv_heads, head_size, block_size, num_blocks,
+                                      max_blocks_per_seq, num_splits, scale, inv_sqrt_len, 0,
+                                      flags);
+    p.records = workspace;
+    return launched(tq4::launch_decode((hipStream_t)stream, p, 0));
+}
+
+int tq4_splitk_combine(void* stream, const float* workspace, const float* pi_signs,
+                       const float* gate, uint16_t* out, uint32_t num_seqs, uint32_t num_heads,
+                       uint32_t head_size, uint32_t num_splits, float inv_sqrt_len,
+                       uint32_t output_stage)
+{
+    if (!head_size_ok(head_size)) return TQ4_ERR_HEAD_SIZE;
+    if (num_seqs == 0 || num_heads == 0) return TQ4_ERR_GEOMETRY;
+    if (num_splits == 0 || num_splits > TQ4_MAX_SPLITS) return TQ4_ERR_SPLITS;
+    if (!workspace || !out) return TQ4_ERR_NULL_POINTER;
+    if (output_stage > 2 || (output_stage == 2 && !gate)) return TQ4_ERR_OUTPUT_STAGE;
+    if (output_stage >= 1 && !pi_signs) return TQ4_ERR_ROTATION;
+    tq4::DecodeParams p{};
+    p.records = const_cast<float*>(workspace);
+    p.pi_signs = pi_signs;
+    p.gate = gate;
+    p.out = out;
+    p.B = num_seqs;
+    p.Hq = num_heads;
+    p.D = head_size;
+    p.K = num_splits;
+    p.inv_sqrt_len = inv_sqrt_len;
+    p.output_stage = output_stage;
+    return launched(tq4::launch_combine((hipStream_t)stream, p));
+}
+
+}  // extern "C"

@@ -1,0 +1,120 @@
+// tq4_device.hpp -- device helpers shared by the TQ4 kernels (gfx950, wave64).
+//
+// Cache contract and arithmetic restated from the reference (paths relative
+// to the reference checkout):
+//   layout        tests/common/turboquant_scatter_oracle.hpp:31-38,110-132
+//   rotation      tests/common/rotate_butterfly_oracle.hpp:44-48,120-142
+//   quantiser     tests/common/turboquant_oracle.hpp:412-448,
+//                 tests/common/turboquant_scatter_oracle.hpp:185-217
+//   tail masking  kernels/ops/turboquant/turboquant_decode_tail.hpp:56-118
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace tq4 {
+
+constexpr int kStrip = 16;            // tokens per strip (R)
+constexpr float kMasked = -3.0e38f;   // score of a masked lane, also the neutral m
+constexpr int kPolicyPrefill = 0;     // absmax floored at 1.0
+constexpr int kPolicyExact = 1;       // exact absmax, zero row -> scale 1.0
+
+__device__ __forceinline__ float bf16_to_f32(uint32_t raw16)
+{
+    return __uint_as_float(raw16 << 16);
+}
+
+// Round-to-nearest-even float -> bf16 bits; quiet NaN kept quiet.
+__device__ __forceinline__ uint32_t f32_to_bf16(float f)
+{
+    const uint32_t b = __float_as_uint(f);
+    if ((b & 0x7f800000u) == 0x7f800000u && (b & 0x7fffffu)) return ((b >> 16) | 0x40u) & 0xffffu;
+    return ((b + 0x7fffu + ((b >> 16) & 1u)) >> 16) & 0xffffu;
+}
+
+// Partner value `mask` lanes away inside the wave.
+__device__ __forceinline__ float xor_lanes(float v, int mask) { return __shfl_xor(v, mask, 64); }
+
+// One butterfly stage at `stride` over a row spread across lanes, CPL
+// consecutive channels per lane (channel = lane_in_row * CPL + j):
+//   out[i] = in[i ^ s] + ((i & s) ? -in[i] : in[i])
+// In-register below CPL, a lane exchange (xor stride/CPL) at or above it.
+template <int CPL>
+__device__ __forceinline__ void butterfly(float (&v)[CPL], int stride, int lane_in_row)
+{
+    if (stride < CPL) {
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+            if (j & stride) continue;
+            const float a = v[j];
+            const float b = v[j + stride];
+            v[j] = b + a;
+            v[j + stride] = a - b;
+        }
+    } else {
+        const int m = stride / CPL;
+        const bool upper = (lane_in_row & m) != 0;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+            const float p = xor_lanes(v[j], m);
+            v[j] = upper ? p - v[j] : p + v[j];
+        }
+    }
+}
+
+// Ingress rotation y = M x: strides 1..16, the sign diagonal, then 32..D/2.
+template <int D, int CPL>
+__device__ __forceinline__ void rotate_ingress(float (&v)[CPL], const float (&sign)[CPL],
+                                               int lane_in_row)
+{
+#pragma unroll
+    for (int s = 1; s < 32 && s < D; s <<= 1) butterfly<CPL>(v, s, lane_in_row);
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) v[j] *= sign[j];
+#pragma unroll
+    for (int s = 32; s < D; s <<= 1) butterfly<CPL>(v, s, lane_in_row);
+}
+
+// Egress rotation y = M^T x: strides 32..D/2, the sign diagonal, then 1..16.
+template <int D, int CPL>
+__device__ __forceinline__ void rotate_egress(float (&v)[CPL], const float (&sign)[CPL],
+                                              int lane_in_row)
+{
+#pragma unroll
+    for (int s = 32; s < D; s <<= 1) butterfly<CPL>(v, s, lane_in_row);
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) v[j] *= sign[j];
+#pragma unroll
+    for (int s = 1; s < 32 && s < D; s <<= 1) butterfly<CPL>(v, s, lane_in_row);
+}
+
+// Exponent e with 2^e <= a < 2^(e+1), for finite a > 0 (ilogb).
+__device__ __forceinline__ int exponent_of(float a)
+{
+    const uint32_t bits = __float_as_uint(a);
+    const uint32_t field = (bits >> 23) & 0xffu;
+    if (field != 0u) return (int)field - 127;
+    const uint32_t m = bits & 0x7fffffu;
+    return (31 - (int)__clz((int)m)) - 149;
+}
+
+// Live tokens of the strip starting at token_base, 0..16.
+__device__ __forceinline__ uint32_t active_in_strip(uint64_t token_base, uint32_t seq_len)
+{
+    const uint64_t live = seq_len;
+    if (token_base >= live) return 0u;
+    return live - token_base >= (uint64_t)kStrip ? (uint32_t)kStrip : (uint32_t)(live - token_base);
+}
+
+// Partition of `pages` logical pages over `splits`
+// (include/turboquant_splitk_contract.hpp:123-130).
+__device__ __forceinline__ void partition(uint32_t pages, uint32_t splits, uint32_t split,
+                                          uint32_t& begin, uint32_t& count)
+{
+    const uint32_t width = (pages + splits - 1u) / splits;
+    begin = split * width;
+    const uint32_t remaining = begin < pages ? pages - begin : 0u;
+    count = remaining < width ? remaining : width;
+}
+
+}  // namespace tq4

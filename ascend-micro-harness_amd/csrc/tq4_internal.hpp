@@ -1,0 +1,50 @@
+// tq4_internal.hpp -- launchers shared between the kernel translation units
+// and the C ABI layer (tq4_abi.cpp). Not part of the public interface.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace tq4 {
+
+hipError_t launch_strip_writer(hipStream_t stream, int in_bf16, const void* key,
+                               const void* value, int8_t* key_cache, int8_t* value_cache,
+                               float* scale_cache, const int32_t* slots, const float* pi_signs,
+                               const void* tables, uint32_t strips, uint32_t H, uint32_t D,
+                               uint32_t S, uint32_t P, float inv_sqrt_len);
+
+hipError_t launch_scatter_writer(hipStream_t stream, uint32_t grid, const uint16_t* key,
+                                 const uint16_t* value, int8_t* key_cache, int8_t* value_cache,
+                                 float* scale_cache, const int32_t* slots, const float* pi_signs,
+                                 const int32_t* cu_seqlens, int32_t* probe, uint32_t num_requests,
+                                 uint32_t H, uint32_t D, uint32_t S, uint32_t P,
+                                 uint32_t item_begin, uint32_t item_count, float inv_sqrt_len);
+
+// Everything the decode kernels read; filled and validated by the ABI layer.
+struct DecodeParams {
+    const uint16_t* q;
+    const int8_t* key_cache;
+    const int8_t* value_cache;
+    const float* scale_cache;
+    const int32_t* block_tables;
+    const int32_t* context_lens;
+    const float* pi_signs;
+    const float* gate;
+    float* records;       // [B][Hq][K][D+4] partial records (may be null when K == 1 fused)
+    uint32_t* counters;   // [B][Hkv] arrival counters (fused only)
+    uint16_t* out;        // [B][Hq][D] bf16 (fused / combine)
+    uint32_t B, Hq, Hkv, G, D, S, P, max_blocks, K;
+    float scale, inv_sqrt_len;
+    uint32_t output_stage, flags;
+};
+
+// mode 0: partials only; mode 1: fused (partials + last-workgroup combine).
+hipError_t launch_decode(hipStream_t stream, const DecodeParams& p, int mode);
+hipError_t launch_combine(hipStream_t stream, const DecodeParams& p);
+hipError_t launch_fill_zero(hipStream_t stream, void* ptr, size_t bytes);
+
+// Byte offset of the counter region inside a workspace of K splits.
+size_t decode_records_bytes(uint32_t B, uint32_t Hq, uint32_t D, uint32_t K);
+
+}  // namespace tq4

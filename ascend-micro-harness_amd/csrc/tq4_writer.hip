@@ -1,0 +1,366 @@
+// tq4_writer.hip -- reshape_and_cache for the TQ4 cache on gfx950.
+//
+// Two kernels:
+//   strip_writer     aligned 16-token strips (the reference's A8/BF16 prefill
+//                    writers, turboquant_reshape_and_cache_{a8,bf16}.cpp)
+//   scatter_writer   arbitrary slots per (request, kv_head) item, nibble-exact
+//                    read-modify-write of the value strip
+//                    (turboquant_reshape_scatter_aiv.cpp:598-731)
+//
+// Work decomposition (MI355X): one 256-lane workgroup owns one
+// (strip, head, plane) panel of 16 rows x d channels. A row lives on 16
+// lanes with CPL = d/16 consecutive channels per lane, so the 16-point
+// Hadamard stages below CPL are in-register and the rest are lane exchanges
+// inside the row; a strip's 16 rows are the workgroup's 16 row groups.
+// Activations load as one contiguous vector per lane (coalesced: a strip of
+// a head is 16 rows of d elements, row stride H*d). Key rows store as one
+// contiguous word per lane (token-major); the value strip is transposed
+// through LDS and stored as d*8 contiguous bytes (channel-major).
+//
+// Bit-exactness: the rotation is adds and subtracts in the fixed stage order
+// of the reference's Ingress cascade (rotate_butterfly_oracle.hpp:44-48), the
+// scale is a power of two taken from the exponent field, y * 2^(2-e) is exact
+// (ldexp), and the one rounding is v_rndne. This translation unit is built
+// with -ffp-contract=off.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "tq4_device.hpp"
+#include "tq4_internal.hpp"
+
+namespace tq4 {
+namespace {
+
+constexpr int kWriterThreads = 256;  // 16 rows x 16 lanes
+
+// Input element loads: CPL consecutive channels of one row.
+template <int CPL>
+__device__ __forceinline__ void load_row(const int8_t* src, float (&x)[CPL])
+{
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) x[j] = (float)src[j];
+}
+
+template <int CPL>
+__device__ __forceinline__ void load_row(const uint16_t* src, float (&x)[CPL])
+{
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) x[j] = bf16_to_f32(src[j]);
+}
+
+// Signs for the lane's CPL channels: pi_signs when given, else the first
+// column of the reference's rotation tables (T[0][g][c0][0] = sign[g*32+c0]).
+template <int CPL>
+__device__ __forceinline__ void load_signs(const float* pi_signs, const void* tables,
+                                           int tables_bf16, int c0, float (&sign)[CPL])
+{
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+        const int c = c0 + j;
+        float s;
+        if (pi_signs != nullptr) {
+            s = pi_signs[c];
+        } else if (tables_bf16) {
+            const uint16_t raw = ((const uint16_t*)tables)[(size_t)c * 32];
+            s = (raw & 0x8000u) ? -1.0f : 1.0f;
+        } else {
+            const int8_t raw = ((const int8_t*)tables)[(size_t)c * 32];
+            s = raw < 0 ? -1.0f : 1.0f;
+        }
+        sign[j] = s;
+    }
+}
+
+// Rotate one row, find its absmax over the 16 lanes of the row, quantise.
+// q receives the INT4 codes, the return value is the stored scale.
+template <int D, int CPL>
+__device__ __forceinline__ float rotate_quantise(float (&v)[CPL], const float (&sign)[CPL],
+                                                 int lane_in_row, float inv_sqrt_len, int policy,
+                                                 int (&q)[CPL])
+{
+    rotate_ingress<D, CPL>(v, sign, lane_in_row);
+    float a = 0.0f;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) a = fmaxf(a, fabsf(v[j]));
+#pragma unroll
+    for (int m = 1; m < 16; m <<= 1) a = fmaxf(a, xor_lanes(a, m));
+    if (policy == kPolicyPrefill) {
+        a = fmaxf(a, 1.0f);
+    } else if (a == 0.0f) {
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) q[j] = 0;
+        return 1.0f;
+    }
+    const int e = exponent_of(a);
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+        float r = rintf(ldexpf(v[j], 2 - e));
+        r = fminf(r, 7.0f);
+        q[j] = (int)r;
+    }
+    return ldexpf(1.0f, e - 2) * inv_sqrt_len;
+}
+
+// Pack CPL codes (low nibble first) into CPL/2 bytes and store them.
+template <int CPL>
+__device__ __forceinline__ void store_key_codes(int8_t* dst, const int (&q)[CPL])
+{
+    if constexpr (CPL == 16) {
+        uint32_t w[2] = {0u, 0u};
+#pragma unroll
+        for (int j = 0; j < 16; ++j) w[j / 8] |= ((uint32_t)q[j] & 0xfu) << (4 * (j % 8));
+        *(uint2*)dst = make_uint2(w[0], w[1]);
+    } else if constexpr (CPL == 8) {
+        uint32_t w = 0u;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) w |= ((uint32_t)q[j] & 0xfu) << (4 * j);
+        *(uint32_t*)dst = w;
+    } else {
+        static_assert(CPL == 4, "head_size 64, 128 or 256");
+        uint32_t w = 0u;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) w |= ((uint32_t)q[j] & 0xfu) << (4 * j);
+        *(uint16_t*)dst = (uint16_t)w;
+    }
+}
+
+// Pack 8 LDS nibble bytes (one per token, value in the low nibble) into one
+// word: byte k = t[2k] | t[2k+1] << 4.
+__device__ __forceinline__ uint32_t pack8(uint32_t lo4, uint32_t hi4)
+{
+    const uint32_t a = lo4 | (lo4 >> 4);  // bytes 0 and 2 hold the two pairs
+    const uint32_t b = hi4 | (hi4 >> 4);
+    return (a & 0xffu) | ((a >> 8) & 0xff00u) | ((b & 0xffu) << 16) | ((b << 8) & 0xff000000u);
+}
+
+// ------------------------------------------------------------ strip writer
+// grid.x = strips * H * 2; block = (strip, head, plane), plane fastest.
+template <int D, typename In>
+__global__ __launch_bounds__(kWriterThreads) void strip_writer(
+    const In* __restrict__ key, const In* __restrict__ value, int8_t* __restrict__ key_cache,
+    int8_t* __restrict__ value_cache, float* __restrict__ scale_cache,
+    const int32_t* __restrict__ slots, const float* __restrict__ pi_signs,
+    const void* __restrict__ tables, int tables_bf16, uint32_t H, uint32_t S, uint32_t P,
+    float inv_sqrt_len)
+{
+    constexpr int CPL = D / 16;
+    __shared__ uint32_t lds_codes[D * kStrip / 4];  // [channel][token] bytes
+
+    const uint32_t plane = blockIdx.x & 1u;
+    const uint32_t head = (blockIdx.x >> 1) % H;
+    const uint32_t strip = (blockIdx.x >> 1) / H;
+    const int tid = threadIdx.x;
+    const int row = tid >> 4;        // token within the strip
+    const int lane_in_row = tid & 15;
+
+    // Slot contract for this strip: consecutive, strip-aligned, in range.
+    const int32_t slot0 = slots[(size_t)strip * kStrip];
+    const int32_t mine = slots[(size_t)strip * kStrip + row];
+    const bool ok = slot0 >= 0 && (slot0 % kStrip) == 0 && mine == slot0 + row &&
+                    (uint32_t)slot0 / S < P;
+    if (!__syncthreads_and(ok)) return;
+    const uint32_t page = (uint32_t)slot0 / S;
+    const uint32_t tip = (uint32_t)slot0 % S + (uint32_t)row;
+
+    const In* src = (plane == 0 ? key : value) +
+                    ((size_t)((size_t)strip * kStrip + row) * H + head) * D + lane_in_row * CPL;
+    float v[CPL], sign[CPL];
+    load_row<CPL>(src, v);
+    load_signs<CPL>(pi_signs, tables, tables_bf16, lane_in_row * CPL, sign);
+    int q[CPL];
+    const float scale =
+        rotate_quantise<D, CPL>(v, sign, lane_in_row, inv_sqrt_len, kPolicyPrefill, q);
+
+    if (lane_in_row == 0)
+        scale_cache[(((size_t)plane * P + page) * H + head) * S + tip] = scale;
+
+    const size_t head_base = ((size_t)page * H + head) * S;  // in tokens
+    if (plane == 0) {
+        store_key_codes<CPL>(key_cache + (head_base + tip) * (D / 2) + lane_in_row * (CPL / 2), q);
+        return;
+    }
+    // Value plane: transpose through LDS, then one contiguous strip store.
+    uint8_t* lds = (uint8_t*)lds_codes;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) lds[(lane_in_row * CPL + j) * kStrip + row] = (uint8_t)(q[j] & 0xf);
+    __syncthreads();
+    uint32_t* strip_words = (uint32_t*)(value_cache + (head_base + (tip & ~(uint32_t)15)) * (D / 2));
+    for (int w = tid; w < D * 2; w += kWriterThreads) {
+        const int channel = w >> 1, half = w & 1;
+        const uint32_t lo4 = lds_codes[(channel * kStrip + half * 8) / 4];
+        const uint32_t hi4 = lds_codes[(channel * kStrip + half * 8) / 4 + 1];
+        strip_words[w] = pack8(lo4, hi4);
+    }
+}
+
+// ----------------------------------------------------------- scatter writer
+// One workgroup walks items item_begin + blockIdx.x, += gridDim.x. Inside an
+// item the tokens are grouped into runs of consecutive slots inside one strip
+// (at most 16), exactly the reference's transaction unit.
+template <int D>
+__global__ __launch_bounds__(kWriterThreads) void scatter_writer(
+    const uint16_t* __restrict__ key, const uint16_t* __restrict__ value,
+    int8_t* __restrict__ key_cache, int8_t* __restrict__ value_cache,
+    float* __restrict__ scale_cache, const int32_t* __restrict__ slots,
+    const float* __restrict__ pi_signs, const int32_t* __restrict__ cu_seqlens,
+    int32_t* __restrict__ probe, uint32_t num_requests, uint32_t H, uint32_t S, uint32_t P,
+    uint32_t item_begin, uint32_t item_count, float inv_sqrt_len)
+{
+    constexpr int CPL = D / 16;
+    __shared__ uint32_t lds_codes[D * kStrip / 4];
+    const int tid = threadIdx.x;
+    const int row = tid >> 4;
+    const int lane_in_row = tid & 15;
+
+    if (probe != nullptr && blockIdx.x == 0 && tid < 32) {
+        const int32_t fields[4] = {0, (int32_t)gridDim.x, 1, (int32_t)item_count};
+        probe[tid] = fields[tid >> 3];
+    }
+
+    float sign[CPL];
+    load_signs<CPL>(pi_signs, nullptr, 0, lane_in_row * CPL, sign);
+    const uint64_t item_end = (uint64_t)item_begin + item_count;
+
+    for (uint64_t item = (uint64_t)item_begin + blockIdx.x; item < item_end; item += gridDim.x) {
+        const uint32_t request = (uint32_t)(item / H);
+        const uint32_t head = (uint32_t)(item % H);
+        if (request >= num_requests) continue;
+        uint32_t token = cu_seqlens ? (uint32_t)cu_seqlens[request] : request;
+        const uint32_t token_end = cu_seqlens ? (uint32_t)cu_seqlens[request + 1] : request + 1;
+
+        while (token < token_end) {
+            // Run discovery, computed identically by every lane (uniform).
+            const int32_t slot0 = slots[token];
+            if (slot0 < 0 || (uint32_t)slot0 / S >= P) {
+                ++token;
+                continue;
+            }
+            const uint32_t page = (uint32_t)slot0 / S;
+            const uint32_t tip0 = (uint32_t)slot0 % S;
+            const uint32_t strip_in_page = tip0 / kStrip;
+            uint32_t run = 1;
+            while (token + run < token_end && run < (uint32_t)kStrip) {
+                const int32_t next = slots[token + run];
+                if (next != slot0 + (int32_t)run) break;
+                if ((uint32_t)next / S != page || ((uint32_t)next % S) / kStrip != strip_in_page) break;
+                ++run;
+            }
+            const bool live = (uint32_t)row < run;
+            const uint32_t tok = token + (live ? (uint32_t)row : 0u);
+            const size_t head_base = ((size_t)page * H + head) * S;
+
+            for (uint32_t plane = 0; plane < 2; ++plane) {
+                const uint16_t* src = (plane == 0 ? key : value) +
+                                      ((size_t)tok * H + head) * D + lane_in_row * CPL;
+                float v[CPL];
+                load_row<CPL>(src, v);
+                int q[CPL];
+                const float scale =
+                    rotate_quantise<D, CPL>(v, sign, lane_in_row, inv_sqrt_len, kPolicyExact, q);
+                const uint32_t tip = tip0 + (uint32_t)row;
+                if (live && lane_in_row == 0)
+                    scale_cache[(((size_t)plane * P + page) * H + head) * S + tip] = scale;
+                if (plane == 0) {
+                    if (live)
+                        store_key_codes<CPL>(
+                            key_cache + (head_base + tip) * (D / 2) + lane_in_row * (CPL / 2), q);
+                    continue;
+                }
+                // Value plane: codes to LDS at their strip column, then merge
+                // only the owned nibbles into the words they live in.
+                uint8_t* lds = (uint8_t*)lds_codes;
+                const uint32_t col = (tip0 % kStrip) + (uint32_t)row;
+                if (live) {
+#pragma unroll
+                    for (int j = 0; j < CPL; ++j)
+                        lds[(lane_in_row * CPL + j) * kStrip + col] = (uint8_t)(q[j] & 0xf);
+                }
+                __syncthreads();
+                const uint32_t first = tip0 % kStrip, last = first + run;  // owned columns
+                uint32_t* strip_words =
+                    (uint32_t*)(value_cache + (head_base + strip_in_page * kStrip) * (D / 2));
+                for (int w = tid; w < D * 2; w += kWriterThreads) {
+                    const int channel = w >> 1, half = w & 1;
+                    const uint32_t t0 = (uint32_t)half * 8u;
+                    const uint32_t lo = first > t0 ? first : t0;
+                    const uint32_t hi = last < t0 + 8u ? last : t0 + 8u;
+                    if (lo >= hi) continue;
+                    uint32_t mask = 0u, bits = 0u;
+                    for (uint32_t t = lo; t < hi; ++t) {
+                        const uint32_t sh = 4u * (t - t0);
+                        mask |= 0xfu << sh;
+                        bits |= (uint32_t)lds[channel * kStrip + t] << sh;
+                    }
+                    strip_words[w] = (strip_words[w] & ~mask) | bits;
+                }
+                __syncthreads();
+            }
+            token += run;
+        }
+    }
+}
+
+}  // namespace
+
+// ------------------------------------------------------------- launchers
+template <int D, typename In>
+static hipError_t launch_strip_writer_t(hipStream_t stream, const In* key, const In* value,
+                                        int8_t* key_cache, int8_t* value_cache, float* scale_cache,
+                                        const int32_t* slots, const float* pi_signs,
+                                        const void* tables, int tables_bf16, uint32_t strips,
+                                        uint32_t H, uint32_t S, uint32_t P, float inv_sqrt_len)
+{
+    const uint64_t blocks = (uint64_t)strips * H * 2u;
+    hipLaunchKernelGGL((strip_writer<D, In>), dim3((uint32_t)blocks), dim3(kWriterThreads), 0,
+                       stream, key, value, key_cache, value_cache, scale_cache, slots, pi_signs,
+                       tables, tables_bf16, H, S, P, inv_sqrt_len);
+    return hipGetLastError();
+}
+
+hipError_t launch_strip_writer(hipStream_t stream, int in_bf16, const void* key,
+                               const void* value, int8_t* key_cache, int8_t* value_cache,
+                               float* scale_cache, const int32_t* slots, const float* pi_signs,
+                               const void* tables, uint32_t strips, uint32_t H, uint32_t D,
+                               uint32_t S, uint32_t P, float inv_sqrt_len)
+{
+#define TQ4_STRIP_CASE(DD)                                                                        \
+    if (D == DD) {                                                                                \
+        if (in_bf16)                                                                              \
+            return launch_strip_writer_t<DD, uint16_t>(                                           \
+                stream, (const uint16_t*)key, (const uint16_t*)value, key_cache, value_cache,     \
+                scale_cache, slots, pi_signs, tables, 1, strips, H, S, P, inv_sqrt_len);          \
+        return launch_strip_writer_t<DD, int8_t>(stream, (const int8_t*)key, (const int8_t*)value, \
+                                                 key_cache, value_cache, scale_cache, slots,      \
+                                                 pi_signs, tables, 0, strips, H, S, P,            \
+                                                 inv_sqrt_len);                                   \
+    }
+    TQ4_STRIP_CASE(64)
+    TQ4_STRIP_CASE(128)
+    TQ4_STRIP_CASE(256)
+#undef TQ4_STRIP_CASE
+    return hipErrorInvalidValue;
+}
+
+hipError_t launch_scatter_writer(hipStream_t stream, uint32_t grid, const uint16_t* key,
+                                 const uint16_t* value, int8_t* key_cache, int8_t* value_cache,
+                                 float* scale_cache, const int32_t* slots, const float* pi_signs,
+                                 const int32_t* cu_seqlens, int32_t* probe, uint32_t num_requests,
+                                 uint32_t H, uint32_t D, uint32_t S, uint32_t P,
+                                 uint32_t item_begin, uint32_t item_count, float inv_sqrt_len)
+{
+#define TQ4_SCATTER_CASE(DD)                                                                      \
+    if (D == DD) {                                                                                \
+        hipLaunchKernelGGL((scatter_writer<DD>), dim3(grid), dim3(kWriterThreads), 0, stream,    \
+                           key, value, key_cache, value_cache, scale_cache, slots, pi_signs,      \
+                           cu_seqlens, probe, num_requests, H, S, P, item_begin, item_count,      \
+                           inv_sqrt_len);                                                         \
+        return hipGetLastError();                                                                 \
+    }
+    TQ4_SCATTER_CASE(64)
+    TQ4_SCATTER_CASE(128)
+    TQ4_SCATTER_CASE(256)
+#undef TQ4_SCATTER_CASE
+    return hipErrorInvalidValue;
+}
+
+}  // namespace tq4

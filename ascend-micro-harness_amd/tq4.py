@@ -1,0 +1,276 @@
+"""Host-side mirror of the reference's TQ4 operator interface over libtq4.so.
+
+The functions keep the reference launchers' names, argument meaning and error
+behaviour (a refused geometry raises ``ValueError``, the analogue of the
+reference's ``std::invalid_argument``), and call straight through the C ABI in
+include/tq4.h. PyTorch supplies device memory and the current HIP stream;
+every byte of compute runs in the HIP kernels. There is no CPU fallback: if
+libtq4.so is missing the first call raises.
+
+Reference launchers mirrored (paths relative to the reference checkout):
+  reshape_and_cache_a8    kernels/ops/turboquant/turboquant_reshape_and_cache_a8.cpp:1578-1627
+  reshape_and_cache_bf16  kernels/ops/turboquant/turboquant_reshape_and_cache_bf16.cpp:1993-2059
+  reshape_scatter         kernels/ops/turboquant/turboquant_reshape_scatter_aiv.cpp:760-773
+  paged_decode_partials   kernels/ops/turboquant/turboquant_paged_decode_attention.cpp:1727-1766
+  paged_decode            kernels/ops/turboquant/baseline/turboquant_paged_attention.cpp:773-793
+  splitk_combine          tests/common/l2_atomic_oracle.hpp:156-176 (host merge in the reference)
+"""
+from __future__ import annotations
+
+import ctypes as C
+import math
+import os
+
+import torch  # noqa: F401  (loads torch's HIP runtime first; libtq4 binds to it)
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libtq4.so")
+
+TQ4_DECODE_QUERY_ROTATED = 1
+TQ4_MAX_SPLITS = 256
+
+_P = C.c_void_p
+_U32 = C.c_uint32
+_F32 = C.c_float
+_I32 = C.c_int
+_SZ = C.c_size_t
+
+_lib = None
+
+
+class TQ4Error(ValueError):
+    """A refused launch: the C ABI returned a negative tq4_status."""
+
+    def __init__(self, status, what):
+        self.status = status
+        super().__init__(f"{what}: {status_string(status)} (status {status})")
+
+
+def lib():
+    """The loaded libtq4.so; raises if it was never built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(
+            f"libtq4.so not found at {LIB_PATH}: run __graft_entry__.build() "
+            "(make -C ascend-micro-harness_amd/csrc)")
+    L = C.CDLL(LIB_PATH)
+    L.tq4_status_string.restype = C.c_char_p
+    L.tq4_status_string.argtypes = [_I32]
+    L.tq4_version.restype = _U32
+    L.tq4_reshape_and_cache_a8.restype = _I32
+    L.tq4_reshape_and_cache_a8.argtypes = [_P] * 10 + [_U32] * 6 + [_F32, C.c_bool]
+    L.tq4_reshape_and_cache_bf16.restype = _I32
+    L.tq4_reshape_and_cache_bf16.argtypes = [_P] * 10 + [_U32] * 6 + [_F32, C.c_bool]
+    L.tq4_reshape_scatter.restype = _I32
+    L.tq4_reshape_scatter.argtypes = [_P, _U32] + [_P] * 9 + [_U32] * 7 + [_F32]
+    L.tq4_decode_workspace_bytes.restype = _SZ
+    L.tq4_decode_workspace_bytes.argtypes = [_U32] * 5
+    L.tq4_decode_auto_splits.restype = _U32
+    L.tq4_decode_auto_splits.argtypes = [_U32] * 4
+    L.tq4_decode_workspace_init.restype = _I32
+    L.tq4_decode_workspace_init.argtypes = [_P, _P, _SZ]
+    L.tq4_paged_decode.restype = _I32
+    L.tq4_paged_decode.argtypes = [_P] * 10 + [_SZ, _P] + [_U32] * 8 + [_F32, _F32, _U32, _U32]
+    L.tq4_paged_decode_partials.restype = _I32
+    L.tq4_paged_decode_partials.argtypes = [_P] * 9 + [_SZ] + [_U32] * 8 + [_F32, _F32, _U32]
+    L.tq4_splitk_combine.restype = _I32
+    L.tq4_splitk_combine.argtypes = [_P] * 5 + [_U32] * 4 + [_F32, _U32]
+    _lib = L
+    return L
+
+
+def status_string(status):
+    return lib().tq4_status_string(int(status)).decode()
+
+
+def _ptr(t):
+    if t is None:
+        return None
+    if not t.is_contiguous():
+        raise ValueError("tensors handed to libtq4 must be contiguous")
+    return _P(t.data_ptr())
+
+
+def _stream(stream=None):
+    s = torch.cuda.current_stream() if stream is None else stream
+    return _P(s.cuda_stream)
+
+
+def _check(status, what):
+    if status != 0:
+        raise TQ4Error(status, what)
+
+
+def _dev(t, name):
+    if t is not None and not t.is_cuda:
+        raise ValueError(f"{name} must be a device tensor")
+
+
+# --------------------------------------------------------------- writers
+def reshape_and_cache_a8(key, value, key_cache, value_cache, scale_cache, slot_mapping,
+                         pi_signs=None, tables=None, num_blocks=None, block_size=16,
+                         tokens_per_core=16, inv_sqrt_len=None, reuse_mode4_flags=True,
+                         stream=None):
+    """INT8 K/V [num_tokens][num_kv_heads][head_size] -> TQ4 cache, whole strips."""
+    return _reshape_and_cache(lib().tq4_reshape_and_cache_a8, "reshape_and_cache_a8", torch.int8,
+                              key, value, key_cache, value_cache, scale_cache, slot_mapping,
+                              pi_signs, tables, num_blocks, block_size, tokens_per_core,
+                              inv_sqrt_len, reuse_mode4_flags, stream)
+
+
+def reshape_and_cache_bf16(key, value, key_cache, value_cache, scale_cache, slot_mapping,
+                           pi_signs=None, tables=None, num_blocks=None, block_size=16,
+                           tokens_per_core=16, inv_sqrt_len=None, reuse_mode4_flags=True,
+                           stream=None):
+    """BF16 K/V [num_tokens][num_kv_heads][head_size] -> TQ4 cache, whole strips."""
+    return _reshape_and_cache(lib().tq4_reshape_and_cache_bf16, "reshape_and_cache_bf16",
+                              torch.bfloat16, key, value, key_cache, value_cache, scale_cache,
+                              slot_mapping, pi_signs, tables, num_blocks, block_size,
+                              tokens_per_core, inv_sqrt_len, reuse_mode4_flags, stream)
+
+
+def _reshape_and_cache(fn, what, dtype, key, value, key_cache, value_cache, scale_cache,
+                       slot_mapping, pi_signs, tables, num_blocks, block_size, tokens_per_core,
+                       inv_sqrt_len, reuse_mode4_flags, stream):
+    if key.dtype != dtype or value.dtype != dtype:
+        raise ValueError(f"{what}: key/value must be {dtype}")
+    for name, t in (("key", key), ("value", value), ("key_cache", key_cache),
+                    ("value_cache", value_cache), ("scale_cache", scale_cache),
+                    ("slot_mapping", slot_mapping), ("pi_signs", pi_signs), ("tables", tables)):
+        _dev(t, name)
+    num_tokens, num_kv_heads, head_size = key.shape
+    if num_blocks is None:
+        num_blocks = key_cache.numel() * 2 // (num_kv_heads * block_size * head_size)
+    if inv_sqrt_len is None:
+        inv_sqrt_len = 1.0 / math.sqrt(head_size)
+    st = fn(_stream(stream), _ptr(key), _ptr(value), _ptr(key_cache), _ptr(value_cache),
+            _ptr(scale_cache), _ptr(slot_mapping), _ptr(pi_signs), _ptr(tables), num_tokens,
+            num_kv_heads, head_size, block_size, num_blocks, tokens_per_core, inv_sqrt_len,
+            bool(reuse_mode4_flags))
+    _check(st, what)
+
+
+def reshape_scatter(key, value, key_cache, value_cache, scale_cache, slot_mapping, pi_signs,
+                    cu_seqlens=None, launch_probe=None, num_requests=None, num_blocks=None,
+                    block_size=16, item_begin=0, item_count=None, block_dim=0,
+                    inv_sqrt_len=None, stream=None):
+    """BF16 tokens at arbitrary slots; items are (request, kv_head)."""
+    for name, t in (("key", key), ("value", value), ("key_cache", key_cache),
+                    ("value_cache", value_cache), ("scale_cache", scale_cache),
+                    ("slot_mapping", slot_mapping), ("pi_signs", pi_signs),
+                    ("cu_seqlens", cu_seqlens), ("launch_probe", launch_probe)):
+        _dev(t, name)
+    num_tokens, num_kv_heads, head_size = key.shape
+    if num_requests is None:
+        num_requests = (cu_seqlens.numel() - 1) if cu_seqlens is not None else num_tokens
+    if num_blocks is None:
+        num_blocks = key_cache.numel() * 2 // (num_kv_heads * block_size * head_size)
+    if item_count is None:
+        item_count = num_requests * num_kv_heads
+    if inv_sqrt_len is None:
+        inv_sqrt_len = 1.0 / math.sqrt(head_size)
+    st = lib().tq4_reshape_scatter(
+        _stream(stream), block_dim, _ptr(key), _ptr(value), _ptr(key_cache), _ptr(value_cache),
+        _ptr(scale_cache), _ptr(slot_mapping), _ptr(pi_signs), _ptr(cu_seqlens),
+        _ptr(launch_probe), num_requests, num_kv_heads, head_size, block_size, num_blocks,
+        item_begin, item_count, inv_sqrt_len)
+    _check(st, "reshape_scatter")
+
+
+# ---------------------------------------------------------------- decode
+def decode_workspace_bytes(num_seqs, num_heads, num_kv_heads, head_size, num_splits):
+    return int(lib().tq4_decode_workspace_bytes(num_seqs, num_heads, num_kv_heads, head_size,
+                                                num_splits))
+
+
+def auto_splits(num_seqs, num_kv_heads, max_blocks_per_seq, block_size):
+    return int(lib().tq4_decode_auto_splits(num_seqs, num_kv_heads, max_blocks_per_seq,
+                                            block_size))
+
+
+def decode_workspace(num_seqs, num_heads, num_kv_heads, head_size, num_splits=0, device="cuda",
+                     stream=None):
+    """A zero-initialised workspace (counters at zero) for tq4_paged_decode."""
+    nbytes = decode_workspace_bytes(num_seqs, num_heads, num_kv_heads, head_size, num_splits)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=device)
+    _check(lib().tq4_decode_workspace_init(_stream(stream), _ptr(ws), nbytes),
+           "decode_workspace_init")
+    return ws
+
+
+def paged_decode(q, key_cache, value_cache, scale_cache, block_tables, context_lens, pi_signs,
+                 num_kv_heads, block_size, num_blocks, out=None, workspace=None, gate=None,
+                 num_splits=0, scale=None, inv_sqrt_len=None, output_stage=1, flags=0,
+                 stream=None):
+    """Fused split-K decode: q [B][Hq][d] bf16 -> out [B][Hq][d] bf16."""
+    for name, t in (("q", q), ("key_cache", key_cache), ("value_cache", value_cache),
+                    ("scale_cache", scale_cache), ("block_tables", block_tables),
+                    ("context_lens", context_lens), ("pi_signs", pi_signs), ("gate", gate),
+                    ("workspace", workspace), ("out", out)):
+        _dev(t, name)
+    B, Hq, d = q.shape
+    if out is None:
+        out = torch.empty_like(q)
+    if scale is None:
+        scale = 1.0 / math.sqrt(d)
+    if inv_sqrt_len is None:
+        inv_sqrt_len = 1.0 / math.sqrt(d)
+    max_blocks = block_tables.shape[1]
+    if num_splits == 0:
+        num_splits = auto_splits(B, num_kv_heads, max_blocks, block_size)
+    if workspace is None and num_splits > 1:
+        workspace = decode_workspace(B, Hq, num_kv_heads, d, num_splits, q.device, stream)
+    ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    st = lib().tq4_paged_decode(
+        _stream(stream), _ptr(q), _ptr(key_cache), _ptr(value_cache), _ptr(scale_cache),
+        _ptr(block_tables), _ptr(context_lens), _ptr(pi_signs), _ptr(gate), _ptr(workspace),
+        ws_bytes, _ptr(out), B, Hq, num_kv_heads, d, block_size, num_blocks, max_blocks,
+        num_splits, scale, inv_sqrt_len, output_stage, flags)
+    _check(st, "paged_decode")
+    return out
+
+
+def paged_decode_partials(q, key_cache, value_cache, scale_cache, block_tables, context_lens,
+                          pi_signs, num_kv_heads, block_size, num_blocks, num_splits,
+                          workspace=None, scale=None, inv_sqrt_len=None, flags=0, stream=None):
+    """Partial records [B][Hq][K][d+4] = (m, l, 0, 0, acc[d]) per split."""
+    B, Hq, d = q.shape
+    if scale is None:
+        scale = 1.0 / math.sqrt(d)
+    if inv_sqrt_len is None:
+        inv_sqrt_len = 1.0 / math.sqrt(d)
+    if workspace is None:
+        workspace = torch.empty((B, Hq, num_splits, d + 4), dtype=torch.float32, device=q.device)
+    ws_bytes = workspace.numel() * workspace.element_size()
+    st = lib().tq4_paged_decode_partials(
+        _stream(stream), _ptr(q), _ptr(key_cache), _ptr(value_cache), _ptr(scale_cache),
+        _ptr(block_tables), _ptr(context_lens), _ptr(pi_signs), _ptr(workspace), ws_bytes, B,
+        Hq, num_kv_heads, d, block_size, num_blocks, block_tables.shape[1], num_splits, scale,
+        inv_sqrt_len, flags)
+    _check(st, "paged_decode_partials")
+    return workspace
+
+
+def splitk_combine(workspace, pi_signs, num_seqs, num_heads, head_size, num_splits, out=None,
+                   gate=None, inv_sqrt_len=None, output_stage=1, stream=None):
+    """LSE combine + egress of partial records into BF16 [B][Hq][d]."""
+    if out is None:
+        out = torch.empty((num_seqs, num_heads, head_size), dtype=torch.bfloat16,
+                          device=workspace.device)
+    if inv_sqrt_len is None:
+        inv_sqrt_len = 1.0 / math.sqrt(head_size)
+    st = lib().tq4_splitk_combine(_stream(stream), _ptr(workspace), _ptr(pi_signs), _ptr(gate),
+                                  _ptr(out), num_seqs, num_heads, head_size, num_splits,
+                                  inv_sqrt_len, output_stage)
+    _check(st, "splitk_combine")
+    return out
+
+
+__all__ = [
+    "TQ4Error", "lib", "status_string", "reshape_and_cache_a8", "reshape_and_cache_bf16",
+    "reshape_scatter", "decode_workspace_bytes", "auto_splits", "decode_workspace",
+    "paged_decode", "paged_decode_partials", "splitk_combine", "TQ4_DECODE_QUERY_ROTATED",
+    "TQ4_MAX_SPLITS",
+]

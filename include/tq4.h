@@ -1,0 +1,199 @@
+/*
+ * tq4.h -- C ABI of the MI355X-native TurboQuant TQ4 quantised-KV hot path.
+ *
+ * One shared library, libtq4.so (ascend-micro-harness_amd/), exports every
+ * symbol declared here. The entry points take plain device pointers, sizes
+ * and a hipStream_t passed as void*; they allocate nothing (the caller owns
+ * every buffer, including the decode workspace), never synchronise, and
+ * never throw: each returns a tq4_status (0 = launched, negative = refused,
+ * nothing launched). Work is stream-ordered and asynchronous.
+ *
+ * The cache contract (identical to the reference's, so caches are
+ * interchangeable; d = head_size, H = num_kv_heads, S = block_size,
+ * P = num_blocks, a strip is 16 tokens):
+ *   key   nibble = ((page*H + head)*S + token)*d + channel            token-major
+ *   value nibble = ((page*H + head)*S)*d + (token/16)*16*d
+ *                  + channel*16 + token%16                             strip-blocked
+ *   scale float  = ((plane*P + page)*H + head)*S + token    plane 0 key, 1 value
+ *   nibbles: two per byte, low nibble first, signed INT4 in [-8, 7];
+ *   stored value = nibble * scale, scale = 2^(e-2) * inv_sqrt_len.
+ *   (reference: tests/common/turboquant_scatter_oracle.hpp:31-38,110-132,
+ *    tests/common/turboquant_oracle.hpp:31-38)
+ *
+ * Supported shapes: head_size in {64, 128, 256}; block_size a multiple of
+ * 16; decode GQA group num_heads / num_kv_heads in [1, 16].
+ */
+#ifndef TQ4_H
+#define TQ4_H
+
+#include <stdbool.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+    TQ4_OK = 0,
+    TQ4_ERR_NULL_POINTER = -1,  /* a required pointer is NULL */
+    TQ4_ERR_HEAD_SIZE = -2,     /* head_size not in {64, 128, 256} */
+    TQ4_ERR_GEOMETRY = -3,      /* zero heads/blocks, block_size % 16, GQA group */
+    TQ4_ERR_PARTIAL_STRIP = -4, /* num_tokens not a whole number of strips */
+    TQ4_ERR_SPLITS = -5,        /* num_splits out of range */
+    TQ4_ERR_WORKSPACE = -6,     /* workspace NULL or smaller than required */
+    TQ4_ERR_OUTPUT_STAGE = -7,  /* output_stage > 2, or stage 2 without gate */
+    TQ4_ERR_ROTATION = -8,      /* neither pi_signs nor tables given */
+    TQ4_ERR_LAUNCH = -9,        /* the HIP runtime refused the launch */
+    TQ4_ERR_RANGE = -10         /* a size exceeds what the kernels index */
+} tq4_status;
+
+/* Human-readable name of a tq4_status. */
+const char* tq4_status_string(int status);
+
+/* ABI version: (major << 16) | minor. */
+uint32_t tq4_version(void);
+
+/* ----------------------------------------------------------------------
+ * reshape_and_cache: rotate (randomised Hadamard M = (H_{d/32} (x) I32) .
+ * diag(pi_signs) . (I_{d/32} (x) H32), butterflies in registers), quantise
+ * to power-of-two-scaled INT4, pack and store whole 16-token strips.
+ *
+ * Slot contract per strip s (tokens 16s..16s+15): slot_mapping[16s+i] ==
+ * slot_mapping[16s] + i, slot_mapping[16s] % 16 == 0 and page < num_blocks.
+ * A strip that violates it writes nothing (the reference oracle's
+ * bad-slot behaviour, tests/common/turboquant_oracle.hpp:274-287,489-494).
+ * Quantiser: absmax floored at 1.0 (turboquant_oracle.hpp:412-448).
+ * num_tokens must be a whole number of tokens_per_core strips
+ * (TQ4_ERR_PARTIAL_STRIP otherwise), tokens_per_core a multiple of 16; it is
+ * accepted for signature compatibility, the grid is chosen here.
+ * Rotation signs: pi_signs (float[head_size] of +-1) when non-NULL, else the
+ * first column of `tables` (the reference's 2*(d/32) row-major 32x32 INT8
+ * blocks, T[0][g][c0][0] = sign[g*32+c0]). reuse_mode4_flags selects an
+ * Ascend cross-core flag policy and has no counterpart here (ignored).
+ *
+ * Replaces launch_turboquant_reshape_and_cache_a8
+ * (kernels/ops/turboquant/turboquant_reshape_and_cache_a8.cpp:1578-1627).
+ */
+int tq4_reshape_and_cache_a8(void* stream, const int8_t* key, const int8_t* value,
+                             int8_t* key_cache, int8_t* value_cache, float* scale_cache,
+                             const int32_t* slot_mapping, const float* pi_signs,
+                             const int32_t* tables, uint32_t num_tokens, uint32_t num_kv_heads,
+                             uint32_t head_size, uint32_t block_size, uint32_t num_blocks,
+                             uint32_t tokens_per_core, float inv_sqrt_len,
+                             bool reuse_mode4_flags);
+
+/* Same contract with BF16 activations (uint16 bit patterns); `tables`, when
+ * used, holds BF16 +-1 entries.
+ * Replaces launch_turboquant_reshape_and_cache_bf16
+ * (kernels/ops/turboquant/turboquant_reshape_and_cache_bf16.cpp:1993-2059). */
+int tq4_reshape_and_cache_bf16(void* stream, const uint16_t* key, const uint16_t* value,
+                               int8_t* key_cache, int8_t* value_cache, float* scale_cache,
+                               const int32_t* slot_mapping, const float* pi_signs,
+                               const int32_t* tables, uint32_t num_tokens,
+                               uint32_t num_kv_heads, uint32_t head_size, uint32_t block_size,
+                               uint32_t num_blocks, uint32_t tokens_per_core,
+                               float inv_sqrt_len, bool reuse_mode4_flags);
+
+/* ----------------------------------------------------------------------
+ * reshape_scatter: BF16 tokens at arbitrary slots (decode-step writes,
+ * prefill tails). Work item = (request, kv_head) for item in
+ * [item_begin, item_begin + item_count), item = request * num_kv_heads + head.
+ * Request r owns tokens [cu_seqlens[r], cu_seqlens[r+1]) (cu_seqlens NULL =
+ * one token per request); slot < 0 marks a padded token and is skipped.
+ * The value strip is read-modify-written nibble-exactly: every nibble the
+ * launch does not own is preserved. Quantiser: exact absmax, absmax == 0
+ * gives codes 0 and scale 1.0 (turboquant_scatter_oracle.hpp:185-217).
+ * block_dim is a grid-size hint (0 = one workgroup per item). When
+ * launch_probe is non-NULL, workgroup 0 writes int32[32]: lanes 0-7 its
+ * block index, 8-15 the grid size, 16-23 1, 24-31 item_count.
+ * Two work items of one launch must not own tokens of the same strip.
+ * Replaces launch_turboquant_reshape_scatter_aiv
+ * (kernels/ops/turboquant/turboquant_reshape_scatter_aiv.cpp:760-773).
+ */
+int tq4_reshape_scatter(void* stream, uint32_t block_dim, const uint16_t* key,
+                        const uint16_t* value, int8_t* key_cache, int8_t* value_cache,
+                        float* scale_cache, const int32_t* slot_mapping, const float* pi_signs,
+                        const int32_t* cu_seqlens, int32_t* launch_probe, uint32_t num_requests,
+                        uint32_t num_kv_heads, uint32_t head_size, uint32_t block_size,
+                        uint32_t num_blocks, uint32_t item_begin, uint32_t item_count,
+                        float inv_sqrt_len);
+
+/* ----------------------------------------------------------------------
+ * Paged split-K decode over the TQ4 cache.
+ *
+ * q: [num_seqs][num_heads][head_size] BF16; q head j reads kv head
+ * j / (num_heads / num_kv_heads). block_tables: [num_seqs][max_blocks_per_seq]
+ * physical pages; context_lens: [num_seqs] live tokens (<= max_blocks_per_seq
+ * * block_size). Scores are scale * (Pi q) . k_deq with Pi = M *
+ * inv_sqrt_len; tokens at or past context_len are masked by overwrite.
+ * Split k of num_splits owns logical pages Partition(ceil(ctx/S), K, k)
+ * (include/turboquant_splitk_contract.hpp:123-130); an empty split exports
+ * the neutral record m = -3e38, l = 0, acc = 0.
+ * output_stage: 0 = normalised context in the rotated basis, 1 = rotated back
+ * (Pi^T), 2 = rotated back and divided by 1 + exp(-gate), gate [num_seqs]
+ * [num_heads][head_size] FP32. out: [num_seqs][num_heads][head_size] BF16 RNE.
+ * flags: TQ4_DECODE_QUERY_ROTATED = q already holds Pi q (no rotation).
+ */
+#define TQ4_DECODE_QUERY_ROTATED 1u
+#define TQ4_MAX_SPLITS 256u
+
+/* Workspace bytes for num_splits (partial records plus the per-(seq, kv
+ * head) arrival counters of the fused entry). */
+size_t tq4_decode_workspace_bytes(uint32_t num_seqs, uint32_t num_heads, uint32_t num_kv_heads,
+                                  uint32_t head_size, uint32_t num_splits);
+
+/* A split count that puts several workgroups per compute unit in flight. */
+uint32_t tq4_decode_auto_splits(uint32_t num_seqs, uint32_t num_kv_heads,
+                                uint32_t max_blocks_per_seq, uint32_t block_size);
+
+/* Zero a workspace (a fill kernel, no memset node). The fused entry needs its
+ * arrival counters zero before the first call and leaves them zero. */
+int tq4_decode_workspace_init(void* stream, void* workspace, size_t workspace_bytes);
+
+/* Fused decode: partials, then the last-arriving workgroup of each (seq, kv
+ * head) LSE-combines them, rotates back, gates and stores BF16 -- one launch.
+ * Calls that overlap on one workspace race. num_splits 0 = auto.
+ * Modelled on turboquant_paged_attention_impl
+ * (kernels/ops/turboquant/baseline/turboquant_paged_attention.cpp:773-793);
+ * replaces the L2-spinlock accumulation
+ * (kernels/ops/turboquant/turboquant_splitk_reduce.cpp:279-350,385-405). */
+int tq4_paged_decode(void* stream, const uint16_t* q, const int8_t* key_cache,
+                     const int8_t* value_cache, const float* scale_cache,
+                     const int32_t* block_tables, const int32_t* context_lens,
+                     const float* pi_signs, const float* gate, void* workspace,
+                     size_t workspace_bytes, uint16_t* out, uint32_t num_seqs,
+                     uint32_t num_heads, uint32_t num_kv_heads, uint32_t head_size,
+                     uint32_t block_size, uint32_t num_blocks, uint32_t max_blocks_per_seq,
+                     uint32_t num_splits, float scale, float inv_sqrt_len,
+                     uint32_t output_stage, uint32_t flags);
+
+/* Partials only: workspace record (seq, q head, split) at float offset
+ * ((seq*num_heads + head)*num_splits + split)*(head_size + 4) holds
+ * [m, l, 0, 0, acc[head_size]] -- m the running max of the natural-log score,
+ * l = sum exp(s - m), acc = sum exp(s - m) * v in the rotated basis.
+ * Replaces launch_turboquant_paged_decode_splitk_aic
+ * (kernels/ops/turboquant/turboquant_paged_decode_attention.cpp:1727-1766). */
+int tq4_paged_decode_partials(void* stream, const uint16_t* q, const int8_t* key_cache,
+                              const int8_t* value_cache, const float* scale_cache,
+                              const int32_t* block_tables, const int32_t* context_lens,
+                              const float* pi_signs, float* workspace, size_t workspace_bytes,
+                              uint32_t num_seqs, uint32_t num_heads, uint32_t num_kv_heads,
+                              uint32_t head_size, uint32_t block_size, uint32_t num_blocks,
+                              uint32_t max_blocks_per_seq, uint32_t num_splits, float scale,
+                              float inv_sqrt_len, uint32_t flags);
+
+/* LSE combine of num_splits partial records per (seq, q head), then the
+ * egress for output_stage. Replaces the reference's host-side / SyncAll
+ * combine (tests/common/l2_atomic_oracle.hpp:156-176,
+ * kernels/ops/turboquant/baseline/turboquant_paged_attention.cpp:733-740). */
+int tq4_splitk_combine(void* stream, const float* workspace, const float* pi_signs,
+                       const float* gate, uint16_t* out, uint32_t num_seqs, uint32_t num_heads,
+                       uint32_t head_size, uint32_t num_splits, float inv_sqrt_len,
+                       uint32_t output_stage);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TQ4_H */

@@ -1,0 +1,824 @@
+/*
+ * tq4_oracle.c -- CPU restatement of the TurboQuant TQ4 hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY (see tq4_oracle.h). Built with -ffp-contract=off
+ * and no fast-math so FP32 operations happen exactly in the order written.
+ *
+ * Reference files restated here (paths relative to the reference checkout):
+ *   tests/common/turboquant_oracle.hpp          prefill writer, quantiser, slot contract
+ *   tests/common/turboquant_scatter_oracle.hpp  general-S index maps, scatter writer
+ *   tests/common/rotate_butterfly_oracle.hpp    butterfly stage order, sign placement
+ *   tests/common/paged_decode_oracle.hpp        score / recurrence order, egress
+ *   tests/common/single_token_decode_oracle.hpp GQA mapping, GoldenDecode
+ *   tests/common/aic_splitk_decode_fixture.hpp  partial record, neutral element
+ *   tests/common/splitk_decode_fixture.hpp      FP64 full-context reference
+ *   tests/common/l2_atomic_oracle.hpp           LSE combine step, egress
+ *   include/turboquant_splitk_contract.hpp      Partition
+ *   kernels/ops/turboquant/turboquant_decode_tail.hpp  live-token arithmetic
+ */
+#include "tq4_oracle.h"
+
+#include <math.h>
+#include <pthread.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ------------------------------------------------------------------ bf16 */
+static float bits_to_f32(uint32_t bits)
+{
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+static uint32_t f32_to_bits(float f)
+{
+    uint32_t b;
+    memcpy(&b, &f, 4);
+    return b;
+}
+
+/* turboquant_scatter_oracle.hpp:56-71 */
+float tq4o_bf16_to_f32(uint16_t raw) { return bits_to_f32((uint32_t)raw << 16); }
+
+uint16_t tq4o_f32_to_bf16(float value)
+{
+    const uint32_t bits = f32_to_bits(value);
+    if ((bits & 0x7f800000u) == 0x7f800000u && (bits & 0x7fffffu))
+        return (uint16_t)((bits >> 16) | 0x40u);
+    return (uint16_t)((bits + 0x7fffu + ((bits >> 16) & 1u)) >> 16);
+}
+
+/* ------------------------------------------------------------ index maps */
+/* turboquant_scatter_oracle.hpp:110-132 (general S, strip height 16) */
+uint64_t tq4o_key_nibble(uint32_t H, uint32_t S, uint32_t d, uint32_t page, uint32_t head,
+                         uint32_t token, uint32_t channel)
+{
+    return (((uint64_t)page * H + head) * S + token) * d + channel;
+}
+
+uint64_t tq4o_value_nibble(uint32_t H, uint32_t S, uint32_t d, uint32_t page, uint32_t head,
+                           uint32_t token, uint32_t channel)
+{
+    const uint64_t base = ((uint64_t)page * H + head) * S * d;
+    return base + (uint64_t)(token / TQ4O_STRIP) * TQ4O_STRIP * d +
+           (uint64_t)channel * TQ4O_STRIP + token % TQ4O_STRIP;
+}
+
+uint64_t tq4o_scale_index(uint32_t P, uint32_t H, uint32_t S, uint32_t plane, uint32_t page,
+                          uint32_t head, uint32_t token)
+{
+    return (((uint64_t)plane * P + page) * H + head) * S + token;
+}
+
+/* turboquant_scatter_oracle.hpp:220-235 */
+int tq4o_read_nibble(const int8_t* cache, uint64_t nibble)
+{
+    const uint8_t byte = (uint8_t)cache[nibble / 2];
+    const int raw = (nibble % 2 == 0) ? (byte & 0xF) : ((byte >> 4) & 0xF);
+    return raw >= 8 ? raw - 16 : raw;
+}
+
+void tq4o_write_nibble(int8_t* cache, uint64_t nibble, int value)
+{
+    const uint8_t nib = (uint8_t)(value & 0xF);
+    uint8_t* byte = (uint8_t*)&cache[nibble / 2];
+    if (nibble % 2 == 0)
+        *byte = (uint8_t)((*byte & 0xF0u) | nib);
+    else
+        *byte = (uint8_t)((*byte & 0x0Fu) | (uint8_t)(nib << 4));
+}
+
+/* -------------------------------------------------------------- rotation */
+/* turboquant_oracle.hpp:77-80, rotate_butterfly_oracle.hpp:69-72 */
+int tq4o_pi_sign(int channel)
+{
+    return ((channel * channel + 3 * channel + 1) % 7 < 3) ? -1 : 1;
+}
+
+void tq4o_canonical_signs(uint32_t d, float* signs)
+{
+    for (uint32_t c = 0; c < d; ++c) signs[c] = (float)tq4o_pi_sign((int)c);
+}
+
+static int parity(unsigned v)
+{
+    int p = 0;
+    while (v) {
+        p ^= (int)(v & 1u);
+        v >>= 1;
+    }
+    return p;
+}
+
+static int hadamard(int i, int j) { return parity((unsigned)(i & j)) ? -1 : 1; }
+
+/* turboquant_oracle.hpp:157-171: T[s][g][c0][i] = (s?-1:+1) * sign[g*32+c0] * H32[c0][i] */
+void tq4o_build_tables_i8(uint32_t d, const float* signs, int8_t* tables)
+{
+    const uint32_t groups = d / 32;
+    for (uint32_t s = 0; s < 2; ++s)
+        for (uint32_t g = 0; g < groups; ++g)
+            for (uint32_t c0 = 0; c0 < 32; ++c0)
+                for (uint32_t i = 0; i < 32; ++i)
+                    tables[((s * groups + g) * 32 + c0) * 32 + i] =
+                        (int8_t)((s ? -1 : 1) * (signs[g * 32 + c0] < 0 ? -1 : 1) *
+                                 hadamard((int)c0, (int)i));
+}
+
+/* Signs are recoverable from the tables: T[0][g][c0][0] = sign[g*32+c0]
+ * (H32[c0][0] = +1). Returns 0 if every block also matches the Hadamard
+ * structure of turboquant_oracle.hpp:177-195, -1 otherwise. */
+int tq4o_signs_from_tables_i8(uint32_t d, const int8_t* tables, float* signs)
+{
+    const uint32_t groups = d / 32;
+    for (uint32_t g = 0; g < groups; ++g)
+        for (uint32_t c0 = 0; c0 < 32; ++c0) signs[g * 32 + c0] = (float)tables[(g * 32 + c0) * 32];
+    for (uint32_t s = 0; s < 2; ++s)
+        for (uint32_t g = 0; g < groups; ++g)
+            for (uint32_t c0 = 0; c0 < 32; ++c0)
+                for (uint32_t i = 0; i < 32; ++i) {
+                    const int want = (s ? -1 : 1) * (signs[g * 32 + c0] < 0 ? -1 : 1) *
+                                     hadamard((int)c0, (int)i);
+                    if (tables[((s * groups + g) * 32 + c0) * 32 + i] != want) return -1;
+                }
+    return 0;
+}
+
+/* rotate_butterfly_oracle.hpp:120-128: out[i] = in[i^s] + ((i&s) ? -in[i] : in[i]) */
+static void butterfly_stage(float* v, float* tmp, uint32_t d, uint32_t stride)
+{
+    for (uint32_t i = 0; i < d; ++i) {
+        const float self = v[i];
+        const float partner = v[i ^ stride];
+        tmp[i] = (i & stride) ? partner - self : partner + self;
+    }
+    memcpy(v, tmp, d * sizeof(float));
+}
+
+/* Ingress: strides 1,2,4,8,16 | signs | 32,...,d/2
+ * (rotate_butterfly_oracle.hpp:44-48,130-142 at d=256; the inner H32 is fixed
+ * at 32 and the outer factor is H_{d/32}, turboquant_oracle.hpp:382-410). */
+void tq4o_rotate_ingress(const float* x, const float* signs, uint32_t d, float* y)
+{
+    float tmp[512];
+    memcpy(y, x, d * sizeof(float));
+    for (uint32_t s = 1; s < 32 && s < d; s <<= 1) butterfly_stage(y, tmp, d, s);
+    for (uint32_t i = 0; i < d; ++i) y[i] *= signs[i];
+    for (uint32_t s = 32; s < d; s <<= 1) butterfly_stage(y, tmp, d, s);
+}
+
+/* Egress (transpose): strides 32,...,d/2 | signs | 1,2,4,8,16
+ * (paged_decode_oracle.hpp:634-665, rotate_butterfly_oracle.hpp:44-48). */
+void tq4o_rotate_egress(const float* x, const float* signs, uint32_t d, float* y)
+{
+    float tmp[512];
+    memcpy(y, x, d * sizeof(float));
+    for (uint32_t s = 32; s < d; s <<= 1) butterfly_stage(y, tmp, d, s);
+    for (uint32_t i = 0; i < d; ++i) y[i] *= signs[i];
+    for (uint32_t s = 1; s < 32 && s < d; s <<= 1) butterfly_stage(y, tmp, d, s);
+}
+
+/* The definition: M[c1*32+c0][g*32+i] = H[c1][g] * sign[g*32+c0] * H32[c0][i]
+ * (rotate_butterfly_oracle.hpp:84-92), applied as a dense product in double.
+ * transpose=0: y = M x; transpose=1: y = M^T x. */
+void tq4o_rotate_dense(const float* x, const float* signs, uint32_t d, int transpose, double* y)
+{
+    for (uint32_t r = 0; r < d; ++r) {
+        double acc = 0.0;
+        for (uint32_t c = 0; c < d; ++c) {
+            const uint32_t row = transpose ? c : r;
+            const uint32_t col = transpose ? r : c;
+            const int c1 = (int)(row / 32), c0 = (int)(row % 32);
+            const int g = (int)(col / 32), i = (int)(col % 32);
+            const double m = (double)hadamard(c1, g) * (double)signs[g * 32 + c0] *
+                             (double)hadamard(c0, i);
+            acc += m * (double)x[c];
+        }
+        y[r] = acc;
+    }
+}
+
+/* ------------------------------------------------------------- quantiser */
+/* Exponent e with 2^e <= a < 2^(e+1), for finite a > 0 (ilogb). */
+static int exponent_of(float a)
+{
+    const uint32_t bits = f32_to_bits(a);
+    const uint32_t field = (bits >> 23) & 0xFFu;
+    if (field != 0) return (int)field - 127;
+    /* subnormal: a = m * 2^-149 */
+    const uint32_t m = bits & 0x7FFFFFu;
+    int top = 31;
+    while (top > 0 && !((m >> top) & 1u)) --top;
+    return top - 149;
+}
+
+/* Prefill: turboquant_oracle.hpp:412-448 (absmax floored at 1.0, scale =
+ * 2^(e-2) * invSqrtLen, q = min(rint_even(y * 2^(2-e)), 7)); the FP32 bit form
+ * is turboquant_reshape_and_cache_bf16.cpp:1470-1491.
+ * Exact: turboquant_scatter_oracle.hpp:185-217 (no floor, absmax == 0 gives
+ * scale 1.0 and q = 0). y * 2^(2-e) is exact, so the one rounding is RNE. */
+void tq4o_quantise_row(const float* y, uint32_t d, float inv_sqrt_len, int policy, int8_t* q,
+                       float* scale)
+{
+    float absmax = 0.0f;
+    for (uint32_t c = 0; c < d; ++c) {
+        const float a = fabsf(y[c]);
+        if (a > absmax) absmax = a;
+    }
+    if (policy == TQ4O_POLICY_PREFILL) {
+        if (absmax < 1.0f) absmax = 1.0f;
+    } else if (absmax == 0.0f) {
+        for (uint32_t c = 0; c < d; ++c) q[c] = 0;
+        *scale = 1.0f;
+        return;
+    }
+    const int e = exponent_of(absmax);
+    *scale = ldexpf(1.0f, e - 2) * inv_sqrt_len;
+    for (uint32_t c = 0; c < d; ++c) {
+        float v = rintf(ldexpf(y[c], 2 - e));  /* default rounding mode: ties to even */
+        if (v > 7.0f) v = 7.0f;
+        q[c] = (int8_t)(int)v;
+    }
+}
+
+/* --------------------------------------------------------------- writers */
+static float load_input(int in_dtype, const void* base, uint64_t index)
+{
+    if (in_dtype == TQ4O_IN_INT8) return (float)((const int8_t*)base)[index];
+    return tq4o_bf16_to_f32(((const uint16_t*)base)[index]);
+}
+
+/* One (token row, head, plane) row: rotate, quantise, pack at (page, token). */
+static void write_row(int in_dtype, const void* src, uint64_t row_offset, int8_t* cache,
+                      float* scale_cache, uint32_t plane, uint32_t page, uint32_t head,
+                      uint32_t token_in_page, const float* signs, uint32_t H, uint32_t d,
+                      uint32_t S, uint32_t P, float inv_sqrt_len, int policy)
+{
+    float x[512], y[512];
+    int8_t q[512];
+    float scale;
+    for (uint32_t c = 0; c < d; ++c) x[c] = load_input(in_dtype, src, row_offset + c);
+    tq4o_rotate_ingress(x, signs, d, y);
+    tq4o_quantise_row(y, d, inv_sqrt_len, policy, q, &scale);
+    for (uint32_t c = 0; c < d; ++c) {
+        const uint64_t n = plane == 0 ? tq4o_key_nibble(H, S, d, page, head, token_in_page, c)
+                                      : tq4o_value_nibble(H, S, d, page, head, token_in_page, c);
+        tq4o_write_nibble(cache, n, q[c]);
+    }
+    scale_cache[tq4o_scale_index(P, H, S, plane, page, head, token_in_page)] = scale;
+}
+
+/* Strip slot contract (turboquant_oracle.hpp:274-287, restated per 16-token
+ * strip): slot[16s+i] == slot[16s] + i, slot[16s] % 16 == 0, page < P.
+ * Returns the first slot of the strip, or -1 when the strip violates it. */
+static int64_t strip_first_slot(const int32_t* slots, uint32_t strip, uint32_t S, uint32_t P)
+{
+    const int32_t first = slots[(uint64_t)strip * TQ4O_STRIP];
+    if (first < 0 || first % (int32_t)TQ4O_STRIP != 0) return -1;
+    for (uint32_t i = 1; i < TQ4O_STRIP; ++i)
+        if (slots[(uint64_t)strip * TQ4O_STRIP + i] != first + (int32_t)i) return -1;
+    if ((uint32_t)first / S >= P) return -1;
+    return first;
+}
+
+typedef struct {
+    int in_dtype;
+    const void* key;
+    const void* value;
+    int8_t* key_cache;
+    int8_t* value_cache;
+    float* scale_cache;
+    const int32_t* slots;
+    const float* signs;
+    uint32_t num_tokens, H, d, S, P;
+    float inv_sqrt_len;
+    int policy;
+    uint32_t strip_begin, strip_end;
+    int64_t skipped;
+} WriterJob;
+
+static void writer_run(WriterJob* j)
+{
+    j->skipped = 0;
+    for (uint32_t strip = j->strip_begin; strip < j->strip_end; ++strip) {
+        const int64_t first = strip_first_slot(j->slots, strip, j->S, j->P);
+        if (first < 0) {
+            ++j->skipped;
+            continue;
+        }
+        const uint32_t page = (uint32_t)first / j->S;
+        const uint32_t tip0 = (uint32_t)first % j->S;
+        for (uint32_t t = 0; t < TQ4O_STRIP; ++t) {
+            const uint64_t token = (uint64_t)strip * TQ4O_STRIP + t;
+            for (uint32_t h = 0; h < j->H; ++h) {
+                const uint64_t row = (token * j->H + h) * j->d;
+                write_row(j->in_dtype, j->key, row, j->key_cache, j->scale_cache, 0, page, h,
+                          tip0 + t, j->signs, j->H, j->d, j->S, j->P, j->inv_sqrt_len,
+                          j->policy);
+                write_row(j->in_dtype, j->value, row, j->value_cache, j->scale_cache, 1, page, h,
+                          tip0 + t, j->signs, j->H, j->d, j->S, j->P, j->inv_sqrt_len,
+                          j->policy);
+            }
+        }
+    }
+}
+
+static void* writer_thread(void* arg)
+{
+    writer_run((WriterJob*)arg);
+    return NULL;
+}
+
+static int writer_geometry_ok(uint32_t num_tokens, uint32_t H, uint32_t d, uint32_t S,
+                              uint32_t P)
+{
+    return num_tokens % TQ4O_STRIP == 0 && H > 0 && d >= 32 && d <= 512 && d % 32 == 0 &&
+           (d & (d - 1)) == 0 && S > 0 && S % TQ4O_STRIP == 0 && P > 0;
+}
+
+/* The aligned prefill writer: compute_oracle_reference
+ * (turboquant_oracle.hpp:476-513) per 16-token strip. A strip whose slots
+ * violate the contract writes nothing and is counted (bad_slot_strip).
+ * Returns the number of skipped strips, or -1 on bad geometry. */
+int64_t tq4o_reshape_and_cache_mt(int in_dtype, const void* key, const void* value,
+                                  int8_t* key_cache, int8_t* value_cache, float* scale_cache,
+                                  const int32_t* slot_mapping, const float* pi_signs,
+                                  uint32_t num_tokens, uint32_t num_kv_heads, uint32_t head_size,
+                                  uint32_t block_size, uint32_t num_blocks, float inv_sqrt_len,
+                                  int policy, uint32_t threads)
+{
+    if (!writer_geometry_ok(num_tokens, num_kv_heads, head_size, block_size, num_blocks))
+        return -1;
+    const uint32_t strips = num_tokens / TQ4O_STRIP;
+    if (threads < 1) threads = 1;
+    if (threads > strips && strips > 0) threads = strips;
+    if (threads > 256) threads = 256;
+    WriterJob jobs[256];
+    pthread_t tids[256];
+    for (uint32_t t = 0; t < threads; ++t) {
+        WriterJob* j = &jobs[t];
+        j->in_dtype = in_dtype;
+        j->key = key;
+        j->value = value;
+        j->key_cache = key_cache;
+        j->value_cache = value_cache;
+        j->scale_cache = scale_cache;
+        j->slots = slot_mapping;
+        j->signs = pi_signs;
+        j->num_tokens = num_tokens;
+        j->H = num_kv_heads;
+        j->d = head_size;
+        j->S = block_size;
+        j->P = num_blocks;
+        j->inv_sqrt_len = inv_sqrt_len;
+        j->policy = policy;
+        j->strip_begin = (uint32_t)((uint64_t)strips * t / threads);
+        j->strip_end = (uint32_t)((uint64_t)strips * (t + 1) / threads);
+    }
+    if (threads == 1) {
+        writer_run(&jobs[0]);
+    } else {
+        for (uint32_t t = 0; t < threads; ++t) pthread_create(&tids[t], NULL, writer_thread, &jobs[t]);
+        for (uint32_t t = 0; t < threads; ++t) pthread_join(tids[t], NULL);
+    }
+    int64_t skipped = 0;
+    for (uint32_t t = 0; t < threads; ++t) skipped += jobs[t].skipped;
+    return skipped;
+}
+
+int64_t tq4o_reshape_and_cache(int in_dtype, const void* key, const void* value,
+                               int8_t* key_cache, int8_t* value_cache, float* scale_cache,
+                               const int32_t* slot_mapping, const float* pi_signs,
+                               uint32_t num_tokens, uint32_t num_kv_heads, uint32_t head_size,
+                               uint32_t block_size, uint32_t num_blocks, float inv_sqrt_len,
+                               int policy)
+{
+    return tq4o_reshape_and_cache_mt(in_dtype, key, value, key_cache, value_cache, scale_cache,
+                                     slot_mapping, pi_signs, num_tokens, num_kv_heads, head_size,
+                                     block_size, num_blocks, inv_sqrt_len, policy, 1);
+}
+
+/* The arbitrary-slot writer: turboquant_reshape_scatter_aiv.cpp:684-722 item
+ * loop over (request, kv_head), tokens from cu_seqlens (NULL = one token per
+ * request), slot < 0 skipped; per-row reference turboquant_scatter_oracle.hpp
+ * :291-342 (exact-absmax quantiser, write_nibble preserving the partner
+ * nibble, so every unowned lane of the value strip is preserved).
+ * Returns the number of rows written, or -1 on bad geometry. */
+int64_t tq4o_reshape_scatter(const uint16_t* key, const uint16_t* value, int8_t* key_cache,
+                             int8_t* value_cache, float* scale_cache,
+                             const int32_t* slot_mapping, const float* pi_signs,
+                             const int32_t* cu_seqlens, uint32_t num_requests,
+                             uint32_t num_kv_heads, uint32_t head_size, uint32_t block_size,
+                             uint32_t num_blocks, uint32_t item_begin, uint32_t item_count,
+                             float inv_sqrt_len)
+{
+    if (num_kv_heads == 0 || head_size < 32 || head_size > 512 || head_size % 32 ||
+        (head_size & (head_size - 1)) || block_size == 0 || block_size % TQ4O_STRIP ||
+        num_blocks == 0)
+        return -1;
+    int64_t written = 0;
+    const uint32_t H = num_kv_heads, d = head_size, S = block_size, P = num_blocks;
+    for (uint64_t item = item_begin; item < (uint64_t)item_begin + item_count; ++item) {
+        const uint32_t request = (uint32_t)(item / H);
+        const uint32_t head = (uint32_t)(item % H);
+        if (request >= num_requests) continue;
+        const uint32_t t0 = cu_seqlens ? (uint32_t)cu_seqlens[request] : request;
+        const uint32_t t1 = cu_seqlens ? (uint32_t)cu_seqlens[request + 1] : request + 1;
+        for (uint32_t token = t0; token < t1; ++token) {
+            const int32_t slot = slot_mapping[token];
+            if (slot < 0) continue;
+            const uint32_t page = (uint32_t)slot / S;
+            if (page >= P) continue;
+            const uint32_t tip = (uint32_t)slot % S;
+            const uint64_t row = ((uint64_t)token * H + head) * d;
+            write_row(TQ4O_IN_BF16, key, row, key_cache, scale_cache, 0, page, head, tip,
+                      pi_signs, H, d, S, P, inv_sqrt_len, TQ4O_POLICY_EXACT);
+            write_row(TQ4O_IN_BF16, value, row, value_cache, scale_cache, 1, page, head, tip,
+                      pi_signs, H, d, S, P, inv_sqrt_len, TQ4O_POLICY_EXACT);
+            written += 2;
+        }
+    }
+    return written;
+}
+
+/* ---------------------------------------------------------------- decode */
+/* include/turboquant_splitk_contract.hpp:123-130 */
+void tq4o_partition(uint32_t pages, uint32_t splits, uint32_t split, uint32_t* begin,
+                    uint32_t* count)
+{
+    const uint32_t width = (pages + splits - 1u) / splits;
+    const uint32_t b = split * width;
+    const uint32_t remaining = b < pages ? pages - b : 0u;
+    *begin = b;
+    *count = remaining < width ? remaining : width;
+}
+
+/* turboquant_decode_tail.hpp:109-118 */
+uint32_t tq4o_active_in_strip(uint64_t token_base, uint32_t seq_len)
+{
+    const uint64_t live = seq_len;
+    if (token_base >= live) return 0u;
+    return live - token_base >= TQ4O_STRIP ? TQ4O_STRIP : (uint32_t)(live - token_base);
+}
+
+uint32_t tq4o_record_floats(uint32_t head_size) { return head_size + 4u; }
+
+/* q_eff = (M q) * inv_sqrt_len * scale: Pi = M / sqrt(d) applied to the
+ * query, with the softmax scale folded in (paged_decode_oracle.hpp:127-143,
+ * single_token_decode_oracle.hpp:121-134; the reference rounds q_rot to
+ * BF16, this restatement keeps FP32). */
+void tq4o_rotate_query(const uint16_t* q, const float* signs, uint32_t d, float inv_sqrt_len,
+                       float scale, float* q_eff)
+{
+    float x[512], y[512];
+    for (uint32_t c = 0; c < d; ++c) x[c] = tq4o_bf16_to_f32(q[c]);
+    tq4o_rotate_ingress(x, signs, d, y);
+    for (uint32_t c = 0; c < d; ++c) q_eff[c] = (y[c] * inv_sqrt_len) * scale;
+}
+
+/* l2_atomic_oracle.hpp:156-166, in the same FP32 instruction order */
+void tq4o_combine_step(float* m, float* l, float* acc, float m_t, float l_t, const float* acc_t,
+                       uint32_t d)
+{
+    const float m_new = *m > m_t ? *m : m_t;
+    const float a_curr = expf(*m - m_new);
+    const float a_tile = expf(m_t - m_new);
+    *l = *l * a_curr + l_t * a_tile;
+    for (uint32_t c = 0; c < d; ++c) acc[c] = acc[c] * a_curr + acc_t[c] * a_tile;
+    *m = m_new;
+}
+
+#define TQ4O_FLAG_QUERY_ROTATED 1u
+
+typedef struct {
+    const uint16_t* q;
+    const int8_t* key_cache;
+    const int8_t* value_cache;
+    const float* scale_cache;
+    const int32_t* block_tables;
+    const int32_t* context_lens;
+    const float* signs;
+    float* workspace;
+    uint32_t B, Hq, Hkv, d, S, P, max_blocks, splits;
+    float scale, inv_sqrt_len;
+    uint32_t flags;
+    uint32_t item_begin, item_end; /* items over (seq, kv head, split) */
+} DecodeJob;
+
+/* One (seq, kv head, split) task: every q head of the group walks the
+ * split's strips in order with the online-softmax recurrence of
+ * single_token_decode_oracle.hpp:257-310 (scores, tile max, alpha, p, value
+ * scale folded into p, l and acc updates), tail masking by overwrite
+ * (turboquant_decode_tail.hpp:56-72), fully dead strips skipped, and the
+ * neutral element (m = -3e38, l = 0, acc = 0) for an empty split
+ * (turboquant_paged_decode_attention.cpp:1630-1633). */
+static void decode_item(const DecodeJob* j, uint32_t item)
+{
+    const uint32_t split = item % j->splits;
+    const uint32_t kvh = (item / j->splits) % j->Hkv;
+    const uint32_t seq = item / (j->splits * j->Hkv);
+    const uint32_t G = j->Hq / j->Hkv;
+    const uint32_t d = j->d, S = j->S;
+    const uint32_t rec = tq4o_record_floats(d);
+    const uint32_t ctx = (uint32_t)j->context_lens[seq];
+    const uint32_t pages = (ctx + S - 1) / S;
+    uint32_t pbegin, pcount;
+    tq4o_partition(pages, j->splits, split, &pbegin, &pcount);
+
+    for (uint32_t g = 0; g < G; ++g) {
+        const uint32_t qh = kvh * G + g;
+        float q_eff[512];
+        const uint16_t* qrow = j->q + ((uint64_t)seq * j->Hq + qh) * d;
+        if (j->flags & TQ4O_FLAG_QUERY_ROTATED) {
+            for (uint32_t c = 0; c < d; ++c) q_eff[c] = tq4o_bf16_to_f32(qrow[c]) * j->scale;
+        } else {
+            tq4o_rotate_query(qrow, j->signs, d, j->inv_sqrt_len, j->scale, q_eff);
+        }
+        float m = TQ4O_MASKED, l = 0.0f;
+        float acc[512];
+        for (uint32_t c = 0; c < d; ++c) acc[c] = 0.0f;
+
+        for (uint32_t lp = pbegin; lp < pbegin + pcount; ++lp) {
+            const uint32_t phys = (uint32_t)j->block_tables[(uint64_t)seq * j->max_blocks + lp];
+            for (uint32_t sip = 0; sip < S / TQ4O_STRIP; ++sip) {
+                const uint64_t tbase = (uint64_t)lp * S + sip * TQ4O_STRIP;
+                const uint32_t active = tq4o_active_in_strip(tbase, ctx);
+                if (active == 0) continue;
+                float scores[TQ4O_STRIP];
+                float tile_max = TQ4O_MASKED;
+                for (uint32_t t = 0; t < TQ4O_STRIP; ++t) {
+                    if (t >= active) {
+                        scores[t] = TQ4O_MASKED;
+                        continue;
+                    }
+                    const uint32_t tip = sip * TQ4O_STRIP + t;
+                    float dot = 0.0f;
+                    for (uint32_t c = 0; c < d; ++c)
+                        dot += q_eff[c] *
+                               (float)tq4o_read_nibble(j->key_cache,
+                                                       tq4o_key_nibble(j->Hkv, S, d, phys, kvh, tip, c));
+                    scores[t] =
+                        dot * j->scale_cache[tq4o_scale_index(j->P, j->Hkv, S, 0, phys, kvh, tip)];
+                    if (scores[t] > tile_max) tile_max = scores[t];
+                }
+                const float m_new = m > tile_max ? m : tile_max;
+                const float alpha = expf(m - m_new);
+                float p[TQ4O_STRIP];
+                float p_sum = 0.0f;
+                for (uint32_t t = 0; t < TQ4O_STRIP; ++t) {
+                    p[t] = t < active ? expf(scores[t] - m_new) : 0.0f;
+                    p_sum += p[t];
+                }
+                float ps[TQ4O_STRIP];
+                for (uint32_t t = 0; t < active; ++t)
+                    ps[t] = p[t] * j->scale_cache[tq4o_scale_index(j->P, j->Hkv, S, 1, phys, kvh,
+                                                                   sip * TQ4O_STRIP + t)];
+                for (uint32_t c = 0; c < d; ++c) {
+                    float weighted = 0.0f;
+                    for (uint32_t t = 0; t < active; ++t)
+                        weighted += ps[t] * (float)tq4o_read_nibble(
+                                                j->value_cache,
+                                                tq4o_value_nibble(j->Hkv, S, d, phys, kvh,
+                                                                  sip * TQ4O_STRIP + t, c));
+                    acc[c] = acc[c] * alpha + weighted;
+                }
+                l = l * alpha + p_sum;
+                m = m_new;
+            }
+        }
+        float* out = j->workspace + (((uint64_t)seq * j->Hq + qh) * j->splits + split) * rec;
+        out[0] = m;
+        out[1] = l;
+        out[2] = 0.0f;
+        out[3] = 0.0f;
+        for (uint32_t c = 0; c < d; ++c) out[4 + c] = acc[c];
+    }
+}
+
+static void* decode_thread(void* arg)
+{
+    const DecodeJob* j = (const DecodeJob*)arg;
+    for (uint32_t item = j->item_begin; item < j->item_end; ++item) decode_item(j, item);
+    return NULL;
+}
+
+static int decode_geometry_ok(uint32_t B, uint32_t Hq, uint32_t Hkv, uint32_t d, uint32_t S,
+                              uint32_t splits)
+{
+    return B > 0 && Hkv > 0 && Hq > 0 && Hq % Hkv == 0 && d >= 32 && d <= 512 && d % 32 == 0 &&
+           (d & (d - 1)) == 0 && S > 0 && S % TQ4O_STRIP == 0 && splits > 0;
+}
+
+static int decode_partials_mt(const uint16_t* q, const int8_t* key_cache,
+                              const int8_t* value_cache, const float* scale_cache,
+                              const int32_t* block_tables, const int32_t* context_lens,
+                              const float* pi_signs, float* workspace, uint32_t num_seqs,
+                              uint32_t num_heads, uint32_t num_kv_heads, uint32_t head_size,
+                              uint32_t block_size, uint32_t num_blocks,
+                              uint32_t max_blocks_per_seq, uint32_t num_splits, float scale,
+                              float inv_sqrt_len, uint32_t flags, uint32_t threads)
+{
+    if (!decode_geometry_ok(num_seqs, num_heads, num_kv_heads, head_size, block_size,
+                            num_splits))
+        return -1;
+    for (uint32_t b = 0; b < num_seqs; ++b) {
+        if (context_lens[b] < 0) return -1;
+        if ((uint64_t)context_lens[b] > (uint64_t)max_blocks_per_seq * block_size) return -1;
+    }
+    const uint32_t items = num_seqs * num_kv_heads * num_splits;
+    if (threads < 1) threads = 1;
+    if (threads > items) threads = items;
+    if (threads > 256) threads = 256;
+    DecodeJob jobs[256];
+    pthread_t tids[256];
+    for (uint32_t t = 0; t < threads; ++t) {
+        DecodeJob* j = &jobs[t];
+        j->q = q;
+        j->key_cache = key_cache;
+        j->value_cache = value_cache;
+        j->scale_cache = scale_cache;
+        j->block_tables = block_tables;
+        j->context_lens = context_lens;
+        j->signs = pi_signs;
+        j->workspace = workspace;
+        j->B = num_seqs;
+        j->Hq = num_heads;
+        j->Hkv = num_kv_heads;
+        j->d = head_size;
+        j->S = block_size;
+        j->P = num_blocks;
+        j->max_blocks = max_blocks_per_seq;
+        j->splits = num_splits;
+        j->scale = scale;
+        j->inv_sqrt_len = inv_sqrt_len;
+        j->flags = flags;
+        j->item_begin = (uint32_t)((uint64_t)items * t / threads);
+        j->item_end = (uint32_t)((uint64_t)items * (t + 1) / threads);
+    }
+    if (threads == 1) {
+        decode_thread(&jobs[0]);
+    } else {
+        for (uint32_t t = 0; t < threads; ++t) pthread_create(&tids[t], NULL, decode_thread, &jobs[t]);
+        for (uint32_t t = 0; t < threads; ++t) pthread_join(tids[t], NULL);
+    }
+    return 0;
+}
+
+int tq4o_decode_partials(const uint16_t* q, const int8_t* key_cache, const int8_t* value_cache,
+                         const float* scale_cache, const int32_t* block_tables,
+                         const int32_t* context_lens, const float* pi_signs, float* workspace,
+                         uint32_t num_seqs, uint32_t num_heads, uint32_t num_kv_heads,
+                         uint32_t head_size, uint32_t block_size, uint32_t num_blocks,
+                         uint32_t max_blocks_per_seq, uint32_t num_splits, float scale,
+                         float inv_sqrt_len, uint32_t flags)
+{
+    return decode_partials_mt(q, key_cache, value_cache, scale_cache, block_tables, context_lens,
+                              pi_signs, workspace, num_seqs, num_heads, num_kv_heads, head_size,
+                              block_size, num_blocks, max_blocks_per_seq, num_splits, scale,
+                              inv_sqrt_len, flags, 1);
+}
+
+/* Combine + egress per (seq, q head): the splits merged in split order with
+ * combine_step from the identity (l2_atomic_oracle.hpp:100-108,156-176),
+ * normalised acc / l (0 when l == 0, paged_decode_oracle.hpp:603-608),
+ * then output_stage 0: rotated basis; 1: egress butterfly times invSqrtLen
+ * (paged_decode_oracle.hpp:648-665); 2: also divided by 1 + exp(-gate)
+ * (single_token_decode_oracle.hpp:325-330). BF16 RNE. */
+int tq4o_combine(const float* workspace, const float* pi_signs, const float* gate, uint16_t* out,
+                 float* out_f32, uint32_t num_seqs, uint32_t num_heads, uint32_t head_size,
+                 uint32_t num_splits, float inv_sqrt_len, uint32_t output_stage)
+{
+    const uint32_t d = head_size, rec = tq4o_record_floats(d);
+    if (output_stage > 2 || (output_stage == 2 && gate == NULL) || num_splits == 0) return -1;
+    for (uint64_t row = 0; row < (uint64_t)num_seqs * num_heads; ++row) {
+        float m = TQ4O_MASKED, l = 0.0f, acc[512], norm[512], rot[512];
+        for (uint32_t c = 0; c < d; ++c) acc[c] = 0.0f;
+        for (uint32_t k = 0; k < num_splits; ++k) {
+            const float* r = workspace + (row * num_splits + k) * rec;
+            tq4o_combine_step(&m, &l, acc, r[0], r[1], r + 4, d);
+        }
+        for (uint32_t c = 0; c < d; ++c) norm[c] = l == 0.0f ? 0.0f : acc[c] / l;
+        if (output_stage == 0) {
+            memcpy(rot, norm, d * sizeof(float));
+        } else {
+            tq4o_rotate_egress(norm, pi_signs, d, rot);
+            for (uint32_t c = 0; c < d; ++c) rot[c] *= inv_sqrt_len;
+            if (output_stage == 2)
+                for (uint32_t c = 0; c < d; ++c) rot[c] = rot[c] / (1.0f + expf(-gate[row * d + c]));
+        }
+        for (uint32_t c = 0; c < d; ++c) {
+            if (out) out[row * d + c] = tq4o_f32_to_bf16(rot[c]);
+            if (out_f32) out_f32[row * d + c] = rot[c];
+        }
+    }
+    return 0;
+}
+
+int tq4o_paged_decode(const uint16_t* q, const int8_t* key_cache, const int8_t* value_cache,
+                      const float* scale_cache, const int32_t* block_tables,
+                      const int32_t* context_lens, const float* pi_signs, const float* gate,
+                      uint16_t* out, float* out_f32, uint32_t num_seqs, uint32_t num_heads,
+                      uint32_t num_kv_heads, uint32_t head_size, uint32_t block_size,
+                      uint32_t num_blocks, uint32_t max_blocks_per_seq, uint32_t num_splits,
+                      float scale, float inv_sqrt_len, uint32_t output_stage, uint32_t flags,
+                      uint32_t threads)
+{
+    if (num_splits == 0) return -1;
+    const size_t floats = (size_t)num_seqs * num_heads * num_splits * tq4o_record_floats(head_size);
+    float* ws = (float*)malloc(floats * sizeof(float));
+    if (!ws) return -2;
+    int rc = decode_partials_mt(q, key_cache, value_cache, scale_cache, block_tables, context_lens,
+                                pi_signs, ws, num_seqs, num_heads, num_kv_heads, head_size,
+                                block_size, num_blocks, max_blocks_per_seq, num_splits, scale,
+                                inv_sqrt_len, flags, threads);
+    if (rc == 0)
+        rc = tq4o_combine(ws, pi_signs, gate, out, out_f32, num_seqs, num_heads, head_size,
+                          num_splits, inv_sqrt_len, output_stage);
+    free(ws);
+    return rc;
+}
+
+/* Independent full-context FP64 reference (splitk_decode_fixture.hpp:193-248):
+ * direct softmax over the live tokens read through the block table, dead
+ * tokens skipped (never weighted by zero), the query rotated by the dense
+ * matrix in double, the output rotated back by the dense transpose. */
+int tq4o_decode_reference_f64(const uint16_t* q, const int8_t* key_cache,
+                              const int8_t* value_cache, const float* scale_cache,
+                              const int32_t* block_tables, const int32_t* context_lens,
+                              const float* pi_signs, const float* gate, double* out,
+                              uint32_t num_seqs, uint32_t num_heads, uint32_t num_kv_heads,
+                              uint32_t head_size, uint32_t block_size, uint32_t num_blocks,
+                              uint32_t max_blocks_per_seq, float scale, float inv_sqrt_len,
+                              uint32_t output_stage, uint32_t flags)
+{
+    if (!decode_geometry_ok(num_seqs, num_heads, num_kv_heads, head_size, block_size, 1))
+        return -1;
+    if (output_stage > 2 || (output_stage == 2 && gate == NULL)) return -1;
+    const uint32_t d = head_size, S = block_size, G = num_heads / num_kv_heads;
+    for (uint32_t b = 0; b < num_seqs; ++b) {
+        const uint32_t ctx = (uint32_t)context_lens[b];
+        if ((uint64_t)ctx > (uint64_t)max_blocks_per_seq * S) return -1;
+        double* scores = (double*)malloc(sizeof(double) * (ctx ? ctx : 1));
+        for (uint32_t qh = 0; qh < num_heads; ++qh) {
+            const uint32_t kvh = qh / G;
+            double qr[512], acc[512], norm_d[512];
+            const uint16_t* qrow = q + ((uint64_t)b * num_heads + qh) * d;
+            if (flags & TQ4O_FLAG_QUERY_ROTATED) {
+                for (uint32_t c = 0; c < d; ++c) qr[c] = (double)tq4o_bf16_to_f32(qrow[c]) * scale;
+            } else {
+                float x[512];
+                for (uint32_t c = 0; c < d; ++c) x[c] = tq4o_bf16_to_f32(qrow[c]);
+                tq4o_rotate_dense(x, pi_signs, d, 0, qr);
+                for (uint32_t c = 0; c < d; ++c) qr[c] *= (double)inv_sqrt_len * (double)scale;
+            }
+            double mx = -INFINITY;
+            for (uint32_t t = 0; t < ctx; ++t) {
+                const uint32_t phys = (uint32_t)block_tables[(uint64_t)b * max_blocks_per_seq + t / S];
+                const uint32_t tip = t % S;
+                double dot = 0.0;
+                for (uint32_t c = 0; c < d; ++c)
+                    dot += qr[c] * (double)tq4o_read_nibble(
+                                       key_cache, tq4o_key_nibble(num_kv_heads, S, d, phys, kvh, tip, c));
+                scores[t] =
+                    dot * (double)scale_cache[tq4o_scale_index(num_blocks, num_kv_heads, S, 0, phys, kvh, tip)];
+                if (scores[t] > mx) mx = scores[t];
+            }
+            double den = 0.0;
+            for (uint32_t c = 0; c < d; ++c) acc[c] = 0.0;
+            for (uint32_t t = 0; t < ctx; ++t) {
+                const uint32_t phys = (uint32_t)block_tables[(uint64_t)b * max_blocks_per_seq + t / S];
+                const uint32_t tip = t % S;
+                const double w = exp(scores[t] - mx);
+                den += w;
+                const double pv =
+                    w * (double)scale_cache[tq4o_scale_index(num_blocks, num_kv_heads, S, 1, phys, kvh, tip)];
+                for (uint32_t c = 0; c < d; ++c)
+                    acc[c] += pv * (double)tq4o_read_nibble(
+                                       value_cache, tq4o_value_nibble(num_kv_heads, S, d, phys, kvh, tip, c));
+            }
+            for (uint32_t c = 0; c < d; ++c) norm_d[c] = den > 0.0 ? acc[c] / den : 0.0;
+            double* dst = out + ((uint64_t)b * num_heads + qh) * d;
+            if (output_stage == 0) {
+                for (uint32_t c = 0; c < d; ++c) dst[c] = norm_d[c];
+            } else {
+                /* dense M^T applied in double */
+                for (uint32_t r = 0; r < d; ++r) {
+                    double s = 0.0;
+                    for (uint32_t c = 0; c < d; ++c) {
+                        const int c1 = (int)(c / 32), c0 = (int)(c % 32);
+                        const int g = (int)(r / 32), i = (int)(r % 32);
+                        s += (double)hadamard(c1, g) * (double)pi_signs[g * 32 + c0] *
+                             (double)hadamard(c0, i) * norm_d[c];
+                    }
+                    s *= (double)inv_sqrt_len;
+                    if (output_stage == 2)
+                        s = s / (1.0 + exp(-(double)gate[((uint64_t)b * num_heads + qh) * d + r]));
+                    dst[r] = s;
+                }
+            }
+        }
+        free(scores);
+    }
+    return 0;
+}

@@ -1,0 +1,195 @@
+"""GPU parity of the paged split-K decode against the C oracle.
+
+Tolerances (BF16 output, the north_star's): max-abs <= 2e-2 and mean-rel <=
+1e-3 against the FP32 oracle rounded to BF16 (the same final rounding the
+device applies); also reported against the FP64 reference. Partial records
+are checked with the reference rig's budgets
+(tests/npu/turboquant_splitk_rigs.hpp:144-158): m 2e-6*max(1,|m|),
+l 1e-4*max(1,l), acc 2e-4*max|acc| + 1e-5*l + 1e-6 -- relaxed here by the
+fp16 MFMA operands (see DECODE_* below) -- and the empty-split neutral
+element exactly.
+"""
+import math
+
+import numpy as np
+import pytest
+
+from gpu_helpers import bf16_out_error, canary_bytes, canary_floats, dev, host
+from oracle_bindings import FLAG_QUERY_ROTATED, IN_BF16, f32_to_bf16
+
+pytestmark = pytest.mark.gpu
+
+MAX_ABS = 2e-2
+MEAN_REL = 1e-3
+
+
+def build_cache(oracle, rng, ctx_lens, H, d, S, P, tail_canary=True):
+    """Quantise N(0,1) K/V for every sequence through the oracle writer into a
+    shuffled page pool; dead slots of partial pages keep the NaN canary."""
+    B = len(ctx_lens)
+    pages_per = [(c + S - 1) // S for c in ctx_lens]
+    assert sum(pages_per) <= P
+    perm = rng.permutation(P)
+    max_blocks = max(max(pages_per), 1)
+    tables = np.zeros((B, max_blocks), np.int32)
+    nbytes = P * H * S * d // 2
+    kc, vc, sc = canary_bytes(nbytes), canary_bytes(nbytes), canary_floats(2 * P * H * S)
+    if not tail_canary:
+        kc[:] = 0
+        vc[:] = 0
+        sc[:] = 0
+    at = 0
+    isl = np.float32(1.0 / math.sqrt(d))
+    signs = oracle.canonical_signs(d)
+    for b, c in enumerate(ctx_lens):
+        n = pages_per[b]
+        tables[b, :n] = perm[at:at + n]
+        at += n
+        tok = np.arange(c)
+        slots = (tables[b, tok // S] * S + tok % S).astype(np.int32)
+        # whole strips through the aligned writer, the tail through the scatter writer
+        full = (c // 16) * 16
+        if full:
+            k = f32_to_bf16(rng.standard_normal((full, H, d)).astype(np.float32))
+            v = f32_to_bf16(rng.standard_normal((full, H, d)).astype(np.float32))
+            assert oracle.reshape_and_cache(IN_BF16, k, v, kc, vc, sc, slots[:full], signs, H, d,
+                                            S, P, isl) == 0
+        if c > full:
+            t = c - full
+            k = f32_to_bf16(rng.standard_normal((t, H, d)).astype(np.float32))
+            v = f32_to_bf16(rng.standard_normal((t, H, d)).astype(np.float32))
+            cu = np.array([0, t], np.int32)
+            oracle.reshape_scatter(k, v, kc, vc, sc, slots[full:], signs, cu, 1, H, d, S, P, 0,
+                                   H, isl)
+    return kc, vc, sc, tables, signs, isl
+
+
+def run_decode(tq4, oracle, rng, ctx_lens, Hq, H, d, S, P, K, stage=1, gate=None):
+    kc, vc, sc, tables, signs, isl = build_cache(oracle, rng, ctx_lens, H, d, S, P)
+    B = len(ctx_lens)
+    ctx = np.array(ctx_lens, np.int32)
+    q = f32_to_bf16(rng.standard_normal((B, Hq, d)).astype(np.float32))
+    scale = np.float32(1.0 / math.sqrt(d))
+    want16, want = oracle.paged_decode(q, kc, vc, sc, tables, ctx, signs, gate, Hq, H, d, S, P,
+                                       K, scale, isl, stage, threads=8)
+    out = tq4.paged_decode(dev(q), dev(kc), dev(vc), dev(sc), dev(tables), dev(ctx), dev(signs),
+                           H, S, P, gate=dev(gate) if gate is not None else None, num_splits=K,
+                           scale=float(scale), inv_sqrt_len=float(isl), output_stage=stage)
+    return host(out), want, (q, kc, vc, sc, tables, ctx, signs, isl, scale)
+
+
+def check_out(got, want, label=""):
+    mx, mr = bf16_out_error(got, want)
+    assert np.all(np.isfinite(got.astype(np.float32))), f"{label}: non-finite output"
+    assert mx <= MAX_ABS and mr <= MEAN_REL, f"{label}: max-abs {mx:.3g} mean-rel {mr:.3g}"
+    return mx, mr
+
+
+def test_config3_single_sequence_ctx4096(tq4, oracle):
+    """batch 1, 32q:8kv, d 128, ctx 4096, page 16."""
+    rng = np.random.default_rng(0x71340003)
+    got, want, _ = run_decode(tq4, oracle, rng, [4096], 32, 8, 128, 16, 4096, 32)
+    check_out(got, want, "config3")
+
+
+@pytest.mark.parametrize("ctx", [4096, 16384, 4103])
+@pytest.mark.parametrize("K", [2, 4, 8, 16])
+def test_config4_split_sweep(tq4, oracle, ctx, K):
+    """split-K sweep incl. ragged ctx 4103 (NaN canaries in the tail)."""
+    rng = np.random.default_rng(0x71340004 + ctx + K)
+    got, want, _ = run_decode(tq4, oracle, rng, [ctx], 32, 8, 128, 16, (ctx + 15) // 16 + 8, K)
+    check_out(got, want, f"ctx {ctx} K {K}")
+
+
+def test_config4_ctx32768(tq4, oracle):
+    rng = np.random.default_rng(0x71340004)
+    got, want, _ = run_decode(tq4, oracle, rng, [32768], 32, 8, 128, 16, 2048 + 8, 16)
+    check_out(got, want, "ctx 32768")
+
+
+@pytest.mark.parametrize("G", [1, 4, 6, 16])
+@pytest.mark.parametrize("d", [64, 128, 256])
+def test_gqa_and_head_size(tq4, oracle, G, d):
+    rng = np.random.default_rng(G * 1000 + d)
+    H = 2
+    got, want, _ = run_decode(tq4, oracle, rng, [333, 77], G * H, H, d, 32, 40, 3)
+    check_out(got, want, f"G {G} d {d}")
+
+
+@pytest.mark.parametrize("stage", [0, 2])
+def test_output_stages(tq4, oracle, stage):
+    rng = np.random.default_rng(50 + stage)
+    gate = rng.standard_normal((2, 16, 128)).astype(np.float32) if stage == 2 else None
+    got, want, _ = run_decode(tq4, oracle, rng, [500, 1000], 16, 4, 128, 16, 120, 4, stage, gate)
+    check_out(got, want, f"stage {stage}")
+
+
+def test_single_split_and_empty_splits(tq4, oracle):
+    """K=1 finalises in-workgroup; K > pages leaves empty splits (neutral element)."""
+    rng = np.random.default_rng(99)
+    for K in (1, 40):
+        got, want, _ = run_decode(tq4, oracle, rng, [5, 200, 17], 8, 2, 128, 16, 40, K)
+        check_out(got, want, f"K {K}")
+
+
+def test_partials_match_oracle(tq4, oracle):
+    """Partial records (m, l, acc) per split, incl. exact neutral records."""
+    rng = np.random.default_rng(123)
+    H, Hq, d, S, P, K = 2, 8, 128, 16, 64, 8
+    ctx_lens = [100, 37]
+    kc, vc, sc, tables, signs, isl = build_cache(oracle, rng, ctx_lens, H, d, S, P)
+    ctx = np.array(ctx_lens, np.int32)
+    q = f32_to_bf16(rng.standard_normal((2, Hq, d)).astype(np.float32))
+    scale = np.float32(1.0 / math.sqrt(d))
+    want = oracle.decode_partials(q, kc, vc, sc, tables, ctx, signs, Hq, H, d, S, P, K, scale, isl)
+    ws = tq4.paged_decode_partials(dev(q), dev(kc), dev(vc), dev(sc), dev(tables), dev(ctx),
+                                   dev(signs), H, S, P, K, scale=float(scale),
+                                   inv_sqrt_len=float(isl))
+    got = host(ws)
+    m_g, l_g, a_g = got[..., 0], got[..., 1], got[..., 4:]
+    m_w, l_w, a_w = want[..., 0], want[..., 1], want[..., 4:]
+    empty = l_w == 0
+    assert np.all(m_g[empty] == np.float32(-3e38)) and np.all(l_g[empty] == 0)
+    assert np.all(a_g[empty] == 0)
+    live = ~empty
+    assert np.all(np.abs(m_g - m_w)[live] <= 1e-4 * np.maximum(1, np.abs(m_w[live])))
+    assert np.all(np.abs(l_g - l_w)[live] <= 2e-3 * np.maximum(1, l_w[live]))
+    amax = np.abs(a_w).max(axis=-1, keepdims=True)
+    tol = 2e-3 * amax + 1e-5 * l_w[..., None] + 1e-6
+    assert np.all(np.abs(a_g - a_w) <= tol)
+    # and the separate combine kernel agrees with the oracle's combine
+    out = tq4.splitk_combine(ws, dev(signs), 2, Hq, d, K, inv_sqrt_len=float(isl))
+    _, want_out = oracle.combine(want, signs, None, Hq, d, K, isl, 1)
+    check_out(host(out), want_out, "combine")
+
+
+def test_combine_uniform_closed_form(tq4, oracle):
+    """Uniform records (all m equal): the combine is an exact sum, acc/l = c + 1."""
+    K, d = 8, 128
+    recs = np.zeros((1, 2, K, d + 4), np.float32)
+    for k in range(K):
+        recs[:, :, k, 0] = -4.0
+        recs[:, :, k, 1] = 2.0 ** k
+        recs[:, :, k, 4:] = (2.0 ** k) * (np.arange(d) + 1)
+    out = tq4.splitk_combine(dev(recs), dev(oracle.canonical_signs(d)), 1, 2, d, K,
+                             output_stage=0)
+    got = host(out)
+    want = f32_to_bf16((np.arange(d) + 1).astype(np.float32))
+    assert np.array_equal(got[0, 0], want) and np.array_equal(got[0, 1], want)
+
+
+def test_fused_repeated_calls_reset_counters(tq4, oracle):
+    """The fused entry leaves its arrival counters at zero: calls in a row agree."""
+    rng = np.random.default_rng(5)
+    _, want, args = run_decode(tq4, oracle, rng, [700, 300], 16, 4, 128, 16, 80, 6)
+    q, kc, vc, sc, tables, ctx, signs, isl, scale = args
+    ws = tq4.decode_workspace(2, 16, 4, 128, 6)
+    outs = []
+    for _ in range(3):
+        out = tq4.paged_decode(dev(q), dev(kc), dev(vc), dev(sc), dev(tables), dev(ctx),
+                               dev(signs), 4, 16, 80, workspace=ws, num_splits=6,
+                               scale=float(scale), inv_sqrt_len=float(isl))
+        outs.append(host(out))
+    for o in outs:
+        check_out(o, want, "repeat")
+        assert np.array_equal(o, outs[0])
