@@ -149,6 +149,9 @@ uint32_t tq4_decode_auto_splits(uint32_t num_seqs, uint32_t num_kv_heads,
     if (k > by_len) k = by_len;
     if (k > TQ4_MAX_SPLITS) k = TQ4_MAX_SPLITS;
     if (k < 1) k = 1;
+    // one split stages at most TQ4_MAX_SPLIT_PAGES block-table entries
+    const uint64_t k_min = ((uint64_t)max_blocks_per_seq + TQ4_MAX_SPLIT_PAGES - 1) / TQ4_MAX_SPLIT_PAGES;
+    if (k < k_min) k = k_min;
     return (uint32_t)k;
 }
 
@@ -174,6 +177,11 @@ int decode_checks(const uint16_t* q, const int8_t* kc, const int8_t* vc, const f
     if (!q || !kc || !vc || !sc || !tables || !ctx) return TQ4_ERR_NULL_POINTER;
     if (!(flags & TQ4_DECODE_QUERY_ROTATED) && !pi_signs) return TQ4_ERR_ROTATION;
     return TQ4_OK;
+}
+
+bool split_pages_ok(uint32_t max_blocks_per_seq, uint32_t num_splits)
+{
+    return ((uint64_t)max_blocks_per_seq + num_splits - 1) / num_splits <= TQ4_MAX_SPLIT_PAGES;
 }
 
 tq4::DecodeParams make_params(const uint16_t* q, const int8_t* kc, const int8_t* vc,
@@ -230,7 +238,8 @@ int tq4_paged_decode(void* stream, const uint16_t* q, const int8_t* key_cache,
     if (output_stage >= 1 && !pi_signs) return TQ4_ERR_ROTATION;
     if (num_splits == 0)
         num_splits = tq4_decode_auto_splits(num_seqs, num_kv_heads, max_blocks_per_seq, block_size);
-    if (num_splits > TQ4_MAX_SPLITS) return TQ4_ERR_SPLITS;
+    if (num_splits > TQ4_MAX_SPLITS || !split_pages_ok(max_blocks_per_seq, num_splits))
+        return TQ4_ERR_SPLITS;
     if ((uint64_t)num_seqs * num_kv_heads * num_splits > 0x7fffffffull) return TQ4_ERR_RANGE;
     tq4::DecodeParams p = make_params(q, key_cache, value_cache, scale_cache, block_tables,
                                       context_lens, pi_signs, gate, num_seqs, num_heads,
@@ -265,7 +274,9 @@ int tq4_paged_decode_partials(void* stream, const uint16_t* q, const int8_t* key
                            pi_signs, num_seqs, num_heads, num_kv_heads, head_size, block_size,
                            num_blocks, max_blocks_per_seq, flags);
     if (rc != TQ4_OK) return rc;
-    if (num_splits == 0 || num_splits > TQ4_MAX_SPLITS) return TQ4_ERR_SPLITS;
+    if (num_splits == 0 || num_splits > TQ4_MAX_SPLITS ||
+        !split_pages_ok(max_blocks_per_seq, num_splits))
+        return TQ4_ERR_SPLITS;
     if ((uint64_t)num_seqs * num_kv_heads * num_splits > 0x7fffffffull) return TQ4_ERR_RANGE;
     if (!workspace ||
         workspace_bytes < tq4::decode_records_bytes(num_seqs, num_heads, head_size, num_splits))

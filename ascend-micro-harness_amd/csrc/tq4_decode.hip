@@ -105,38 +105,136 @@ __device__ __forceinline__ void load_strip(StripRegs<D>& r, const int8_t* kb, co
     r.vs = *(const f4_t*)(vsp + 4 * kg);
 }
 
-// LDS layout (floats): [0, 2*G*D) two exchange slots, aliased by the q
-// staging area and by the in-LDS record of a single-split fused launch;
-// then m[4][16], l[4][16], q exponents[16], one flag word.
-__host__ __device__ constexpr size_t lds_floats(uint32_t G, uint32_t D)
+
+// LDS layout (floats). A fixed header -- m[4][16], l[4][16], q exponents[16],
+// the last-arrival flag, the combine's per-row M and L[16+16] -- then one big
+// region reused in turn by the q staging area [G][D], the wave-merge slots
+// [2][G][D], and the combine's weights [G][K] + normalised rows [G][D].
+constexpr int kMaxWindowPages = 1024;  // block-table entries one split may own
+constexpr int kHdrFloats = 2 * kWaves * 16 + 16 + 4 + 32 + 12 + kMaxWindowPages;
+
+__host__ __device__ constexpr size_t region_floats(uint32_t G, uint32_t D, uint32_t K)
 {
-    return 2ull * G * D + 2ull * kWaves * 16 + 16 + 4;
+    const size_t merge = 2ull * G * D;
+    const size_t comb = 2ull * G * K + (size_t)G * D;
+    return merge > comb ? merge : comb;
 }
 
-// LSE-combine K records of one (seq, q head) row (first record at `rec`,
-// stride D+4 floats), normalise, optionally rotate back and gate, store BF16.
-// One wave; lane holds CPL = D/64 consecutive channels.
+// Workgroup barrier for LDS traffic only: unlike __syncthreads() it does not
+// wait for outstanding global loads (vmcnt), so prefetched strips stay in
+// flight across it.
+__device__ __forceinline__ void lds_barrier()
+{
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+__device__ __forceinline__ float wave_max(float v)
+{
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) v = fmaxf(v, xor_lanes(v, m));
+    return v;
+}
+
+// LSE-combine `nrows` rows of K partial records each (row r, split k at
+// rec + r*row_stride + k*(D+4)) with all 256 threads, leaving the normalised
+// rows acc / L (0 when L == 0) in out[r*D + c]. The (m, l) pairs load in one
+// parallel pass; each thread then sums its channel pairs over the splits with
+// 16 independent record loads in flight.
+// Record traffic between workgroups of one launch: agent-scope atomic
+// (device-coherent, sc1) stores and loads, so no whole-L2 write-back or
+// invalidate is needed around the arrival counter.
+__device__ __forceinline__ void store_coherent(float* p, float v)
+{
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <bool COHERENT>
+__device__ __forceinline__ float load_rec(const float* p)
+{
+    if constexpr (COHERENT)
+        return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return *p;
+}
+
+template <int D, bool COHERENT>
+__device__ void combine_rows(const float* rec, size_t row_stride, uint32_t nrows, uint32_t K,
+                             float* w, float* lk, float* ML, float* out)
+{
+    constexpr int RS = D + 4;
+    constexpr int CH = 16;
+    const int tid = threadIdx.x;
+    const uint32_t nk = nrows * K;
+    for (uint32_t t = tid; t < nk; t += kThreads) {
+        const float* rr = rec + (t / K) * row_stride + (size_t)(t % K) * RS;
+        w[t] = load_rec<COHERENT>(rr);
+        lk[t] = load_rec<COHERENT>(rr + 1);
+    }
+    __syncthreads();
+    if ((uint32_t)tid < nrows) {
+        float M = kMasked;
+        for (uint32_t k = 0; k < K; ++k) M = fmaxf(M, w[tid * K + k]);
+        ML[tid] = M;
+    }
+    __syncthreads();
+    for (uint32_t t = tid; t < nk; t += kThreads) {
+        const float e = expf(w[t] - ML[t / K]);
+        w[t] = e;
+        lk[t] *= e;
+    }
+    __syncthreads();
+    if ((uint32_t)tid < nrows) {
+        float L = 0.0f;
+        for (uint32_t k = 0; k < K; ++k) L += lk[tid * K + k];
+        ML[16 + tid] = L;
+    }
+    const uint32_t npairs = nrows * (D / 2);
+    for (uint32_t pi = tid; pi < npairs; pi += kThreads) {
+        const uint32_t r = pi / (D / 2), c = 2 * (pi % (D / 2));
+        const float* rr = rec + r * row_stride + 4 + c;
+        const float* wr = w + r * K;
+        float a0 = 0.0f, a1 = 0.0f;
+        for (uint32_t k0 = 0; k0 < K; k0 += CH) {
+            float2 v[CH];
+#pragma unroll
+            for (int i = 0; i < CH; ++i) {
+                if (k0 + i < K) {
+                    const float* at = rr + (size_t)(k0 + i) * RS;
+                    if constexpr (COHERENT)
+                        v[i] = make_float2(load_rec<true>(at), load_rec<true>(at + 1));
+                    else
+                        v[i] = *(const float2*)at;
+                } else {
+                    v[i] = make_float2(0.0f, 0.0f);
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < CH; ++i) {
+                const float wk = k0 + i < K ? wr[k0 + i] : 0.0f;
+                a0 += v[i].x * wk;
+                a1 += v[i].y * wk;
+            }
+        }
+        out[r * D + c] = a0;
+        out[r * D + c + 1] = a1;
+    }
+    __syncthreads();
+    for (uint32_t e = tid; e < nrows * D; e += kThreads) {
+        const float L = ML[16 + e / D];
+        out[e] = L == 0.0f ? 0.0f : out[e] / L;
+    }
+    __syncthreads();
+}
+
+// Egress of one normalised row (in LDS) by one wave: optionally Pi^T and
+// 1/sqrt(d), optionally the gate, BF16 RNE store.
 template <int D>
-__device__ void finish_row(const float* rec, uint32_t K, const float* pi_signs, const float* gate,
+__device__ void egress_row(const float* row, const float* pi_signs, const float* gate,
                            uint16_t* out, float inv_sqrt_len, uint32_t stage, int lane)
 {
     constexpr int CPL = D / 64;
-    constexpr int RS = D + 4;
-    float M = kMasked;
-    for (uint32_t k = 0; k < K; ++k) M = fmaxf(M, rec[(size_t)k * RS]);
-    float L = 0.0f, acc[CPL];
-#pragma unroll
-    for (int j = 0; j < CPL; ++j) acc[j] = 0.0f;
-    for (uint32_t k = 0; k < K; ++k) {
-        const float* r = rec + (size_t)k * RS;
-        const float w = expf(r[0] - M);
-        L += r[1] * w;
-#pragma unroll
-        for (int j = 0; j < CPL; ++j) acc[j] += r[4 + lane * CPL + j] * w;
-    }
     float v[CPL];
 #pragma unroll
-    for (int j = 0; j < CPL; ++j) v[j] = L == 0.0f ? 0.0f : acc[j] / L;
+    for (int j = 0; j < CPL; ++j) v[j] = row[lane * CPL + j];
     if (stage >= 1) {
         float sg[CPL];
 #pragma unroll
@@ -163,10 +261,13 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p)
     extern __shared__ float smem[];
 
     const uint32_t G = p.G, S = p.S;
-    float* m_x = smem + 2 * (size_t)G * D;
+    float* m_x = smem;
     float* l_x = m_x + kWaves * 16;
     int* q_exp = (int*)(l_x + kWaves * 16);
     int* flag = q_exp + 16;
+    float* ML = (float*)(flag + 4);
+    int32_t* page_lds = (int32_t*)(smem + 192);
+    float* region = smem + kHdrFloats;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int n = lane & 15, kg = lane >> 4;
@@ -175,33 +276,86 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p)
     const uint32_t kvh = (item / p.K) % p.Hkv;
     const uint32_t seq = item / (p.K * p.Hkv);
 
-    int32_t ctx_raw = p.context_lens[seq];
+    // ---- phase 0: every small load -- context length, q rows, rotation
+    // signs, the split's block-table window -- is issued before any strip
+    // load: vmcnt retires in order, so a later wait for one of these would
+    // otherwise also wait for the strip stream.
+    const int32_t ctx_raw = p.context_lens[seq];
+    const bool rotate = !(p.flags & kFlagRotated);
+    uint16_t qraw[4][CPL];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t g = min((uint32_t)wave + kWaves * i, G - 1);  // branch-free
+        const uint16_t* qr = p.q + ((size_t)seq * p.Hq + kvh * G + g) * D + lane * CPL;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) qraw[i][j] = qr[j];
+    }
+    float sg[CPL];
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) sg[j] = 1.0f;
+    if (rotate) {
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) sg[j] = p.pi_signs[lane * CPL + j];
+    }
+    // The split's window of the block table: the reference AIC decode's
+    // Partition(page_count, splits, split) over the table's max_blocks_per_seq
+    // pages (turboquant_paged_decode_attention.cpp:1598-1624), staged in LDS
+    // so the strip loop reads page ids without touching vmcnt.
+    uint32_t pb, pc;
+    partition(p.max_blocks, p.K, split, pb, pc);
+    const uint32_t spp = S / kStrip;
+    const uint32_t n_window = pc * spp;
+    const uint32_t n_win_mine =
+        n_window > (uint32_t)wave ? (n_window - wave + kWaves - 1) / kWaves : 0u;
+    const int32_t* tbl = p.block_tables + (size_t)seq * p.max_blocks;
+    for (uint32_t t = tid; t < pc; t += kThreads) page_lds[t] = tbl[pb + t];
+    // Unconditional vmcnt(0) (expcnt and lgkmcnt left at their maxima): the
+    // loads above are all complete from here on every path, so the compiler's
+    // wait analysis never again waits on them -- or on what is queued after.
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    lds_barrier();
+    const size_t plane_floats = (size_t)p.P * p.Hkv * S;
+
+    // Operands of this wave's j-th strip; false when its page is out of range
+    // (table entries past the live context may hold anything).
+    auto fetch = [&](uint32_t j, StripRegs<D>& r) -> bool {
+        const uint32_t idx = wave + kWaves * j;
+        const uint32_t phys = (uint32_t)__builtin_amdgcn_readfirstlane(page_lds[idx / spp]);
+        if (phys >= p.P) return false;
+        const size_t row = ((size_t)phys * p.Hkv + kvh) * S + (size_t)(idx % spp) * kStrip;
+        load_strip<D>(r, p.key_cache + row * (D / 2), p.value_cache + row * (D / 2),
+                      p.scale_cache + row, p.scale_cache + row + plane_floats, n, kg);
+        return true;
+    };
+    StripRegs<D> buf0, buf1, buf2;
+    bool ok0 = n_win_mine > 0 ? fetch(0, buf0) : false;
+    bool ok1 = n_win_mine > 1 ? fetch(1, buf1) : false;
+    bool ok2 = false;
+
+    // Live strips of the window: tokens at or past ctx are masked, strips with
+    // none live are not walked (turboquant_decode_tail.hpp:246-272).
     uint32_t ctx = ctx_raw < 0 ? 0u : (uint32_t)ctx_raw;
     const uint64_t capacity = (uint64_t)p.max_blocks * S;
     if (ctx > capacity) ctx = (uint32_t)capacity;
-    const uint32_t pages = (ctx + S - 1) / S;
-    uint32_t pb, pc;
-    partition(pages, p.K, split, pb, pc);
-    const uint32_t spp = S / kStrip;
     const uint64_t tok0 = (uint64_t)pb * S;
     uint32_t live = 0;
     if (pc > 0 && ctx > tok0) {
         const uint64_t need = (ctx - tok0 + kStrip - 1) / kStrip;
-        live = need < (uint64_t)pc * spp ? (uint32_t)need : pc * spp;
+        live = need < (uint64_t)n_window ? (uint32_t)need : n_window;
     }
+    const uint32_t n_mine = live > (uint32_t)wave ? (live - wave + kWaves - 1) / kWaves : 0u;
 
-    // ---- q prologue: rotate (Pi = M * inv_sqrt_len), fold the softmax
-    // scale, normalise each row by a power of two, stage in LDS.
-    float* q_st = smem;
-    for (uint32_t g = wave; g < G; g += kWaves) {
-        const uint16_t* qr = p.q + ((size_t)seq * p.Hq + kvh * G + g) * D + lane * CPL;
+    // ---- phase 2 (overlaps the strip loads): rotate q (Pi = M * inv_sqrt_len),
+    // fold the softmax scale, normalise each row by a power of two, stage in LDS.
+    float* q_st = region;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t g = wave + kWaves * i;
+        if (g >= G) continue;
         float v[CPL];
 #pragma unroll
-        for (int j = 0; j < CPL; ++j) v[j] = bf16_to_f32(qr[j]);
-        if (!(p.flags & kFlagRotated)) {
-            float sg[CPL];
-#pragma unroll
-            for (int j = 0; j < CPL; ++j) sg[j] = p.pi_signs[lane * CPL + j];
+        for (int j = 0; j < CPL; ++j) v[j] = bf16_to_f32(qraw[i][j]);
+        if (rotate) {
             rotate_ingress<D, CPL>(v, sg, lane);
 #pragma unroll
             for (int j = 0; j < CPL; ++j) v[j] = (v[j] * p.inv_sqrt_len) * p.scale;
@@ -212,14 +366,13 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p)
         float a = 0.0f;
 #pragma unroll
         for (int j = 0; j < CPL; ++j) a = fmaxf(a, fabsf(v[j]));
-#pragma unroll
-        for (int m = 1; m < 64; m <<= 1) a = fmaxf(a, xor_lanes(a, m));
+        a = wave_max(a);
         const int kq = a > 0.0f ? exponent_of(a) : 0;
 #pragma unroll
         for (int j = 0; j < CPL; ++j) q_st[g * D + lane * CPL + j] = ldexpf(v[j], -kq);
         if (lane == 0) q_exp[g] = kq;
     }
-    __syncthreads();
+    lds_barrier();
 
     // ---- this lane's B operand (q head n, channel group kg) and constants.
     u2_t qop[NB];
@@ -245,46 +398,18 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p)
     bias += xor_lanes(bias, 16);
     bias += xor_lanes(bias, 32);
     bias *= -1.5f;
-    __syncthreads();  // q staging is dead from here; its LDS is reused below
+    // No barrier here: q_st is next overwritten after the merge barrier,
+    // which every wave reaches only after building its operands.
 
-    // ---- stream the strips.
+    // ---- stream this wave's strips (register double buffer).
     f4_t acc[NB];
 #pragma unroll
     for (int b = 0; b < NB; ++b) acc[b] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
     float m2 = kMasked, lpart = 0.0f;
     int E = 0;  // running max exponent field of the live value scales
-    const int32_t* tbl = p.block_tables + (size_t)seq * p.max_blocks;
-    const size_t plane_floats = (size_t)p.P * p.Hkv * S;
 
-    auto strip_ptrs = [&](uint32_t idx, const int8_t*& kb, const int8_t*& vb, const float*& ksp,
-                          const float*& vsp) -> bool {
-        const uint32_t lp = pb + idx / spp, sip = idx % spp;
-        const uint32_t phys = (uint32_t)tbl[lp];
-        const size_t row = ((size_t)phys * p.Hkv + kvh) * S + (size_t)sip * kStrip;
-        kb = p.key_cache + row * (D / 2);
-        vb = p.value_cache + row * (D / 2);
-        ksp = p.scale_cache + row;
-        vsp = ksp + plane_floats;
-        return phys < p.P;
-    };
-
-    StripRegs<D> cur, nxt;
-    bool cur_ok = false;
-    if ((uint32_t)wave < live) {
-        const int8_t *kb, *vb;
-        const float *ksp, *vsp;
-        cur_ok = strip_ptrs(wave, kb, vb, ksp, vsp);
-        if (cur_ok) load_strip<D>(cur, kb, vb, ksp, vsp, n, kg);
-    }
-    for (uint32_t idx = wave; idx < live; idx += kWaves) {
-        bool nxt_ok = false;
-        if (idx + kWaves < live) {
-            const int8_t *kb, *vb;
-            const float *ksp, *vsp;
-            nxt_ok = strip_ptrs(idx + kWaves, kb, vb, ksp, vsp);
-            if (nxt_ok) load_strip<D>(nxt, kb, vb, ksp, vsp, n, kg);
-        }
-        if (cur_ok) {
+    auto process = [&](const StripRegs<D>& cur, uint32_t j) {
+            const uint32_t idx = wave + kWaves * j;
             // Scores: C[token][q] = sum_c (1 + u/16) q16 - 1.5 sum q16 = sum q16 n / 16.
             f4_t sc = f4_t{bias, bias, bias, bias};
 #pragma unroll
@@ -352,19 +477,27 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p)
             }
             m2 = mn;
             E = En;
-        }
-        cur = nxt;
-        cur_ok = nxt_ok;
+            };
+    // 3-deep ring: strip j computes while strips j+1 and j+2 are in flight.
+    for (uint32_t j = 0; j < n_mine; j += 3) {
+        ok2 = j + 2 < n_mine ? fetch(j + 2, buf2) : false;
+        if (ok0) process(buf0, j);
+        if (j + 1 >= n_mine) break;
+        ok0 = j + 3 < n_mine ? fetch(j + 3, buf0) : false;
+        if (ok1) process(buf1, j + 1);
+        if (j + 2 >= n_mine) break;
+        ok1 = j + 4 < n_mine ? fetch(j + 4, buf1) : false;
+        if (ok2) process(buf2, j + 2);
     }
 
-    // ---- merge the four waves.
+    // ---- merge the four waves: common reference M per row, then sum.
     lpart += xor_lanes(lpart, 16);
     lpart += xor_lanes(lpart, 32);
     if (kg == 0) {
         m_x[wave * 16 + n] = m2;
         l_x[wave * 16 + n] = lpart;
     }
-    __syncthreads();
+    lds_barrier();
     const float unit = ldexpf(16.0f, E - 127);
     float Mrow[4], Lrow[4];
 #pragma unroll
@@ -382,8 +515,8 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p)
         Mrow[i] = M;
         Lrow[i] = L;
     }
-    float* slot0 = smem;
-    float* slot1 = smem + (size_t)G * D;
+    float* slot0 = region;
+    float* slot1 = region + (size_t)G * D;
     auto put = [&](float* slot) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -405,46 +538,67 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p)
         }
     };
     if (wave >= 2) put(wave == 2 ? slot0 : slot1);
-    __syncthreads();
+    lds_barrier();
     if (wave < 2) add(wave == 0 ? slot0 : slot1);
-    __syncthreads();
+    lds_barrier();
     if (wave == 1) put(slot0);
-    __syncthreads();
+    lds_barrier();
+    if (wave == 0) add(slot0);
 
-    // ---- wave 0 owns the workgroup's result: export one record per q head.
-    const bool fused_local = (MODE == 1) && p.K == 1;
-    float* rec_base = fused_local
-                          ? smem
-                          : p.records + (((size_t)seq * p.Hq + (size_t)kvh * G) * p.K + split) * RS;
-    const size_t row_stride = fused_local ? (size_t)RS : (size_t)p.K * RS;
-    if (wave == 0) {
-        add(slot0);
+    const bool local = (MODE == 1) && p.K == 1;
+    if (!local) {
+        // ---- export one record per q head: [m (natural log), l, 0, 0, acc].
+        float* rec_base = p.records + (((size_t)seq * p.Hq + (size_t)kvh * G) * p.K + split) * RS;
+        if (wave == 0) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t r = 4 * kg + i;
-            if (r < G) {
-                float* rec = rec_base + r * row_stride;
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t r = 4 * kg + i;
+                if (r < G) {
+                    float* rec = rec_base + (size_t)r * p.K * RS;
+                    auto put_rec = [&](int at, float v) {
+                        if constexpr (MODE == 1) store_coherent(rec + at, v);
+                        else rec[at] = v;
+                    };
 #pragma unroll
-                for (int b = 0; b < NB; ++b) rec[4 + 16 * b + n] = acc[b][i];
-                if (n == 0) {
-                    rec[0] = Mrow[i] == kMasked ? kMasked : Mrow[i] * kLn2;
-                    rec[1] = Lrow[i];
-                    rec[2] = 0.0f;
-                    rec[3] = 0.0f;
+                    for (int b = 0; b < NB; ++b) put_rec(4 + 16 * b + n, acc[b][i]);
+                    if (n == 0) {
+                        put_rec(0, Mrow[i] == kMasked ? kMasked : Mrow[i] * kLn2);
+                        put_rec(1, Lrow[i]);
+                        put_rec(2, 0.0f);
+                        put_rec(3, 0.0f);
+                    }
                 }
             }
         }
     }
     if constexpr (MODE == 0) return;
 
-    // ---- fused: the last workgroup of this (seq, kv head) combines.
-    uint32_t K_rows = 1;
-    if (!fused_local) {
-        __threadfence();
+    float* rows = region;  // normalised rows [G][D] for the egress
+    if (local) {
+        lds_barrier();  // wave 0 finished reading slot0
+        if (wave == 0) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t r = 4 * kg + i;
+                if (r < G) {
+                    const float L = Lrow[i];
+#pragma unroll
+                    for (int b = 0; b < NB; ++b)
+                        rows[r * D + 16 * b + n] = L == 0.0f ? 0.0f : acc[b][i] / L;
+                }
+            }
+        }
+        lds_barrier();
+    } else {
+        // ---- the last workgroup of this (seq, kv head) to arrive combines.
+        // The records went out as device-coherent stores; waiting for their
+        // completion before the increment publishes them (release), and the
+        // last arriver reads them with device-coherent loads (acquire).
+        __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
         if (tid == 0) {
             uint32_t* ctr = p.counters + (size_t)seq * p.Hkv + kvh;
-            const uint32_t old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_ACQ_REL,
+            const uint32_t old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED,
                                                         __HIP_MEMORY_SCOPE_AGENT);
             const int last = old == p.K - 1;
             if (last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -452,29 +606,39 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p)
         }
         __syncthreads();
         if (!*flag) return;
-        __threadfence();
-        rec_base = p.records + ((size_t)seq * p.Hq + (size_t)kvh * G) * p.K * RS;
-        K_rows = p.K;
-    } else {
-        __syncthreads();
+        float* w = region;
+        float* lk = region + (size_t)G * p.K;
+        rows = lk + (size_t)G * p.K;
+        combine_rows<D, true>(p.records + ((size_t)seq * p.Hq + (size_t)kvh * G) * p.K * RS,
+                        (size_t)p.K * RS, G, p.K, w, lk, ML, rows);
     }
     for (uint32_t g = wave; g < G; g += kWaves) {
         const size_t qh = (size_t)seq * p.Hq + kvh * G + g;
-        finish_row<D>(rec_base + g * row_stride, K_rows, p.pi_signs,
-                      p.gate ? p.gate + qh * D : nullptr, p.out + qh * D, p.inv_sqrt_len,
-                      p.output_stage, lane);
+        egress_row<D>(rows + g * D, p.pi_signs, p.gate ? p.gate + qh * D : nullptr,
+                      p.out + qh * D, p.inv_sqrt_len, p.output_stage, lane);
     }
 }
 
+// Stand-alone combine: 16 consecutive (seq, q head) rows per workgroup.
 template <int D>
 __global__ __launch_bounds__(kThreads) void combine_kernel(DecodeParams p)
 {
+    extern __shared__ float smem[];
+    const size_t total = (size_t)p.B * p.Hq;
+    const size_t row0 = (size_t)blockIdx.x * 16;
+    const uint32_t nrows = (uint32_t)((total - row0) < 16 ? (total - row0) : 16);
+    float* ML = smem;
+    float* w = smem + 32;
+    float* lk = w + (size_t)16 * p.K;
+    float* rows = lk + (size_t)16 * p.K;
+    combine_rows<D, false>(p.records + row0 * p.K * (D + 4), (size_t)p.K * (D + 4), nrows, p.K, w, lk,
+                    ML, rows);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const size_t row = (size_t)blockIdx.x * kWaves + wave;  // seq * Hq + q head
-    if (row >= (size_t)p.B * p.Hq) return;
-    finish_row<D>(p.records + row * p.K * (D + 4), p.K, p.pi_signs,
-                  p.gate ? p.gate + row * D : nullptr, p.out + row * D, p.inv_sqrt_len,
-                  p.output_stage, lane);
+    for (uint32_t r = wave; r < nrows; r += kWaves) {
+        const size_t row = row0 + r;
+        egress_row<D>(rows + r * D, p.pi_signs, p.gate ? p.gate + row * D : nullptr,
+                      p.out + row * D, p.inv_sqrt_len, p.output_stage, lane);
+    }
 }
 
 __global__ void fill_zero_kernel(uint32_t* ptr, size_t words)
@@ -488,13 +652,24 @@ template <int D>
 hipError_t launch_decode_t(hipStream_t stream, const DecodeParams& p, int mode)
 {
     const size_t blocks = (size_t)p.B * p.Hkv * p.K;
-    const size_t lds = lds_floats(p.G, D) * sizeof(float);
+    const uint32_t comb_k = (mode == 1 && p.K > 1) ? p.K : 0u;
+    const size_t lds = (kHdrFloats + region_floats(p.G, D, comb_k)) * sizeof(float);
     if (mode == 0)
         hipLaunchKernelGGL((decode_kernel<D, 0>), dim3((uint32_t)blocks), dim3(kThreads), lds,
                            stream, p);
     else
         hipLaunchKernelGGL((decode_kernel<D, 1>), dim3((uint32_t)blocks), dim3(kThreads), lds,
                            stream, p);
+    return hipGetLastError();
+}
+
+template <int D>
+hipError_t launch_combine_t(hipStream_t stream, const DecodeParams& p)
+{
+    const size_t rows = (size_t)p.B * p.Hq;
+    const uint32_t blocks = (uint32_t)((rows + 15) / 16);
+    const size_t lds = (32 + (size_t)32 * p.K + (size_t)16 * D) * sizeof(float);
+    hipLaunchKernelGGL((combine_kernel<D>), dim3(blocks), dim3(kThreads), lds, stream, p);
     return hipGetLastError();
 }
 
@@ -518,21 +693,12 @@ hipError_t launch_decode(hipStream_t stream, const DecodeParams& p, int mode)
 
 hipError_t launch_combine(hipStream_t stream, const DecodeParams& p)
 {
-    const size_t rows = (size_t)p.B * p.Hq;
-    const uint32_t blocks = (uint32_t)((rows + kWaves - 1) / kWaves);
     switch (p.D) {
-        case 64:
-            hipLaunchKernelGGL((combine_kernel<64>), dim3(blocks), dim3(kThreads), 0, stream, p);
-            break;
-        case 128:
-            hipLaunchKernelGGL((combine_kernel<128>), dim3(blocks), dim3(kThreads), 0, stream, p);
-            break;
-        case 256:
-            hipLaunchKernelGGL((combine_kernel<256>), dim3(blocks), dim3(kThreads), 0, stream, p);
-            break;
+        case 64: return launch_combine_t<64>(stream, p);
+        case 128: return launch_combine_t<128>(stream, p);
+        case 256: return launch_combine_t<256>(stream, p);
         default: return hipErrorInvalidValue;
     }
-    return hipGetLastError();
 }
 
 hipError_t launch_fill_zero(hipStream_t stream, void* ptr, size_t bytes)

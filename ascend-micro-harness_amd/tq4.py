@@ -60,9 +60,9 @@ def lib():
     L.tq4_status_string.argtypes = [_I32]
     L.tq4_version.restype = _U32
     L.tq4_reshape_and_cache_a8.restype = _I32
-    L.tq4_reshape_and_cache_a8.argtypes = [_P] * 10 + [_U32] * 6 + [_F32, C.c_bool]
+    L.tq4_reshape_and_cache_a8.argtypes = [_P] * 9 + [_U32] * 6 + [_F32, C.c_bool]
     L.tq4_reshape_and_cache_bf16.restype = _I32
-    L.tq4_reshape_and_cache_bf16.argtypes = [_P] * 10 + [_U32] * 6 + [_F32, C.c_bool]
+    L.tq4_reshape_and_cache_bf16.argtypes = [_P] * 9 + [_U32] * 6 + [_F32, C.c_bool]
     L.tq4_reshape_scatter.restype = _I32
     L.tq4_reshape_scatter.argtypes = [_P, _U32] + [_P] * 9 + [_U32] * 7 + [_F32]
     L.tq4_decode_workspace_bytes.restype = _SZ

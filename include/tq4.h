@@ -127,9 +127,11 @@ int tq4_reshape_scatter(void* stream, uint32_t block_dim, const uint16_t* key,
  * physical pages; context_lens: [num_seqs] live tokens (<= max_blocks_per_seq
  * * block_size). Scores are scale * (Pi q) . k_deq with Pi = M *
  * inv_sqrt_len; tokens at or past context_len are masked by overwrite.
- * Split k of num_splits owns logical pages Partition(ceil(ctx/S), K, k)
- * (include/turboquant_splitk_contract.hpp:123-130); an empty split exports
- * the neutral record m = -3e38, l = 0, acc = 0.
+ * Split k of num_splits owns logical pages Partition(max_blocks_per_seq, K, k)
+ * of the block-table window (include/turboquant_splitk_contract.hpp:123-130,
+ * as the reference AIC decode partitions its page window); a split with no
+ * live token exports the neutral record m = -3e38, l = 0, acc = 0. Block-table
+ * entries >= num_blocks contribute nothing (they are never dereferenced).
  * output_stage: 0 = normalised context in the rotated basis, 1 = rotated back
  * (Pi^T), 2 = rotated back and divided by 1 + exp(-gate), gate [num_seqs]
  * [num_heads][head_size] FP32. out: [num_seqs][num_heads][head_size] BF16 RNE.
@@ -137,6 +139,9 @@ int tq4_reshape_scatter(void* stream, uint32_t block_dim, const uint16_t* key,
  */
 #define TQ4_DECODE_QUERY_ROTATED 1u
 #define TQ4_MAX_SPLITS 256u
+/* A split owns at most this many block-table pages: num_splits must be at
+ * least ceil(max_blocks_per_seq / TQ4_MAX_SPLIT_PAGES) (TQ4_ERR_SPLITS). */
+#define TQ4_MAX_SPLIT_PAGES 1024u
 
 /* Workspace bytes for num_splits (partial records plus the per-(seq, kv
  * head) arrival counters of the fused entry). */

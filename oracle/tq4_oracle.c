@@ -507,7 +507,7 @@ typedef struct {
 } DecodeJob;
 
 /* One (seq, kv head, split) task: every q head of the group walks the
- * split's strips in order with the online-softmax recurrence of
+ * split's live strips in order with the online-softmax recurrence of
  * single_token_decode_oracle.hpp:257-310 (scores, tile max, alpha, p, value
  * scale folded into p, l and acc updates), tail masking by overwrite
  * (turboquant_decode_tail.hpp:56-72), fully dead strips skipped, and the
@@ -522,9 +522,12 @@ static void decode_item(const DecodeJob* j, uint32_t item)
     const uint32_t d = j->d, S = j->S;
     const uint32_t rec = tq4o_record_floats(d);
     const uint32_t ctx = (uint32_t)j->context_lens[seq];
-    const uint32_t pages = (ctx + S - 1) / S;
+    /* The split partitions the block-table window of max_blocks pages, as the
+     * reference AIC decode partitions its page window
+     * (turboquant_paged_decode_attention.cpp:1598-1624); pages past ctx hold
+     * no live strip and are skipped, so such splits stay neutral. */
     uint32_t pbegin, pcount;
-    tq4o_partition(pages, j->splits, split, &pbegin, &pcount);
+    tq4o_partition(j->max_blocks, j->splits, split, &pbegin, &pcount);
 
     for (uint32_t g = 0; g < G; ++g) {
         const uint32_t qh = kvh * G + g;

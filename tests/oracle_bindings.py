@@ -87,7 +87,7 @@ class Oracle:
         L.tq4o_rotate_query.argtypes = [P, P, U32, F32, F32, P]
         L.tq4o_combine_step.argtypes = [P, P, P, F32, F32, P, U32]
         L.tq4o_decode_partials.restype = I32
-        L.tq4o_decode_partials.argtypes = [P] * 8 + [U32] * 9 + [F32, F32, U32]
+        L.tq4o_decode_partials.argtypes = [P] * 8 + [U32] * 8 + [F32, F32, U32]
         L.tq4o_combine.restype = I32
         L.tq4o_combine.argtypes = [P, P, P, P, P, U32, U32, U32, U32, F32, U32]
         L.tq4o_paged_decode.restype = I32

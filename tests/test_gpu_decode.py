@@ -3,11 +3,14 @@
 Tolerances (BF16 output, the north_star's): max-abs <= 2e-2 and mean-rel <=
 1e-3 against the FP32 oracle rounded to BF16 (the same final rounding the
 device applies); also reported against the FP64 reference. Partial records
-are checked with the reference rig's budgets
-(tests/npu/turboquant_splitk_rigs.hpp:144-158): m 2e-6*max(1,|m|),
-l 1e-4*max(1,l), acc 2e-4*max|acc| + 1e-5*l + 1e-6 -- relaxed here by the
-fp16 MFMA operands (see DECODE_* below) -- and the empty-split neutral
-element exactly.
+are checked against the oracle's FP32 records with budgets 1e-3*max(1,|m|)
+for m, 2e-3*max(1,l) for l and 2e-3*max|acc| + 1e-5*l + 1e-6 for acc, and
+the empty-split neutral element exactly. The reference rig's budgets
+(tests/npu/turboquant_splitk_rigs.hpp:144-158: m 2e-6, l 1e-4, acc 2e-4)
+assume its exact BF16 score panel; this kernel feeds the MFMA the rotated
+query in fp16 (11-bit significand, finer than the reference device's BF16
+q_rot, 8 bits), so a score carries a relative error up to ~2^-11 and m
+moves by that much.
 """
 import math
 
@@ -152,7 +155,7 @@ def test_partials_match_oracle(tq4, oracle):
     assert np.all(m_g[empty] == np.float32(-3e38)) and np.all(l_g[empty] == 0)
     assert np.all(a_g[empty] == 0)
     live = ~empty
-    assert np.all(np.abs(m_g - m_w)[live] <= 1e-4 * np.maximum(1, np.abs(m_w[live])))
+    assert np.all(np.abs(m_g - m_w)[live] <= 1e-3 * np.maximum(1, np.abs(m_w[live])))
     assert np.all(np.abs(l_g - l_w)[live] <= 2e-3 * np.maximum(1, l_w[live]))
     amax = np.abs(a_w).max(axis=-1, keepdims=True)
     tol = 2e-3 * amax + 1e-5 * l_w[..., None] + 1e-6
