@@ -1,0 +1,90 @@
+"""The C ABI without a GPU: libtq4.so loads, exports every symbol include/tq4.h
+declares, and refuses bad geometry before touching the HIP runtime (no compute
+call is made here)."""
+import ctypes as C
+import os
+import re
+
+import pytest
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(REPO, "include", "tq4.h")
+LIB = os.path.join(REPO, "ascend-micro-harness_amd", "libtq4.so")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(tq4_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib(tq4):
+    return tq4.lib()
+
+
+def test_library_exports_every_declared_symbol(lib):
+    names = declared_functions()
+    assert len(names) >= 10
+    for n in names:
+        assert hasattr(lib, n), f"{n} declared in include/tq4.h but not exported"
+
+
+def test_status_strings_and_version(lib):
+    assert lib.tq4_status_string(0) == b"ok"
+    for st in range(-10, 0):
+        assert lib.tq4_status_string(st) != b"unknown status"
+    assert lib.tq4_version() >> 16 == 1
+
+
+def test_writer_refusals(lib):
+    f = lib.tq4_reshape_and_cache_a8
+    dummy = C.c_void_p(16)  # never dereferenced: every call below is refused first
+    args = lambda T, H, d, S, P, tpc, signs=dummy: (None, dummy, dummy, dummy, dummy, dummy, dummy,  # noqa: E731
+                                                    signs, None, T, H, d, S, P, tpc, 0.1, True)
+    assert f(*args(16, 2, 96, 16, 4, 16)) == -2          # head_size
+    assert f(*args(16, 0, 128, 16, 4, 16)) == -3         # no heads
+    assert f(*args(16, 2, 128, 24, 4, 16)) == -3         # block_size % 16
+    assert f(*args(17, 2, 128, 16, 4, 16)) == -4         # partial strip
+    assert f(*args(32, 2, 128, 16, 4, 24)) == -4         # tokens_per_core % 16
+    assert f(*args(16, 2, 128, 16, 4, 16, None)) == -8   # no rotation operand
+    assert f(*args(0, 2, 128, 16, 4, 16)) == 0           # nothing to do
+    g = lib.tq4_reshape_and_cache_bf16
+    assert g(None, None, dummy, dummy, dummy, dummy, dummy, dummy, None, 16, 2, 128, 16, 4, 16,
+             0.1, True) == -1                            # NULL key
+
+
+def test_decode_refusals_and_sizes(lib):
+    d = C.c_void_p(16)
+    dec = lib.tq4_paged_decode
+
+    def call(Hq=32, Hkv=8, hd=128, S=16, K=4, ws=None, wsb=0, stage=1, gate=None, maxb=256):
+        return dec(None, d, d, d, d, d, d, d, gate, ws, wsb, d, 1, Hq, Hkv, hd, S, 4096, maxb, K,
+                   0.1, 0.1, stage, 0)
+
+    assert call(hd=96) == -2
+    assert call(Hq=34) == -3                 # GQA group not integral
+    assert call(Hq=8 * 17) == -3             # GQA group > 16
+    assert call(S=8) == -3
+    assert call(K=300) == -5
+    assert call(K=1, maxb=2048) == -5        # a split may own at most 1024 pages
+    assert call(K=4) == -6                   # no workspace
+    assert call(K=4, ws=d, wsb=100) == -6    # too small
+    assert call(K=1, stage=3) == -7
+    assert call(K=1, stage=2) == -7          # stage 2 needs a gate
+    need = lib.tq4_decode_workspace_bytes(1, 32, 8, 128, 4)
+    assert need >= 1 * 32 * 4 * (128 + 4) * 4 + 8 * 4
+    k = lib.tq4_decode_auto_splits(1, 8, 256, 16)
+    assert 1 <= k <= 256 and (256 + k - 1) // k <= 1024
+    assert lib.tq4_decode_auto_splits(1, 1, 4096, 16) >= 4   # 4096 pages need >= 4 splits
+    comb = lib.tq4_splitk_combine
+    assert comb(None, d, d, None, d, 1, 32, 128, 0, 0.1, 1) == -5
+    assert comb(None, d, d, None, d, 1, 32, 128, 4, 0.1, 2) == -7
+
+
+def test_scatter_refusals(lib):
+    d = C.c_void_p(16)
+    f = lib.tq4_reshape_scatter
+    assert f(None, 0, d, d, d, d, d, d, d, None, None, 1, 2, 48, 16, 4, 0, 2, 0.1) == -2
+    assert f(None, 0, d, d, d, d, d, d, None, None, None, 1, 2, 128, 16, 4, 0, 2, 0.1) == -1
+    assert f(None, 0, d, d, d, d, d, d, d, None, None, 1, 2, 128, 16, 4, 0, 0, 0.1) == 0
