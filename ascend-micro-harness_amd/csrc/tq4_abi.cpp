@@ -149,8 +149,8 @@ uint32_t tq4_decode_auto_splits(uint32_t num_seqs, uint32_t num_kv_heads,
     if (k > by_len) k = by_len;
     if (k > TQ4_MAX_SPLITS) k = TQ4_MAX_SPLITS;
     if (k < 1) k = 1;
-    // one split stages at most TQ4_MAX_SPLIT_PAGES block-table entries
-    const uint64_t k_min = ((uint64_t)max_blocks_per_seq + TQ4_MAX_SPLIT_PAGES - 1) / TQ4_MAX_SPLIT_PAGES;
+    // one split stages at most TQ4_MAX_SPLIT_STRIPS strips of its window
+    const uint64_t k_min = (strips + TQ4_MAX_SPLIT_STRIPS - 1) / TQ4_MAX_SPLIT_STRIPS;
     if (k < k_min) k = k_min;
     return (uint32_t)k;
 }
@@ -176,12 +176,15 @@ int decode_checks(const uint16_t* q, const int8_t* kc, const int8_t* vc, const f
         return TQ4_ERR_GEOMETRY;
     if (!q || !kc || !vc || !sc || !tables || !ctx) return TQ4_ERR_NULL_POINTER;
     if (!(flags & TQ4_DECODE_QUERY_ROTATED) && !pi_signs) return TQ4_ERR_ROTATION;
+    // cache rows are indexed in 32 bits on the device
+    if ((uint64_t)num_blocks * num_kv_heads * block_size > 0xffffffffull) return TQ4_ERR_RANGE;
     return TQ4_OK;
 }
 
-bool split_pages_ok(uint32_t max_blocks_per_seq, uint32_t num_splits)
+bool split_pages_ok(uint32_t max_blocks_per_seq, uint32_t block_size, uint32_t num_splits)
 {
-    return ((uint64_t)max_blocks_per_seq + num_splits - 1) / num_splits <= TQ4_MAX_SPLIT_PAGES;
+    const uint64_t pages = ((uint64_t)max_blocks_per_seq + num_splits - 1) / num_splits;
+    return pages * (block_size / kStrip) <= TQ4_MAX_SPLIT_STRIPS;
 }
 
 tq4::DecodeParams make_params(const uint16_t* q, const int8_t* kc, const int8_t* vc,
@@ -238,7 +241,7 @@ int tq4_paged_decode(void* stream, const uint16_t* q, const int8_t* key_cache,
     if (output_stage >= 1 && !pi_signs) return TQ4_ERR_ROTATION;
     if (num_splits == 0)
         num_splits = tq4_decode_auto_splits(num_seqs, num_kv_heads, max_blocks_per_seq, block_size);
-    if (num_splits > TQ4_MAX_SPLITS || !split_pages_ok(max_blocks_per_seq, num_splits))
+    if (num_splits > TQ4_MAX_SPLITS || !split_pages_ok(max_blocks_per_seq, block_size, num_splits))
         return TQ4_ERR_SPLITS;
     if ((uint64_t)num_seqs * num_kv_heads * num_splits > 0x7fffffffull) return TQ4_ERR_RANGE;
     tq4::DecodeParams p = make_params(q, key_cache, value_cache, scale_cache, block_tables,
@@ -250,7 +253,8 @@ int tq4_paged_decode(void* stream, const uint16_t* q, const int8_t* key_cache,
     if (num_splits > 1) {
         const size_t need =
             tq4_decode_workspace_bytes(num_seqs, num_heads, num_kv_heads, head_size, num_splits);
-        if (!workspace || workspace_bytes < need) return TQ4_ERR_WORKSPACE;
+        if (!workspace || workspace_bytes < need || ((uintptr_t)workspace & 15u))
+            return TQ4_ERR_WORKSPACE;
         p.records = (float*)workspace;
         // The counters sit at the END of the workspace so their place does not
         // depend on num_splits: a workspace zeroed once serves every split count.
@@ -275,10 +279,10 @@ int tq4_paged_decode_partials(void* stream, const uint16_t* q, const int8_t* key
                            num_blocks, max_blocks_per_seq, flags);
     if (rc != TQ4_OK) return rc;
     if (num_splits == 0 || num_splits > TQ4_MAX_SPLITS ||
-        !split_pages_ok(max_blocks_per_seq, num_splits))
+        !split_pages_ok(max_blocks_per_seq, block_size, num_splits))
         return TQ4_ERR_SPLITS;
     if ((uint64_t)num_seqs * num_kv_heads * num_splits > 0x7fffffffull) return TQ4_ERR_RANGE;
-    if (!workspace ||
+    if (!workspace || ((uintptr_t)workspace & 15u) ||
         workspace_bytes < tq4::decode_records_bytes(num_seqs, num_heads, head_size, num_splits))
         return TQ4_ERR_WORKSPACE;
     tq4::DecodeParams p = make_params(q, key_cache, value_cache, scale_cache, block_tables,
@@ -299,6 +303,7 @@ int tq4_splitk_combine(void* stream, const float* workspace, const float* pi_sig
     if (num_seqs == 0 || num_heads == 0) return TQ4_ERR_GEOMETRY;
     if (num_splits == 0 || num_splits > TQ4_MAX_SPLITS) return TQ4_ERR_SPLITS;
     if (!workspace || !out) return TQ4_ERR_NULL_POINTER;
+    if ((uintptr_t)workspace & 15u) return TQ4_ERR_WORKSPACE;
     if (output_stage > 2 || (output_stage == 2 && !gate)) return TQ4_ERR_OUTPUT_STAGE;
     if (output_stage >= 1 && !pi_signs) return TQ4_ERR_ROTATION;
     tq4::DecodeParams p{};

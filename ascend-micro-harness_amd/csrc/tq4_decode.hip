@@ -10,122 +10,105 @@
 //
 // MI355X design
 // -------------
-// One 256-lane workgroup per (seq, kv head, split); its four waves take the
-// split's live strips round-robin and each streams its strips with
-// register-double-buffered loads. Per strip and wave:
-//   * S = K . Q^T on MFMA f32_16x16x16_f16: M = the strip's 16 tokens, N =
-//     the GQA group (up to 16 q heads), K = head_size in head_size/16 steps.
-//     A lane loads d/8 contiguous bytes of one token's key row (one 16-byte
-//     load at d = 128; the whole 1 KiB strip is one coalesced wave load).
-//     Nibbles become fp16 (1 + u/16), u = nibble ^ 8, by shift/and/or only;
-//     the MFMA accumulator starts at -1.5 * sum(q), which removes the bias
-//     exactly in real arithmetic, so the product is sum(q * nibble) / 16.
-//   * The score tile lands in the C layout (lane = q head + 16 * token
-//     quarter), which is exactly the A layout the P.V product needs, so the
-//     online softmax runs in registers (exp2 domain, two lane exchanges for
-//     the row max) and P never leaves the wave.
-//   * O += P . V on the same MFMA, V nibbles as exact fp16 n/16, P scaled by
-//     the value scale and a running power of two so it stays in [0, 2).
+// One 256-lane workgroup per (seq, kv head, split). The split's strips are
+// walked in PAIRS (32 tokens); the four waves take pairs round-robin and each
+// wave streams its pairs through a three-deep register ring (loads for pairs
+// j+1 and j+2 in flight while pair j computes). Every load in the ring is
+// unconditional (indices clamp to the wave's last pair), so the compiler's
+// wait counts stay exact and nothing drains the prefetch.
+//
+// Per pair and wave, on MFMA f32_16x16x32_f16:
+//   * scores, two MFMA chains (token sets T1, T2; M = 16 tokens, N = the GQA
+//     group padded to 16, K = head_size): lane (m, g) loads d/8 contiguous
+//     bytes of one key row, so the wave reads both 1 KiB key strips in one
+//     coalesced pass. Row m of T1 is token 8*((m>>2)&1) + (m&3) of strip m>>3,
+//     T2 the same token + 4 -- chosen so that the score tile leaves each lane
+//     holding exactly the 8 consecutive tokens whose value nibbles form ONE
+//     dword of the channel-major value strip.
+//   * nibbles decode to fp16 (1 + u/64), u = nibble ^ 8, with one and-or per
+//     pair of codes (no conversion instruction); the MFMA accumulator starts
+//     at -1.125 * sum(q), which removes the offset, so the product is
+//     sum(q * nibble) / 64.
+//   * the score tile IS the A operand of P.V (same lane, same token order),
+//     so P never leaves the lane; O += P.V per 16-channel block, plus one
+//     MFMA against a constant 1.125 column that tracks the value offset.
+//   * softmax in the exp2 domain with a lazy maximum: the running maximum
+//     moves only when a score exceeds it by more than 2^8 (or a value scale
+//     outgrows the fp16 headroom), so the accumulator rescale -- the only
+//     cross-lane step -- is off the common path.
 // The four waves' (m, l, acc) merge through LDS; the workgroup then exports
 // one partial record, or, in the fused entry, the last workgroup of each
 // (seq, kv head) to arrive (an agent-scope counter that resets itself)
-// combines all splits, rotates back, gates and stores BF16. No spinlock: the
-// reference's L2-line lock (turboquant_splitk_reduce.cpp:279-350) is replaced
-// by disjoint records plus one counter increment per workgroup.
+// combines all splits -- one q head per wave, every record load in flight at
+// once -- rotates back, gates and stores BF16. No spinlock: the reference's
+// L2-line lock (turboquant_splitk_reduce.cpp:279-350) is replaced by disjoint
+// records plus one counter increment per workgroup.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "../../include/tq4.h"
 #include "tq4_device.hpp"
 #include "tq4_internal.hpp"
 
 namespace tq4 {
 namespace {
 
-typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
-typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
 typedef float f4_t __attribute__((ext_vector_type(4)));
-typedef uint32_t u2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t u4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
-constexpr uint32_t kMant = 0x03C003C0u;  // a nibble placed in fp16 mantissa bits [9:6]
-constexpr uint32_t kOne = 0x3C003C00u;   // fp16 1.0 in both halves
+constexpr uint32_t kNib = 0x00F000F0u;   // a code at fp16 mantissa bits [7:4], both halves
+constexpr uint32_t kCodeBase = 0x3C803C80u;  // fp16 1.0 outside kNib; the nibble sign bit inside
+constexpr float kCodeOffset = 1.125f;    // fp16 code value is 1 + u/64 = 1.125 + n/64
+constexpr float kCodeUnit = 64.0f;
+constexpr float kTau = 8.0f;             // lazy-maximum headroom, log2 units
+constexpr float kShiftLimit = 100.0f;    // bound of the value-scale normalisation shift
+constexpr uint32_t kBadStrip = 0xFFFFFFFFu;
 constexpr uint32_t kFlagRotated = 1u;
+constexpr int kHdrFloats = 160;          // m_x[4][16], l_x[4][16], q_exp[16], flags
 
-__device__ __forceinline__ h4_t as_h4(uint32_t a, uint32_t b)
+// Eight codes of one dword as fp16 (1 + u/64), u = nibble ^ 8; halves in
+// nibble order 0,4,1,5,2,6,3,7 (every operand built against this table uses
+// that order). Each pair is one v_bitop3: kNib ? (bits ^ kCodeBase) :
+// kCodeBase (truth table 0x6A over S0 = bits, S1 = kNib, S2 = kCodeBase),
+// i.e. the nibble with its sign bit flipped under an fp16 1.0.
+__device__ __forceinline__ h8_t codes8(uint32_t w)
 {
-    return __builtin_bit_cast(h4_t, u2_t{a, b});
+    const uint32_t p04 = __builtin_amdgcn_bitop3_b32(w << 4, kNib, kCodeBase, 0x6A);
+    const uint32_t p15 = __builtin_amdgcn_bitop3_b32(w, kNib, kCodeBase, 0x6A);
+    const uint32_t p26 = __builtin_amdgcn_bitop3_b32(w >> 4, kNib, kCodeBase, 0x6A);
+    const uint32_t p37 = __builtin_amdgcn_bitop3_b32(w >> 8, kNib, kCodeBase, 0x6A);
+    return __builtin_bit_cast(h8_t, u4_t{p04, p15, p26, p37});
 }
 
-__device__ __forceinline__ f4_t mfma16(h4_t a, h4_t b, f4_t c)
+__device__ __forceinline__ f4_t mfma32(h8_t a, h8_t b, f4_t c)
 {
-    return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
-// fp16 pair (1 + u/16) with u = n + 8  ->  exact n/16.
-__device__ __forceinline__ uint32_t signed_pair(uint32_t p)
+// Reductions over the four lanes l, l^16, l^32, l^48 (one MFMA column).
+__device__ __forceinline__ float col_max(float v)
 {
-    const h2_t v = __builtin_bit_cast(h2_t, p) - h2_t{(_Float16)1.5f, (_Float16)1.5f};
-    return __builtin_bit_cast(uint32_t, v);
+    const uint32_t u = __float_as_uint(v);
+    const auto a = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const uint32_t w = __float_as_uint(v);
+    const auto b = __builtin_amdgcn_permlane16_swap(w, w, false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
-// One strip's operands for one lane (n = lane & 15, kg = lane >> 4).
-template <int D>
-struct StripRegs {
-    uint32_t k[D / 32];  // key row of token n, bytes kg*d/8 .. +d/8
-    uint32_t v[D / 16];  // value: tokens 4kg..4kg+3 of channel 16b + n (16 bits)
-    f4_t ks;             // key scales of tokens 4kg..4kg+3
-    f4_t vs;             // value scales of tokens 4kg..4kg+3
-};
-
-template <int D>
-__device__ __forceinline__ void load_strip(StripRegs<D>& r, const int8_t* kb, const int8_t* vb,
-                                           const float* ksp, const float* vsp, int n, int kg)
+__device__ __forceinline__ float col_sum(float v)
 {
-    const int8_t* kp = kb + n * (D / 2) + kg * (D / 8);
-    if constexpr (D == 64) {
-        const uint2 w = *(const uint2*)kp;
-        r.k[0] = w.x;
-        r.k[1] = w.y;
-    } else {
-#pragma unroll
-        for (int i = 0; i < D / 128; ++i) {
-            const uint4 w = *(const uint4*)(kp + 16 * i);
-            r.k[4 * i + 0] = w.x;
-            r.k[4 * i + 1] = w.y;
-            r.k[4 * i + 2] = w.z;
-            r.k[4 * i + 3] = w.w;
-        }
-    }
-#pragma unroll
-    for (int b = 0; b < D / 16; ++b) r.v[b] = *(const uint16_t*)(vb + (16 * b + n) * 8 + 2 * kg);
-    r.ks = *(const f4_t*)(ksp + 4 * kg);
-    r.vs = *(const f4_t*)(vsp + 4 * kg);
-}
-
-
-// LDS layout (floats). A fixed header -- m[4][16], l[4][16], q exponents[16],
-// the last-arrival flag, the combine's per-row M and L[16+16] -- then one big
-// region reused in turn by the q staging area [G][D], the wave-merge slots
-// [2][G][D], and the combine's weights [G][K] + normalised rows [G][D].
-constexpr int kMaxWindowPages = 1024;  // block-table entries one split may own
-constexpr int kHdrFloats = 2 * kWaves * 16 + 16 + 4 + 32 + 12 + kMaxWindowPages;
-
-__host__ __device__ constexpr size_t region_floats(uint32_t G, uint32_t D, uint32_t K)
-{
-    const size_t merge = 2ull * G * D;
-    const size_t comb = 2ull * G * K + (size_t)G * D;
-    return merge > comb ? merge : comb;
-}
-
-// Workgroup barrier for LDS traffic only: unlike __syncthreads() it does not
-// wait for outstanding global loads (vmcnt), so prefetched strips stay in
-// flight across it.
-__device__ __forceinline__ void lds_barrier()
-{
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    const uint32_t u = __float_as_uint(v);
+    const auto a = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const uint32_t w = __float_as_uint(v);
+    const auto b = __builtin_amdgcn_permlane16_swap(w, w, false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
 __device__ __forceinline__ float wave_max(float v)
@@ -135,106 +118,140 @@ __device__ __forceinline__ float wave_max(float v)
     return v;
 }
 
-// LSE-combine `nrows` rows of K partial records each (row r, split k at
-// rec + r*row_stride + k*(D+4)) with all 256 threads, leaving the normalised
-// rows acc / L (0 when L == 0) in out[r*D + c]. The (m, l) pairs load in one
-// parallel pass; each thread then sums its channel pairs over the splits with
-// 16 independent record loads in flight.
-// Record traffic between workgroups of one launch: agent-scope atomic
-// (device-coherent, sc1) stores and loads, so no whole-L2 write-back or
-// invalidate is needed around the arrival counter.
+// Workgroup barrier for LDS traffic only: it does not wait for outstanding
+// global loads (vmcnt), so prefetched pairs stay in flight across it.
+__device__ __forceinline__ void lds_barrier()
+{
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// One pair's operands for one lane (n = lane & 15, g = lane >> 4).
+template <int D>
+struct PairRegs {
+    uint32_t k1[D / 32];  // T1 key row (token of row n), channels g*d/4 .. +d/4
+    uint32_t k2[D / 32];  // T2 key row
+    uint32_t v[D / 16];   // value codes: channel 16b + n, 8 tokens of strip g>>1
+    f4_t ks1, ks2;        // key scales of the lane's 8 tokens (T1 then T2)
+    f4_t vs1, vs2;        // value scales of the same tokens
+};
+
+template <int D>
+__device__ __forceinline__ void load_row_chunk(uint32_t (&k)[D / 32], const int8_t* src)
+{
+    if constexpr (D == 64) {
+        const uint2 w = *(const uint2*)src;
+        k[0] = w.x;
+        k[1] = w.y;
+    } else {
+#pragma unroll
+        for (int i = 0; i < D / 128; ++i) {
+            const uint4 w = *(const uint4*)(src + 16 * i);
+            k[4 * i + 0] = w.x;
+            k[4 * i + 1] = w.y;
+            k[4 * i + 2] = w.z;
+            k[4 * i + 3] = w.w;
+        }
+    }
+}
+
+// Record traffic between workgroups of one launch: agent-scope relaxed
+// atomic stores, read back by buffer loads with the device-coherence bit
+// (sc1, what an agent-scope atomic load is on gfx950) -- plain loads to the
+// compiler, so a whole chunk of them is in flight at once. No whole-L2
+// write-back or invalidate is needed around the arrival counter.
 __device__ __forceinline__ void store_coherent(float* p, float v)
 {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+constexpr int kCachePolicySc1 = 16;  // cache-policy operand bit of sc1
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t records_rsrc(const float* base)
+{
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), (short)0, 0x7fffffff,
+                                             0x00020000);
+}
+
 template <bool COHERENT>
-__device__ __forceinline__ float load_rec(const float* p)
+__device__ __forceinline__ float2 rec_load2(__amdgpu_buffer_rsrc_t r, uint32_t byte_off)
 {
-    if constexpr (COHERENT)
-        return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    return *p;
+    const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, byte_off, 0, COHERENT ? kCachePolicySc1 : 0);
+    return make_float2(__uint_as_float(v[0]), __uint_as_float(v[1]));
 }
 
+template <bool COHERENT>
+__device__ __forceinline__ float rec_load1(__amdgpu_buffer_rsrc_t r, uint32_t byte_off)
+{
+    return __uint_as_float(
+        __builtin_amdgcn_raw_buffer_load_b32(r, byte_off, 0, COHERENT ? kCachePolicySc1 : 0));
+}
+
+// LSE-combine the K partial records of one (seq, q head) row -- split k at
+// rr + k*(D+4) = [m, l, 0, 0, acc[D]] -- for the D/64 channels lane*D/64..
+// of one wave lane, leaving acc / L (0 when L == 0). Every record load of a
+// chunk of splits is in flight together (one round trip per chunk).
 template <int D, bool COHERENT>
-__device__ void combine_rows(const float* rec, size_t row_stride, uint32_t nrows, uint32_t K,
-                             float* w, float* lk, float* ML, float* out)
-{
-    constexpr int RS = D + 4;
-    constexpr int CH = 16;
-    const int tid = threadIdx.x;
-    const uint32_t nk = nrows * K;
-    for (uint32_t t = tid; t < nk; t += kThreads) {
-        const float* rr = rec + (t / K) * row_stride + (size_t)(t % K) * RS;
-        w[t] = load_rec<COHERENT>(rr);
-        lk[t] = load_rec<COHERENT>(rr + 1);
-    }
-    __syncthreads();
-    if ((uint32_t)tid < nrows) {
-        float M = kMasked;
-        for (uint32_t k = 0; k < K; ++k) M = fmaxf(M, w[tid * K + k]);
-        ML[tid] = M;
-    }
-    __syncthreads();
-    for (uint32_t t = tid; t < nk; t += kThreads) {
-        const float e = expf(w[t] - ML[t / K]);
-        w[t] = e;
-        lk[t] *= e;
-    }
-    __syncthreads();
-    if ((uint32_t)tid < nrows) {
-        float L = 0.0f;
-        for (uint32_t k = 0; k < K; ++k) L += lk[tid * K + k];
-        ML[16 + tid] = L;
-    }
-    const uint32_t npairs = nrows * (D / 2);
-    for (uint32_t pi = tid; pi < npairs; pi += kThreads) {
-        const uint32_t r = pi / (D / 2), c = 2 * (pi % (D / 2));
-        const float* rr = rec + r * row_stride + 4 + c;
-        const float* wr = w + r * K;
-        float a0 = 0.0f, a1 = 0.0f;
-        for (uint32_t k0 = 0; k0 < K; k0 += CH) {
-            float2 v[CH];
-#pragma unroll
-            for (int i = 0; i < CH; ++i) {
-                if (k0 + i < K) {
-                    const float* at = rr + (size_t)(k0 + i) * RS;
-                    if constexpr (COHERENT)
-                        v[i] = make_float2(load_rec<true>(at), load_rec<true>(at + 1));
-                    else
-                        v[i] = *(const float2*)at;
-                } else {
-                    v[i] = make_float2(0.0f, 0.0f);
-                }
-            }
-#pragma unroll
-            for (int i = 0; i < CH; ++i) {
-                const float wk = k0 + i < K ? wr[k0 + i] : 0.0f;
-                a0 += v[i].x * wk;
-                a1 += v[i].y * wk;
-            }
-        }
-        out[r * D + c] = a0;
-        out[r * D + c + 1] = a1;
-    }
-    __syncthreads();
-    for (uint32_t e = tid; e < nrows * D; e += kThreads) {
-        const float L = ML[16 + e / D];
-        out[e] = L == 0.0f ? 0.0f : out[e] / L;
-    }
-    __syncthreads();
-}
-
-// Egress of one normalised row (in LDS) by one wave: optionally Pi^T and
-// 1/sqrt(d), optionally the gate, BF16 RNE store.
-template <int D>
-__device__ void egress_row(const float* row, const float* pi_signs, const float* gate,
-                           uint16_t* out, float inv_sqrt_len, uint32_t stage, int lane)
+__device__ void combine_row(const float* rr, uint32_t K, int lane, float (&out)[D / 64])
 {
     constexpr int CPL = D / 64;
-    float v[CPL];
+    constexpr int RS = D + 4;
+    constexpr int KC = 16;
+    const __amdgpu_buffer_rsrc_t rsrc = records_rsrc(rr);
+    float M = -INFINITY, L = 0.0f, a[CPL];
 #pragma unroll
-    for (int j = 0; j < CPL; ++j) v[j] = row[lane * CPL + j];
+    for (int c = 0; c < CPL; ++c) a[c] = 0.0f;
+    for (uint32_t k0 = 0; k0 < K; k0 += KC) {
+        const uint32_t kn = K - k0 < (uint32_t)KC ? K - k0 : (uint32_t)KC;
+        float mk[KC], lk[KC], ak[KC][CPL];
+#pragma unroll
+        for (int i = 0; i < KC; ++i) {
+            // unconditional (index clamped to the chunk's last split) so the
+            // whole chunk issues back to back; surplus copies are ignored
+            const uint32_t off = ((k0 + min((uint32_t)i, kn - 1)) * RS) * 4u;
+            const float2 ml = rec_load2<COHERENT>(rsrc, off);
+            mk[i] = ml.x;
+            lk[i] = ml.y;
+            if constexpr (CPL == 1) {
+                ak[i][0] = rec_load1<COHERENT>(rsrc, off + (4 + lane) * 4);
+            } else {
+#pragma unroll
+                for (int c = 0; c < CPL; c += 2) {
+                    const float2 v = rec_load2<COHERENT>(rsrc, off + (4 + lane * CPL + c) * 4);
+                    ak[i][c] = v.x;
+                    ak[i][c + 1] = v.y;
+                }
+            }
+        }
+        float Mc = M;
+#pragma unroll
+        for (int i = 0; i < KC; ++i)
+            if ((uint32_t)i < kn) Mc = fmaxf(Mc, mk[i]);
+        const float s = M == -INFINITY ? 0.0f : expf(M - Mc);
+        L *= s;
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) a[c] *= s;
+#pragma unroll
+        for (int i = 0; i < KC; ++i) {
+            if ((uint32_t)i < kn) {
+                const float w = expf(mk[i] - Mc);
+                L += lk[i] * w;
+#pragma unroll
+                for (int c = 0; c < CPL; ++c) a[c] += w * ak[i][c];
+            }
+        }
+        M = Mc;
+    }
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) out[c] = L == 0.0f ? 0.0f : a[c] / L;
+}
+
+// Egress of one normalised row held by one wave (lane owns channels
+// lane*D/64 ..): optionally Pi^T and 1/sqrt(d), optionally the gate, BF16 RNE.
+template <int D>
+__device__ void egress_regs(float (&v)[D / 64], const float* pi_signs, const float* gate,
+                            uint16_t* out, float inv_sqrt_len, uint32_t stage, int lane)
+{
+    constexpr int CPL = D / 64;
     if (stage >= 1) {
         float sg[CPL];
 #pragma unroll
@@ -251,26 +268,36 @@ __device__ void egress_row(const float* row, const float* pi_signs, const float*
     for (int j = 0; j < CPL; ++j) out[lane * CPL + j] = (uint16_t)f32_to_bf16(v[j]);
 }
 
+__host__ __device__ constexpr size_t region_floats(uint32_t G, uint32_t D)
+{
+    return 4ull * G * D;  // q staging [G][D], then the four waves' rows [4][G][D]
+}
+
+// Two waves per SIMD at d <= 128 (the register ring fits in 256 VGPRs); the
+// d = 256 ring needs the whole file.
 template <int D, int MODE>
-__global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p)
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 2 : 1, 2)))
+void decode_kernel(DecodeParams p)
 {
     constexpr int CPL = D / 64;   // channels per lane in the row layout
-    constexpr int NB = D / 16;    // MFMA steps of the score, blocks of the output
-    constexpr int KDW = D / 32;   // key words per lane per strip
+    constexpr int NJ = D / 32;    // score MFMAs per token set (one per key dword)
+    constexpr int NB = D / 16;    // P.V MFMAs (16-channel blocks)
     constexpr int RS = D + 4;     // record stride in floats
+    constexpr int NBUF = D >= 256 ? 2 : 3;
     extern __shared__ float smem[];
 
     const uint32_t G = p.G, S = p.S;
-    float* m_x = smem;
-    float* l_x = m_x + kWaves * 16;
-    int* q_exp = (int*)(l_x + kWaves * 16);
-    int* flag = q_exp + 16;
-    float* ML = (float*)(flag + 4);
-    int32_t* page_lds = (int32_t*)(smem + 192);
-    float* region = smem + kHdrFloats;
+    float* m_x = smem;                       // [4][16]
+    float* l_x = smem + 64;                  // [4][16]
+    int* q_exp = (int*)(smem + 128);         // [16]
+    int* flag = (int*)(smem + 144);
+    uint32_t* strip_lds = (uint32_t*)(smem + kHdrFloats);  // [TQ4 max split strips]
+    float* region = smem + kHdrFloats + TQ4_MAX_SPLIT_STRIPS;
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int n = lane & 15, kg = lane >> 4;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
+    const int n = lane & 15, g4 = lane >> 4;
+    const int half = g4 & 1, sp = g4 >> 1;  // value/scale lanes: strip sp of the pair, tokens 8*half..
     const uint32_t item = blockIdx.x;
     const uint32_t split = item % p.K;
     const uint32_t kvh = (item / p.K) % p.Hkv;
@@ -278,8 +305,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p)
 
     // ---- phase 0: every small load -- context length, q rows, rotation
     // signs, the split's block-table window -- is issued before any strip
-    // load: vmcnt retires in order, so a later wait for one of these would
-    // otherwise also wait for the strip stream.
+    // load and retired together.
     const int32_t ctx_raw = p.context_lens[seq];
     const bool rotate = !(p.flags & kFlagRotated);
     uint16_t qraw[4][CPL];
@@ -297,56 +323,81 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p)
 #pragma unroll
         for (int j = 0; j < CPL; ++j) sg[j] = p.pi_signs[lane * CPL + j];
     }
-    // The split's window of the block table: the reference AIC decode's
-    // Partition(page_count, splits, split) over the table's max_blocks_per_seq
-    // pages (turboquant_paged_decode_attention.cpp:1598-1624), staged in LDS
-    // so the strip loop reads page ids without touching vmcnt.
+    // The split's window of the block table: Partition(max_blocks_per_seq,
+    // splits, split) (turboquant_paged_decode_attention.cpp:1598-1624),
+    // staged in LDS as the first cache row of every strip.
     uint32_t pb, pc;
     partition(p.max_blocks, p.K, split, pb, pc);
     const uint32_t spp = S / kStrip;
-    const uint32_t n_window = pc * spp;
-    const uint32_t n_win_mine =
-        n_window > (uint32_t)wave ? (n_window - wave + kWaves - 1) / kWaves : 0u;
-    const int32_t* tbl = p.block_tables + (size_t)seq * p.max_blocks;
-    for (uint32_t t = tid; t < pc; t += kThreads) page_lds[t] = tbl[pb + t];
-    // Unconditional vmcnt(0) (expcnt and lgkmcnt left at their maxima): the
-    // loads above are all complete from here on every path, so the compiler's
-    // wait analysis never again waits on them -- or on what is queued after.
-    __builtin_amdgcn_s_waitcnt(0x0F70);
-    lds_barrier();
-    const size_t plane_floats = (size_t)p.P * p.Hkv * S;
-
-    // Operands of this wave's j-th strip; false when its page is out of range
-    // (table entries past the live context may hold anything).
-    auto fetch = [&](uint32_t j, StripRegs<D>& r) -> bool {
-        const uint32_t idx = wave + kWaves * j;
-        const uint32_t phys = (uint32_t)__builtin_amdgcn_readfirstlane(page_lds[idx / spp]);
-        if (phys >= p.P) return false;
-        const size_t row = ((size_t)phys * p.Hkv + kvh) * S + (size_t)(idx % spp) * kStrip;
-        load_strip<D>(r, p.key_cache + row * (D / 2), p.value_cache + row * (D / 2),
-                      p.scale_cache + row, p.scale_cache + row + plane_floats, n, kg);
-        return true;
-    };
-    StripRegs<D> buf0, buf1, buf2;
-    bool ok0 = n_win_mine > 0 ? fetch(0, buf0) : false;
-    bool ok1 = n_win_mine > 1 ? fetch(1, buf1) : false;
-    bool ok2 = false;
-
-    // Live strips of the window: tokens at or past ctx are masked, strips with
-    // none live are not walked (turboquant_decode_tail.hpp:246-272).
+    const int32_t* tbl = p.block_tables + (size_t)seq * p.max_blocks + pb;
     uint32_t ctx = ctx_raw < 0 ? 0u : (uint32_t)ctx_raw;
     const uint64_t capacity = (uint64_t)p.max_blocks * S;
     if (ctx > capacity) ctx = (uint32_t)capacity;
     const uint64_t tok0 = (uint64_t)pb * S;
-    uint32_t live = 0;
+    uint32_t ltok = 0;  // live tokens of the window
     if (pc > 0 && ctx > tok0) {
-        const uint64_t need = (ctx - tok0 + kStrip - 1) / kStrip;
-        live = need < (uint64_t)n_window ? (uint32_t)need : n_window;
+        const uint64_t l = ctx - tok0;
+        ltok = l < (uint64_t)pc * S ? (uint32_t)l : pc * S;
     }
-    const uint32_t n_mine = live > (uint32_t)wave ? (live - wave + kWaves - 1) / kWaves : 0u;
+    const uint32_t live_pages = (ltok + S - 1) / S;
+    int bad = 0;
+    for (uint32_t t = tid; t < pc; t += kThreads) {
+        const uint32_t phys = (uint32_t)tbl[t];
+        const bool ok = phys < p.P;
+        if (!ok && t < live_pages) bad = 1;
+        const uint32_t row = (phys * p.Hkv + kvh) * S;
+        for (uint32_t s = 0; s < spp; ++s) strip_lds[t * spp + s] = ok ? row + kStrip * s : kBadStrip;
+    }
+    bad = __syncthreads_or(bad);
+    // Every phase-0 load is complete here; saying so (vmcnt(0), expcnt and
+    // lgkmcnt left at their maxima) keeps the compiler's wait analysis from
+    // later waiting on them -- and so on the strip loads queued after them.
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    const uint32_t np_total = (ltok + 2 * kStrip - 1) / (2 * kStrip);
+    const uint32_t np_full = bad ? 0u : ltok / (2 * kStrip);
+    const uint32_t nws = pc * spp;  // strips in the window
+    const size_t plane_floats = (size_t)p.P * p.Hkv * S;
 
-    // ---- phase 2 (overlaps the strip loads): rotate q (Pi = M * inv_sqrt_len),
-    // fold the softmax scale, normalise each row by a power of two, stage in LDS.
+    // Operands of pair gp (window strips 2gp, 2gp+1). `safe`: strips past the
+    // window or on invalid pages read row 0 (their tokens are masked).
+    auto fetch = [&](PairRegs<D>& r, uint32_t gp, bool safe) {
+        const uint32_t s0 = 2 * gp;
+        uint32_t sk = s0 + (n >> 3), sv = s0 + sp;
+        if (safe) {
+            sk = min(sk, nws - 1);
+            sv = min(sv, nws - 1);
+        }
+        uint32_t rk = strip_lds[sk], rv = strip_lds[sv];
+        if (safe) {
+            rk = rk == kBadStrip ? 0u : rk;
+            rv = rv == kBadStrip ? 0u : rv;
+        }
+        const uint32_t t1 = 8 * ((n >> 2) & 1) + (n & 3);
+        const int8_t* kb = p.key_cache + (size_t)(rk + t1) * (D / 2) + g4 * (D / 8);
+        load_row_chunk<D>(r.k1, kb);
+        load_row_chunk<D>(r.k2, kb + 4 * (D / 2));
+        const int8_t* vb8 = p.value_cache + (size_t)rv * (D / 2) + n * 8 + 4 * half;
+#pragma unroll
+        for (int b = 0; b < NB; ++b) r.v[b] = *(const uint32_t*)(vb8 + 128 * b);
+        const float* ksp = p.scale_cache + rv + 8 * half;
+        r.ks1 = *(const f4_t*)ksp;
+        r.ks2 = *(const f4_t*)(ksp + 4);
+        r.vs1 = *(const f4_t*)(ksp + plane_floats);
+        r.vs2 = *(const f4_t*)(ksp + plane_floats + 4);
+    };
+
+    // ---- the first pairs of this wave's ring go out before the q prologue.
+    const uint32_t nfw = np_full > (uint32_t)wave ? (np_full - wave + kWaves - 1) / kWaves : 0u;
+    auto gp_of = [&](uint32_t j) { return (uint32_t)wave + kWaves * min(j, nfw - 1); };
+    PairRegs<D> b0, b1;
+    [[maybe_unused]] PairRegs<D> b2;
+    if (nfw > 0) {
+        fetch(b0, gp_of(0), false);
+        if constexpr (NBUF == 3) fetch(b1, gp_of(1), false);
+    }
+
+    // ---- phase 1: rotate q (Pi = M * inv_sqrt_len), fold the softmax scale,
+    // normalise each row by a power of two, stage in LDS.
     float* q_st = region;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -374,270 +425,307 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p)
     }
     lds_barrier();
 
-    // ---- this lane's B operand (q head n, channel group kg) and constants.
-    u2_t qop[NB];
+    // ---- this lane's B operands (q head n, channels g4*d/4 ..) in the
+    // codes8 channel order, and the per-row constants.
+    const bool row_live = (uint32_t)n < G;
+    h8_t qop[NJ];
     float bias = 0.0f, cf = 0.0f;
-    if ((uint32_t)n < G) {
-        const float* qrow = q_st + n * D;
+    if (row_live) {
+        const float* qrow = q_st + n * D + g4 * (D / 4);
 #pragma unroll
-        for (int dd = 0; dd < KDW; ++dd) {
+        for (int j = 0; j < NJ; ++j) {
+            const float4 lo = *(const float4*)(qrow + 8 * j);
+            const float4 hi = *(const float4*)(qrow + 8 * j + 4);
+            const h8_t h = h8_t{(_Float16)lo.x, (_Float16)hi.x, (_Float16)lo.y, (_Float16)hi.y,
+                                (_Float16)lo.z, (_Float16)hi.z, (_Float16)lo.w, (_Float16)hi.w};
+            qop[j] = h;
 #pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const int base = kg * (D / 4) + 8 * dd + 2 * h;
-                const _Float16 a0 = (_Float16)qrow[base], a1 = (_Float16)qrow[base + 4];
-                const _Float16 a2 = (_Float16)qrow[base + 1], a3 = (_Float16)qrow[base + 5];
-                bias += ((float)a0 + (float)a1) + ((float)a2 + (float)a3);
-                qop[2 * dd + h] = __builtin_bit_cast(u2_t, h4_t{a0, a1, a2, a3});
-            }
+            for (int e = 0; e < 8; ++e) bias += (float)h[e];
         }
-        cf = ldexpf(16.0f * kLog2e, q_exp[n]);
+        cf = ldexpf(kCodeUnit * kLog2e, q_exp[n]);
     } else {
 #pragma unroll
-        for (int s = 0; s < NB; ++s) qop[s] = u2_t{0u, 0u};
+        for (int j = 0; j < NJ; ++j) qop[j] = h8_t{0, 0, 0, 0, 0, 0, 0, 0};
     }
-    bias += xor_lanes(bias, 16);
-    bias += xor_lanes(bias, 32);
-    bias *= -1.5f;
-    // No barrier here: q_st is next overwritten after the merge barrier,
-    // which every wave reaches only after building its operands.
+    bias = col_sum(bias) * -kCodeOffset;
+    const f4_t bias4 = f4_t{bias, bias, bias, bias};
+    const _Float16 off16 = (_Float16)kCodeOffset;
+    const h8_t offset_col = h8_t{off16, off16, off16, off16, off16, off16, off16, off16};
+    // q_st is next overwritten after the first merge barrier, which every
+    // wave reaches only after building its operands.
 
-    // ---- stream this wave's strips (register double buffer).
+    // ---- streaming state. Scores t = s - mo with s = score * log2(e)
+    // (log2 units), mo = m_used - sh; P' = exp2(t) = P * 2^sh, where
+    // sh = 127 - E normalises P * vscale into fp16 (E: exponent field bound
+    // of the value scales seen so far, wave-uniform).
     f4_t acc[NB];
 #pragma unroll
     for (int b = 0; b < NB; ++b) acc[b] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
-    float m2 = kMasked, lpart = 0.0f;
-    int E = 0;  // running max exponent field of the live value scales
+    f4_t cr = f4_t{0.0f, 0.0f, 0.0f, 0.0f};  // offset column: 1.125 * sum P'vs per row
+    float m_used = row_live ? -INFINITY : INFINITY;  // padded rows stay silent
+    float mo = m_used;
+    float lpart = 0.0f;
+    int E = 0;
+    float sh = kShiftLimit;
+    float thr = kTau + sh;
+    float vb = ldexpf(1.0f, -126);
 
-    auto process = [&](const StripRegs<D>& cur, uint32_t j) {
-            const uint32_t idx = wave + kWaves * j;
-            // Scores: C[token][q] = sum_c (1 + u/16) q16 - 1.5 sum q16 = sum q16 n / 16.
-            f4_t sc = f4_t{bias, bias, bias, bias};
+    auto process = [&](const PairRegs<D>& r, uint32_t gp, bool masked) {
+        f4_t c1 = bias4, c2 = bias4;
 #pragma unroll
-            for (int dd = 0; dd < KDW; ++dd) {
-                const uint32_t x = cur.k[dd] ^ 0x88888888u;
-                const uint32_t p0 = ((x << 6) & kMant) | kOne;
-                const uint32_t p1 = ((x << 2) & kMant) | kOne;
-                const uint32_t p2 = ((x >> 2) & kMant) | kOne;
-                const uint32_t p3 = ((x >> 6) & kMant) | kOne;
-                sc = mfma16(as_h4(p0, p1), __builtin_bit_cast(h4_t, qop[2 * dd]), sc);
-                sc = mfma16(as_h4(p2, p3), __builtin_bit_cast(h4_t, qop[2 * dd + 1]), sc);
-            }
-            const uint32_t act = active_in_strip(tok0 + (uint64_t)idx * kStrip, ctx);
-            float s[4];
+        for (int j = 0; j < NJ; ++j) {
+            c1 = mfma32(codes8(r.k1[j]), qop[j], c1);
+            c2 = mfma32(codes8(r.k2[j]), qop[j], c2);
+        }
+        float c[8], cfk[8], vs[8];
+        bool live[8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            c[i] = c1[i];
+            c[4 + i] = c2[i];
+            cfk[i] = cf * r.ks1[i];
+            cfk[4 + i] = cf * r.ks2[i];
+            vs[i] = r.vs1[i];
+            vs[4 + i] = r.vs2[i];
+        }
+        if (masked) {
+            // window token of value i: pair base + strip sp + 8*half + (i&3) + 4*(i>>2)
+            const uint32_t tb = 32 * gp + 16 * sp + 8 * half;
+            const uint32_t sv = min(2 * gp + sp, nws - 1);
+            const bool page_ok = strip_lds[sv] != kBadStrip;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) live[i] = page_ok && tb + (i & 3) + 4 * (i >> 2) < ltok;
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) live[i] = true;
+        }
+        float t[8];
+        float tmax = -INFINITY, vmax = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            t[i] = live[i] ? __builtin_fmaf(c[i], cfk[i], -mo) : -INFINITY;
+            tmax = fmaxf(tmax, t[i]);
+            vmax = fmaxf(vmax, live[i] ? vs[i] : 0.0f);
+        }
+        if (__builtin_expect(__any(tmax > thr || vmax >= vb), 0)) {
+            // Move the row maximum / the value-scale bound, rescale.
+            float smax = -INFINITY;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) smax = fmaxf(smax, live[i] ? c[i] * cfk[i] : -INFINITY);
+            smax = col_max(smax);
+            const float vm = wave_max(vmax);
+            const int En = max(E, (int)((__float_as_uint(vm) >> 23) & 0xffu));
+            const float shn = fminf(fmaxf(127.0f - (float)En, -kShiftLimit), kShiftLimit);
+            const float mn = row_live ? fmaxf(m_used, smax) : m_used;
+            const float mon = mn - shn;
+            float f = 1.0f;
+            if (row_live) f = mo == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mo - mon);
+            lpart *= f;
+            float fr[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) fr[i] = __shfl(f, 4 * g4 + i, 64);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const float v = (sc[i] * cf) * cur.ks[i];
-                s[i] = (uint32_t)(4 * kg + i) < act ? v : kMasked;
+#pragma unroll
+                for (int b = 0; b < NB; ++b) acc[b][i] *= fr[i];
+                cr[i] *= fr[i];
             }
-            float mx = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
-            mx = fmaxf(mx, xor_lanes(mx, 16));
-            mx = fmaxf(mx, xor_lanes(mx, 32));
-            const float mn = fmaxf(m2, mx);
-            const float alpha = exp2f(m2 - mn);
-            float pr[4], psum = 0.0f;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                pr[i] = exp2f(s[i] - mn);
-                psum += pr[i];
-            }
-            lpart = lpart * alpha + psum;
-            int e = 0;
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                if ((uint32_t)(4 * kg + i) < act)
-                    e = max(e, (int)((__float_as_uint(cur.vs[i]) >> 23) & 0xffu));
-            e = max(e, __shfl_xor(e, 16, 64));
-            e = max(e, __shfl_xor(e, 32, 64));
-            const int En = max(E, e);
-            const float av = ldexpf(alpha, E - En);
-            _Float16 hp[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float x =
-                    (uint32_t)(4 * kg + i) < act ? ldexpf(pr[i] * cur.vs[i], 127 - En) : 0.0f;
-                hp[i] = (_Float16)x;
-            }
-            const h4_t P = h4_t{hp[0], hp[1], hp[2], hp[3]};
-            if (__any(av != 1.0f)) {
-                float f[4];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) f[i] = __shfl(av, 4 * kg + i, 64);
-#pragma unroll
-                for (int b = 0; b < NB; ++b)
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) acc[b][i] *= f[i];
-            }
-#pragma unroll
-            for (int b = 0; b < NB; ++b) {
-                const uint32_t x = cur.v[b] ^ 0x8888u;
-                const uint32_t y = x | (x << 12);
-                const uint32_t b0 = signed_pair(((y << 6) & kMant) | kOne);
-                const uint32_t b1 = signed_pair(((y >> 2) & kMant) | kOne);
-                acc[b] = mfma16(P, as_h4(b0, b1), acc[b]);
-            }
-            m2 = mn;
+            m_used = mn;
+            mo = mon;
             E = En;
-            };
-    // 3-deep ring: strip j computes while strips j+1 and j+2 are in flight.
-    for (uint32_t j = 0; j < n_mine; j += 3) {
-        ok2 = j + 2 < n_mine ? fetch(j + 2, buf2) : false;
-        if (ok0) process(buf0, j);
-        if (j + 1 >= n_mine) break;
-        ok0 = j + 3 < n_mine ? fetch(j + 3, buf0) : false;
-        if (ok1) process(buf1, j + 1);
-        if (j + 2 >= n_mine) break;
-        ok1 = j + 4 < n_mine ? fetch(j + 4, buf1) : false;
-        if (ok2) process(buf2, j + 2);
+            sh = shn;
+            thr = kTau + shn;
+            vb = ldexpf(1.0f, En - 126);
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                t[i] = live[i] ? __builtin_fmaf(c[i], cfk[i], -mo) : -INFINITY;
+        }
+        _Float16 x[8];
+        float psum = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float pr = __builtin_amdgcn_exp2f(t[i]);
+            psum += pr;
+            x[i] = (_Float16)(live[i] ? pr * vs[i] : 0.0f);
+        }
+        lpart += psum;
+        // A operand in the codes8 token order: (T1[0], T2[0], T1[1], T2[1], ...)
+        const h8_t P = h8_t{x[0], x[4], x[1], x[5], x[2], x[6], x[3], x[7]};
+#pragma unroll
+        for (int b = 0; b < NB; ++b) acc[b] = mfma32(P, codes8(r.v[b]), acc[b]);
+        cr = mfma32(P, offset_col, cr);
+    };
+
+    // ---- full pairs: the three-deep (two-deep at d = 256) register ring.
+    if (nfw > 0) {
+        if constexpr (NBUF == 3) {
+            uint32_t j = 0;
+            for (; j + 3 <= nfw; j += 3) {
+                fetch(b2, gp_of(j + 2), false);
+                process(b0, gp_of(j), false);
+                fetch(b0, gp_of(j + 3), false);
+                process(b1, gp_of(j + 1), false);
+                fetch(b1, gp_of(j + 4), false);
+                process(b2, gp_of(j + 2), false);
+            }
+            if (j < nfw) process(b0, gp_of(j), false);
+            if (j + 1 < nfw) process(b1, gp_of(j + 1), false);
+        } else {
+            uint32_t j = 0;
+            for (; j + 2 <= nfw; j += 2) {
+                fetch(b1, gp_of(j + 1), false);
+                process(b0, gp_of(j), false);
+                fetch(b0, gp_of(j + 2), false);
+                process(b1, gp_of(j + 1), false);
+            }
+            if (j < nfw) process(b0, gp_of(j), false);
+        }
+    }
+    // ---- the partial tail pair (and every pair of a window holding an
+    // invalid page): masked, one pair at a time.
+    if (np_total > np_full) {
+        const uint32_t first = np_full + ((uint32_t)(wave + kWaves) - (np_full & 3u)) % kWaves;
+        for (uint32_t gp = first; gp < np_total; gp += kWaves) {
+            PairRegs<D> bm;
+            fetch(bm, gp, true);
+            process(bm, gp, true);
+        }
     }
 
-    // ---- merge the four waves: common reference M per row, then sum.
-    lpart += xor_lanes(lpart, 16);
-    lpart += xor_lanes(lpart, 32);
-    if (kg == 0) {
-        m_x[wave * 16 + n] = m2;
-        l_x[wave * 16 + n] = lpart;
+    // ---- merge the four waves. Per wave: l = row sum over the four lane
+    // groups; the true scale of l and acc is 2^-sh; the offset column comes
+    // off acc. Each wave scales its rows to the common row maximum and parks
+    // them in LDS; then all 256 threads sum the four copies of each output.
+    const float lsum = col_sum(lpart);
+    const float unscale = ldexpf(1.0f, -(int)sh);
+    if (g4 == 0) {
+        m_x[wave * 16 + n] = row_live ? m_used : -INFINITY;
+        l_x[wave * 16 + n] = lsum * unscale;
     }
     lds_barrier();
-    const float unit = ldexpf(16.0f, E - 127);
-    float Mrow[4], Lrow[4];
+    float* part = region;  // [kWaves][G][D]
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const int r = 4 * kg + i;
+        const int r = 4 * g4 + i;
         float M = m_x[r];
 #pragma unroll
         for (int w = 1; w < kWaves; ++w) M = fmaxf(M, m_x[w * 16 + r]);
-        float L = 0.0f;
+        const float mine = m_x[wave * 16 + r];
+        const float f = (M == -INFINITY || mine == -INFINITY)
+                            ? 0.0f
+                            : __builtin_amdgcn_exp2f(mine - M) * (kCodeUnit * unscale);
+        if ((uint32_t)r < G) {
+            float* dst = part + ((size_t)wave * G + r) * D + n;
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) L += exp2f(m_x[w * 16 + r] - M) * l_x[w * 16 + r];
-        const float f = exp2f(m_x[wave * 16 + r] - M) * unit;
-#pragma unroll
-        for (int b = 0; b < NB; ++b) acc[b][i] *= f;
-        Mrow[i] = M;
-        Lrow[i] = L;
+            for (int b = 0; b < NB; ++b) dst[16 * b] = (acc[b][i] - cr[i]) * f;
+        }
     }
-    float* slot0 = region;
-    float* slot1 = region + (size_t)G * D;
-    auto put = [&](float* slot) {
+    lds_barrier();
+    // Row totals (every thread of a row reads the same four (m, l) pairs).
+    auto row_stats = [&](uint32_t r, float& M, float& L) {
+        M = m_x[r];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t r = 4 * kg + i;
-            if (r < G) {
+        for (int w = 1; w < kWaves; ++w) M = fmaxf(M, m_x[w * 16 + r]);
+        L = 0.0f;
+        if (M != -INFINITY) {
 #pragma unroll
-                for (int b = 0; b < NB; ++b) slot[r * D + 16 * b + n] = acc[b][i];
+            for (int w = 0; w < kWaves; ++w) {
+                const float mw = m_x[w * 16 + r];
+                if (mw != -INFINITY) L += __builtin_amdgcn_exp2f(mw - M) * l_x[w * 16 + r];
             }
         }
     };
-    auto add = [&](const float* slot) {
+    const uint32_t outs = G * D;
+    auto summed = [&](uint32_t e) {
+        float v = part[e];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t r = 4 * kg + i;
-            if (r < G) {
-#pragma unroll
-                for (int b = 0; b < NB; ++b) acc[b][i] += slot[r * D + 16 * b + n];
-            }
-        }
+        for (int w = 1; w < kWaves; ++w) v += part[(size_t)w * outs + e];
+        return v;
     };
-    if (wave >= 2) put(wave == 2 ? slot0 : slot1);
-    lds_barrier();
-    if (wave < 2) add(wave == 0 ? slot0 : slot1);
-    lds_barrier();
-    if (wave == 1) put(slot0);
-    lds_barrier();
-    if (wave == 0) add(slot0);
 
     const bool local = (MODE == 1) && p.K == 1;
-    if (!local) {
-        // ---- export one record per q head: [m (natural log), l, 0, 0, acc].
-        float* rec_base = p.records + (((size_t)seq * p.Hq + (size_t)kvh * G) * p.K + split) * RS;
-        if (wave == 0) {
+    if (local) {
+        // ---- one split: normalise in place (wave-0 slice), then the egress.
+        for (uint32_t e = tid; e < outs; e += kThreads) {
+            float M, L;
+            row_stats(e / D, M, L);
+            const float v = summed(e);
+            part[e] = L == 0.0f ? 0.0f : v / L;  // part[0..outs) is read only by this thread
+        }
+        lds_barrier();
+        for (uint32_t g = wave; g < G; g += kWaves) {
+            float v[CPL];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const uint32_t r = 4 * kg + i;
-                if (r < G) {
-                    float* rec = rec_base + (size_t)r * p.K * RS;
-                    auto put_rec = [&](int at, float v) {
-                        if constexpr (MODE == 1) store_coherent(rec + at, v);
-                        else rec[at] = v;
-                    };
+            for (int j = 0; j < CPL; ++j) v[j] = part[g * D + lane * CPL + j];
+            const size_t qh = (size_t)seq * p.Hq + kvh * G + g;
+            egress_regs<D>(v, p.pi_signs, p.gate ? p.gate + qh * D : nullptr, p.out + qh * D,
+                           p.inv_sqrt_len, p.output_stage, lane);
+        }
+        return;
+    }
+
+    // ---- export one record per q head: [m (natural log), l, 0, 0, acc].
+    float* rec_base = p.records + (((size_t)seq * p.Hq + (size_t)kvh * G) * p.K + split) * RS;
+    for (uint32_t e = tid; e < outs; e += kThreads) {
+        const uint32_t r = e / D, ch = e % D;
+        float* at = rec_base + (size_t)r * p.K * RS + 4 + ch;
+        const float v = summed(e);
+        if constexpr (MODE == 1) store_coherent(at, v);
+        else *at = v;
+    }
+    if ((uint32_t)tid < G) {
+        float M, L;
+        row_stats(tid, M, L);
+        float* rec = rec_base + (size_t)tid * p.K * RS;
+        const float hdr[4] = {M == -INFINITY ? kMasked : M * kLn2, L, 0.0f, 0.0f};
 #pragma unroll
-                    for (int b = 0; b < NB; ++b) put_rec(4 + 16 * b + n, acc[b][i]);
-                    if (n == 0) {
-                        put_rec(0, Mrow[i] == kMasked ? kMasked : Mrow[i] * kLn2);
-                        put_rec(1, Lrow[i]);
-                        put_rec(2, 0.0f);
-                        put_rec(3, 0.0f);
-                    }
-                }
-            }
+        for (int k = 0; k < 4; ++k) {
+            if constexpr (MODE == 1) store_coherent(rec + k, hdr[k]);
+            else rec[k] = hdr[k];
         }
     }
     if constexpr (MODE == 0) return;
 
-    float* rows = region;  // normalised rows [G][D] for the egress
-    if (local) {
-        lds_barrier();  // wave 0 finished reading slot0
-        if (wave == 0) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const uint32_t r = 4 * kg + i;
-                if (r < G) {
-                    const float L = Lrow[i];
-#pragma unroll
-                    for (int b = 0; b < NB; ++b)
-                        rows[r * D + 16 * b + n] = L == 0.0f ? 0.0f : acc[b][i] / L;
-                }
-            }
-        }
-        lds_barrier();
-    } else {
-        // ---- the last workgroup of this (seq, kv head) to arrive combines.
-        // The records went out as device-coherent stores; waiting for their
-        // completion before the increment publishes them (release), and the
-        // last arriver reads them with device-coherent loads (acquire).
-        __builtin_amdgcn_s_waitcnt(0);
-        __syncthreads();
-        if (tid == 0) {
-            uint32_t* ctr = p.counters + (size_t)seq * p.Hkv + kvh;
-            const uint32_t old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED,
-                                                        __HIP_MEMORY_SCOPE_AGENT);
-            const int last = old == p.K - 1;
-            if (last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            *flag = last;
-        }
-        __syncthreads();
-        if (!*flag) return;
-        float* w = region;
-        float* lk = region + (size_t)G * p.K;
-        rows = lk + (size_t)G * p.K;
-        combine_rows<D, true>(p.records + ((size_t)seq * p.Hq + (size_t)kvh * G) * p.K * RS,
-                        (size_t)p.K * RS, G, p.K, w, lk, ML, rows);
+    // ---- the last workgroup of this (seq, kv head) to arrive combines. The
+    // records went out as device-coherent stores; waiting for their
+    // completion before the increment publishes them (release), and the last
+    // arriver reads them with device-coherent loads (acquire).
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tid == 0) {
+        uint32_t* ctr = p.counters + (size_t)seq * p.Hkv + kvh;
+        const uint32_t old =
+            __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int last = old == p.K - 1;
+        if (last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        *flag = last;
     }
+    __syncthreads();
+    if (!*flag) return;
     for (uint32_t g = wave; g < G; g += kWaves) {
         const size_t qh = (size_t)seq * p.Hq + kvh * G + g;
-        egress_row<D>(rows + g * D, p.pi_signs, p.gate ? p.gate + qh * D : nullptr,
-                      p.out + qh * D, p.inv_sqrt_len, p.output_stage, lane);
+        float v[CPL];
+        combine_row<D, true>(p.records + qh * p.K * RS, p.K, lane, v);
+        egress_regs<D>(v, p.pi_signs, p.gate ? p.gate + qh * D : nullptr, p.out + qh * D,
+                       p.inv_sqrt_len, p.output_stage, lane);
     }
 }
 
-// Stand-alone combine: 16 consecutive (seq, q head) rows per workgroup.
+// Stand-alone combine: 16 consecutive (seq, q head) rows per workgroup, four
+// per wave.
 template <int D>
 __global__ __launch_bounds__(kThreads) void combine_kernel(DecodeParams p)
 {
-    extern __shared__ float smem[];
+    constexpr int CPL = D / 64;
     const size_t total = (size_t)p.B * p.Hq;
-    const size_t row0 = (size_t)blockIdx.x * 16;
-    const uint32_t nrows = (uint32_t)((total - row0) < 16 ? (total - row0) : 16);
-    float* ML = smem;
-    float* w = smem + 32;
-    float* lk = w + (size_t)16 * p.K;
-    float* rows = lk + (size_t)16 * p.K;
-    combine_rows<D, false>(p.records + row0 * p.K * (D + 4), (size_t)p.K * (D + 4), nrows, p.K, w, lk,
-                    ML, rows);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    for (uint32_t r = wave; r < nrows; r += kWaves) {
-        const size_t row = row0 + r;
-        egress_row<D>(rows + r * D, p.pi_signs, p.gate ? p.gate + row * D : nullptr,
-                      p.out + row * D, p.inv_sqrt_len, p.output_stage, lane);
+    for (int i = 0; i < 4; ++i) {
+        const size_t row = (size_t)blockIdx.x * 16 + wave + kWaves * i;
+        if (row >= total) break;
+        float v[CPL];
+        combine_row<D, false>(p.records + row * p.K * (D + 4), p.K, lane, v);
+        egress_regs<D>(v, p.pi_signs, p.gate ? p.gate + row * D : nullptr, p.out + row * D,
+                       p.inv_sqrt_len, p.output_stage, lane);
     }
 }
 
@@ -652,8 +740,7 @@ template <int D>
 hipError_t launch_decode_t(hipStream_t stream, const DecodeParams& p, int mode)
 {
     const size_t blocks = (size_t)p.B * p.Hkv * p.K;
-    const uint32_t comb_k = (mode == 1 && p.K > 1) ? p.K : 0u;
-    const size_t lds = (kHdrFloats + region_floats(p.G, D, comb_k)) * sizeof(float);
+    const size_t lds = (kHdrFloats + TQ4_MAX_SPLIT_STRIPS + region_floats(p.G, D)) * sizeof(float);
     if (mode == 0)
         hipLaunchKernelGGL((decode_kernel<D, 0>), dim3((uint32_t)blocks), dim3(kThreads), lds,
                            stream, p);
@@ -668,8 +755,7 @@ hipError_t launch_combine_t(hipStream_t stream, const DecodeParams& p)
 {
     const size_t rows = (size_t)p.B * p.Hq;
     const uint32_t blocks = (uint32_t)((rows + 15) / 16);
-    const size_t lds = (32 + (size_t)32 * p.K + (size_t)16 * D) * sizeof(float);
-    hipLaunchKernelGGL((combine_kernel<D>), dim3(blocks), dim3(kThreads), lds, stream, p);
+    hipLaunchKernelGGL((combine_kernel<D>), dim3(blocks), dim3(kThreads), 0, stream, p);
     return hipGetLastError();
 }
 

@@ -32,8 +32,38 @@ __device__ __forceinline__ uint32_t f32_to_bf16(float f)
     return ((b + 0x7fffu + ((b >> 16) & 1u)) >> 16) & 0xffffu;
 }
 
-// Partner value `mask` lanes away inside the wave.
-__device__ __forceinline__ float xor_lanes(float v, int mask) { return __shfl_xor(v, mask, 64); }
+// Partner value `mask` lanes away inside the wave (mask a power of two < 64),
+// with VALU lane moves only: DPP inside a 16-lane row, permlane swaps across
+// rows. `mask` is a compile-time constant at every call site.
+__device__ __forceinline__ float dpp_move(float v, int ctrl_tag)
+{
+    const int x = __float_as_int(v);
+    int r;
+    switch (ctrl_tag) {
+        case 1: r = __builtin_amdgcn_update_dpp(x, x, 0xB1, 0xF, 0xF, true); break;   // quad_perm 1,0,3,2
+        case 2: r = __builtin_amdgcn_update_dpp(x, x, 0x4E, 0xF, 0xF, true); break;   // quad_perm 2,3,0,1
+        case 4: {
+            const int h = __builtin_amdgcn_update_dpp(x, x, 0x141, 0xF, 0xF, true);    // row_half_mirror
+            r = __builtin_amdgcn_update_dpp(h, h, 0x1B, 0xF, 0xF, true);             // quad_perm 3,2,1,0
+            break;
+        }
+        default: r = __builtin_amdgcn_update_dpp(x, x, 0x128, 0xF, 0xF, true); break; // row_ror:8
+    }
+    return __int_as_float(r);
+}
+
+__device__ __forceinline__ float xor_lanes(float v, int mask)
+{
+    if (mask < 16) return dpp_move(v, mask);
+    const uint32_t u = __float_as_uint(v);
+    const uint32_t lane = __lane_id();
+    if (mask == 16) {
+        const auto p = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+        return __uint_as_float((lane & 16u) ? p[0] : p[1]);
+    }
+    const auto p = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    return __uint_as_float((lane & 32u) ? p[0] : p[1]);
+}
 
 // One butterfly stage at `stride` over a row spread across lanes, CPL
 // consecutive channels per lane (channel = lane_in_row * CPL + j):

@@ -41,7 +41,7 @@ typedef enum {
     TQ4_ERR_GEOMETRY = -3,      /* zero heads/blocks, block_size % 16, GQA group */
     TQ4_ERR_PARTIAL_STRIP = -4, /* num_tokens not a whole number of strips */
     TQ4_ERR_SPLITS = -5,        /* num_splits out of range */
-    TQ4_ERR_WORKSPACE = -6,     /* workspace NULL or smaller than required */
+    TQ4_ERR_WORKSPACE = -6,     /* workspace NULL, smaller than required or not 16-byte aligned */
     TQ4_ERR_OUTPUT_STAGE = -7,  /* output_stage > 2, or stage 2 without gate */
     TQ4_ERR_ROTATION = -8,      /* neither pi_signs nor tables given */
     TQ4_ERR_LAUNCH = -9,        /* the HIP runtime refused the launch */
@@ -139,9 +139,12 @@ int tq4_reshape_scatter(void* stream, uint32_t block_dim, const uint16_t* key,
  */
 #define TQ4_DECODE_QUERY_ROTATED 1u
 #define TQ4_MAX_SPLITS 256u
-/* A split owns at most this many block-table pages: num_splits must be at
- * least ceil(max_blocks_per_seq / TQ4_MAX_SPLIT_PAGES) (TQ4_ERR_SPLITS). */
-#define TQ4_MAX_SPLIT_PAGES 1024u
+/* A split walks at most this many 16-token strips (its block-table window is
+ * staged on chip): num_splits must be at least
+ * ceil(max_blocks_per_seq * block_size / 16 / TQ4_MAX_SPLIT_STRIPS)
+ * (TQ4_ERR_SPLITS). The cache must hold fewer than 2^32 (page, head, token)
+ * rows: num_blocks * num_kv_heads * block_size < 2^32 (TQ4_ERR_RANGE). */
+#define TQ4_MAX_SPLIT_STRIPS 2048u
 
 /* Workspace bytes for num_splits (partial records plus the per-(seq, kv
  * head) arrival counters of the fused entry). */

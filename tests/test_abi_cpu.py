@@ -67,7 +67,7 @@ def test_decode_refusals_and_sizes(lib):
     assert call(Hq=8 * 17) == -3             # GQA group > 16
     assert call(S=8) == -3
     assert call(K=300) == -5
-    assert call(K=1, maxb=2048) == -5        # a split may own at most 1024 pages
+    assert call(K=1, maxb=4096) == -5        # a split may walk at most 2048 strips
     assert call(K=4) == -6                   # no workspace
     assert call(K=4, ws=d, wsb=100) == -6    # too small
     assert call(K=1, stage=3) == -7
@@ -75,8 +75,8 @@ def test_decode_refusals_and_sizes(lib):
     need = lib.tq4_decode_workspace_bytes(1, 32, 8, 128, 4)
     assert need >= 1 * 32 * 4 * (128 + 4) * 4 + 8 * 4
     k = lib.tq4_decode_auto_splits(1, 8, 256, 16)
-    assert 1 <= k <= 256 and (256 + k - 1) // k <= 1024
-    assert lib.tq4_decode_auto_splits(1, 1, 4096, 16) >= 4   # 4096 pages need >= 4 splits
+    assert 1 <= k <= 256 and (256 + k - 1) // k <= 2048
+    assert lib.tq4_decode_auto_splits(1, 1, 8192, 16) >= 4   # 8192 strips need >= 4 splits
     comb = lib.tq4_splitk_combine
     assert comb(None, d, d, None, d, 1, 32, 128, 0, 0.1, 1) == -5
     assert comb(None, d, d, None, d, 1, 32, 128, 4, 0.1, 2) == -7
