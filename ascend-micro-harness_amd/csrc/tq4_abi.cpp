@@ -138,20 +138,24 @@ size_t tq4_decode_workspace_bytes(uint32_t num_seqs, uint32_t num_heads, uint32_
 uint32_t tq4_decode_auto_splits(uint32_t num_seqs, uint32_t num_kv_heads,
                                 uint32_t max_blocks_per_seq, uint32_t block_size)
 {
-    // Enough workgroups for every CU several times over (256 CUs), but at
-    // least ~8 strips per workgroup so a split is not all prologue.
-    const uint64_t items = (uint64_t)num_seqs * num_kv_heads;
-    const uint64_t target_wgs = 1024;
-    uint64_t k = items == 0 ? 1 : (target_wgs + items - 1) / items;
+    // Splits of ~64 strips (32 MFMA pairs over four waves), enough
+    // workgroups to fill every CU's two slots (256 CUs), but never fewer than
+    // 16 strips per split (the combine and the prologue stay a small share),
+    // and at most 64 splits (one or two record chunks per combine). Splits
+    // past a short sequence's end cost a single context-length load.
     const uint64_t strips = (uint64_t)max_blocks_per_seq * (block_size / kStrip);
-    uint64_t by_len = strips / 8;
-    if (by_len < 1) by_len = 1;
+    const uint64_t items = (uint64_t)num_seqs * num_kv_heads;
+    uint64_t k = (strips + 63) / 64;
+    const uint64_t fill = items == 0 ? 1 : (512 + items - 1) / items;
+    if (k < fill) k = fill;
+    const uint64_t by_len = strips / 16 > 0 ? strips / 16 : 1;
     if (k > by_len) k = by_len;
-    if (k > TQ4_MAX_SPLITS) k = TQ4_MAX_SPLITS;
-    if (k < 1) k = 1;
+    if (k > 64) k = 64;
     // one split stages at most TQ4_MAX_SPLIT_STRIPS strips of its window
     const uint64_t k_min = (strips + TQ4_MAX_SPLIT_STRIPS - 1) / TQ4_MAX_SPLIT_STRIPS;
     if (k < k_min) k = k_min;
+    if (k > TQ4_MAX_SPLITS) k = TQ4_MAX_SPLITS;
+    if (k < 1) k = 1;
     return (uint32_t)k;
 }
 

@@ -154,15 +154,11 @@ __device__ __forceinline__ void load_row_chunk(uint32_t (&k)[D / 32], const int8
     }
 }
 
-// Record traffic between workgroups of one launch: agent-scope relaxed
-// atomic stores, read back by buffer loads with the device-coherence bit
-// (sc1, what an agent-scope atomic load is on gfx950) -- plain loads to the
-// compiler, so a whole chunk of them is in flight at once. No whole-L2
+// Record traffic between workgroups of one launch: buffer stores and loads
+// with the device-coherence bit (sc1 -- what agent-scope relaxed atomic
+// stores and loads are on gfx950), plain accesses to the compiler, so they
+// vectorise and a whole chunk of loads is in flight at once. No whole-L2
 // write-back or invalidate is needed around the arrival counter.
-__device__ __forceinline__ void store_coherent(float* p, float v)
-{
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 
 constexpr int kCachePolicySc1 = 16;  // cache-policy operand bit of sc1
 
@@ -170,6 +166,15 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t records_rsrc(const float* base
 {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), (short)0, 0x7fffffff,
                                              0x00020000);
+}
+
+template <bool COHERENT>
+__device__ __forceinline__ void rec_store4(__amdgpu_buffer_rsrc_t r, uint32_t byte_off, float4 v)
+{
+    typedef uint32_t u4v __attribute__((ext_vector_type(4)));
+    const u4v u = u4v{__float_as_uint(v.x), __float_as_uint(v.y), __float_as_uint(v.z),
+                      __float_as_uint(v.w)};
+    __builtin_amdgcn_raw_buffer_store_b128(u, r, byte_off, 0, COHERENT ? kCachePolicySc1 : 0);
 }
 
 template <bool COHERENT>
@@ -222,18 +227,21 @@ __device__ void combine_row(const float* rr, uint32_t K, int lane, float (&out)[
                 }
             }
         }
+        // log2 domain: w = exp(m_k - M) = exp2((m_k - M) * log2(e))
         float Mc = M;
 #pragma unroll
-        for (int i = 0; i < KC; ++i)
+        for (int i = 0; i < KC; ++i) {
+            mk[i] *= kLog2e;
             if ((uint32_t)i < kn) Mc = fmaxf(Mc, mk[i]);
-        const float s = M == -INFINITY ? 0.0f : expf(M - Mc);
+        }
+        const float s = M == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(M - Mc);
         L *= s;
 #pragma unroll
         for (int c = 0; c < CPL; ++c) a[c] *= s;
 #pragma unroll
         for (int i = 0; i < KC; ++i) {
             if ((uint32_t)i < kn) {
-                const float w = expf(mk[i] - Mc);
+                const float w = __builtin_amdgcn_exp2f(mk[i] - Mc);
                 L += lk[i] * w;
 #pragma unroll
                 for (int c = 0; c < CPL; ++c) a[c] += w * ak[i][c];
@@ -291,6 +299,7 @@ void decode_kernel(DecodeParams p)
     float* l_x = smem + 64;                  // [4][16]
     int* q_exp = (int*)(smem + 128);         // [16]
     int* flag = (int*)(smem + 144);
+    float* u_x = smem + 148;                 // [4] per-wave 2^-sh
     uint32_t* strip_lds = (uint32_t*)(smem + kHdrFloats);  // [TQ4 max split strips]
     float* region = smem + kHdrFloats + TQ4_MAX_SPLIT_STRIPS;
 
@@ -338,6 +347,32 @@ void decode_kernel(DecodeParams p)
     if (pc > 0 && ctx > tok0) {
         const uint64_t l = ctx - tok0;
         ltok = l < (uint64_t)pc * S ? (uint32_t)l : pc * S;
+    }
+    // Fused entry: splits past the context hold no live token. They publish
+    // nothing -- the arrival count is the number of non-empty splits,
+    // ceil(ceil(ctx / S) / width), which every workgroup of the sequence
+    // derives from ctx alone -- and leave at once.
+    uint32_t k_live = p.K;
+    if constexpr (MODE == 1) {
+        if (p.K > 1) {
+            const uint32_t width = (p.max_blocks + p.K - 1) / p.K;
+            const uint32_t ctx_pages = (uint32_t)(((uint64_t)ctx + S - 1) / S);
+            k_live = (ctx_pages + width - 1) / width;
+            if (split >= k_live) {
+                if (k_live == 0 && split == 0) {
+                    // empty context: the normalised context is 0 (l = 0)
+                    for (uint32_t g = wave; g < G; g += kWaves) {
+                        float v[CPL];
+#pragma unroll
+                        for (int j = 0; j < CPL; ++j) v[j] = 0.0f;
+                        const size_t qh = (size_t)seq * p.Hq + kvh * G + g;
+                        egress_regs<D>(v, p.pi_signs, p.gate ? p.gate + qh * D : nullptr,
+                                       p.out + qh * D, p.inv_sqrt_len, p.output_stage, lane);
+                    }
+                }
+                return;
+            }
+        }
     }
     const uint32_t live_pages = (ltok + S - 1) / S;
     int bad = 0;
@@ -592,65 +627,66 @@ void decode_kernel(DecodeParams p)
         }
     }
 
-    // ---- merge the four waves. Per wave: l = row sum over the four lane
-    // groups; the true scale of l and acc is 2^-sh; the offset column comes
-    // off acc. Each wave scales its rows to the common row maximum and parks
-    // them in LDS; then all 256 threads sum the four copies of each output.
+    // ---- merge the four waves. Each parks its raw rows (offset column
+    // removed) and (m, l, 2^-sh) in LDS; then every output float4 combines
+    // the four copies with the row's common maximum.
     const float lsum = col_sum(lpart);
-    const float unscale = ldexpf(1.0f, -(int)sh);
     if (g4 == 0) {
         m_x[wave * 16 + n] = row_live ? m_used : -INFINITY;
-        l_x[wave * 16 + n] = lsum * unscale;
+        l_x[wave * 16 + n] = lsum;
     }
-    lds_barrier();
+    if (lane == 0) u_x[wave] = ldexpf(1.0f, -(int)sh);
     float* part = region;  // [kWaves][G][D]
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const int r = 4 * g4 + i;
-        float M = m_x[r];
-#pragma unroll
-        for (int w = 1; w < kWaves; ++w) M = fmaxf(M, m_x[w * 16 + r]);
-        const float mine = m_x[wave * 16 + r];
-        const float f = (M == -INFINITY || mine == -INFINITY)
-                            ? 0.0f
-                            : __builtin_amdgcn_exp2f(mine - M) * (kCodeUnit * unscale);
-        if ((uint32_t)r < G) {
+        const uint32_t r = 4 * g4 + i;
+        if (r < G) {
             float* dst = part + ((size_t)wave * G + r) * D + n;
 #pragma unroll
-            for (int b = 0; b < NB; ++b) dst[16 * b] = (acc[b][i] - cr[i]) * f;
+            for (int b = 0; b < NB; ++b) dst[16 * b] = acc[b][i] - cr[i];
         }
     }
     lds_barrier();
-    // Row totals (every thread of a row reads the same four (m, l) pairs).
-    auto row_stats = [&](uint32_t r, float& M, float& L) {
+    // Per-wave weights of row r (exp2(m_w - M) * 2^-sh_w), the row's M and L.
+    auto row_weights = [&](uint32_t r, float (&f)[kWaves], float& M, float& L) {
         M = m_x[r];
 #pragma unroll
         for (int w = 1; w < kWaves; ++w) M = fmaxf(M, m_x[w * 16 + r]);
         L = 0.0f;
-        if (M != -INFINITY) {
 #pragma unroll
-            for (int w = 0; w < kWaves; ++w) {
-                const float mw = m_x[w * 16 + r];
-                if (mw != -INFINITY) L += __builtin_amdgcn_exp2f(mw - M) * l_x[w * 16 + r];
-            }
+        for (int w = 0; w < kWaves; ++w) {
+            const float mw = m_x[w * 16 + r];
+            f[w] = (M == -INFINITY || mw == -INFINITY) ? 0.0f
+                                                        : __builtin_amdgcn_exp2f(mw - M) * u_x[w];
+            L += l_x[w * 16 + r] * f[w];
         }
     };
-    const uint32_t outs = G * D;
-    auto summed = [&](uint32_t e) {
-        float v = part[e];
+    const uint32_t outs4 = G * D / 4;  // float4 outputs
+    auto combined4 = [&](uint32_t e4, const float (&f)[kWaves]) {
+        float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
-        for (int w = 1; w < kWaves; ++w) v += part[(size_t)w * outs + e];
+        for (int w = 0; w < kWaves; ++w) {
+            const float4 x = *(const float4*)(part + (size_t)w * G * D + 4 * e4);
+            const float fw = f[w] * kCodeUnit;
+            v.x += x.x * fw;
+            v.y += x.y * fw;
+            v.z += x.z * fw;
+            v.w += x.w * fw;
+        }
         return v;
     };
 
     const bool local = (MODE == 1) && p.K == 1;
     if (local) {
-        // ---- one split: normalise in place (wave-0 slice), then the egress.
-        for (uint32_t e = tid; e < outs; e += kThreads) {
-            float M, L;
-            row_stats(e / D, M, L);
-            const float v = summed(e);
-            part[e] = L == 0.0f ? 0.0f : v / L;  // part[0..outs) is read only by this thread
+        // ---- one split: normalise into the wave-0 slice, then the egress.
+        for (uint32_t e4 = tid; e4 < outs4; e4 += kThreads) {
+            float f[kWaves], M, L;
+            row_weights(4 * e4 / D, f, M, L);
+            float4 v = combined4(e4, f);
+            const float inv = L == 0.0f ? 0.0f : 1.0f / L;
+            v = L == 0.0f ? make_float4(0.0f, 0.0f, 0.0f, 0.0f)
+                          : make_float4(v.x * inv, v.y * inv, v.z * inv, v.w * inv);
+            *(float4*)(part + 4 * e4) = v;  // read above only by this thread
         }
         lds_barrier();
         for (uint32_t g = wave; g < G; g += kWaves) {
@@ -665,23 +701,18 @@ void decode_kernel(DecodeParams p)
     }
 
     // ---- export one record per q head: [m (natural log), l, 0, 0, acc].
-    float* rec_base = p.records + (((size_t)seq * p.Hq + (size_t)kvh * G) * p.K + split) * RS;
-    for (uint32_t e = tid; e < outs; e += kThreads) {
-        const uint32_t r = e / D, ch = e % D;
-        float* at = rec_base + (size_t)r * p.K * RS + 4 + ch;
-        const float v = summed(e);
-        if constexpr (MODE == 1) store_coherent(at, v);
-        else *at = v;
-    }
-    if ((uint32_t)tid < G) {
-        float M, L;
-        row_stats(tid, M, L);
-        float* rec = rec_base + (size_t)tid * p.K * RS;
-        const float hdr[4] = {M == -INFINITY ? kMasked : M * kLn2, L, 0.0f, 0.0f};
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            if constexpr (MODE == 1) store_coherent(rec + k, hdr[k]);
-            else rec[k] = hdr[k];
+    {
+        const __amdgpu_buffer_rsrc_t rsrc = records_rsrc(
+            p.records + (((size_t)seq * p.Hq + (size_t)kvh * G) * p.K + split) * RS);
+        const uint32_t row_bytes = p.K * RS * 4u;
+        for (uint32_t e4 = tid; e4 < outs4; e4 += kThreads) {
+            const uint32_t r = 4 * e4 / D, ch = 4 * e4 % D;
+            float f[kWaves], M, L;
+            row_weights(r, f, M, L);
+            rec_store4<MODE == 1>(rsrc, r * row_bytes + (4 + ch) * 4u, combined4(e4, f));
+            if (ch == 0)
+                rec_store4<MODE == 1>(rsrc, r * row_bytes,
+                                      make_float4(M == -INFINITY ? kMasked : M * kLn2, L, 0.0f, 0.0f));
         }
     }
     if constexpr (MODE == 0) return;
@@ -696,7 +727,7 @@ void decode_kernel(DecodeParams p)
         uint32_t* ctr = p.counters + (size_t)seq * p.Hkv + kvh;
         const uint32_t old =
             __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const int last = old == p.K - 1;
+        const int last = old == k_live - 1;
         if (last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         *flag = last;
     }
@@ -705,7 +736,7 @@ void decode_kernel(DecodeParams p)
     for (uint32_t g = wave; g < G; g += kWaves) {
         const size_t qh = (size_t)seq * p.Hq + kvh * G + g;
         float v[CPL];
-        combine_row<D, true>(p.records + qh * p.K * RS, p.K, lane, v);
+        combine_row<D, true>(p.records + qh * p.K * RS, k_live, lane, v);
         egress_regs<D>(v, p.pi_signs, p.gate ? p.gate + qh * D : nullptr, p.out + qh * D,
                        p.inv_sqrt_len, p.output_stage, lane);
     }

@@ -1,21 +1,30 @@
 #!/usr/bin/env python3
 """Benchmark of the TQ4 quantised-KV hot path on one MI355X.
 
-Workload (the metric's "@ctx4096"): single-sequence
-TQ4 paged decode, batch 1, 32 q heads : 8 kv heads, head_dim 128, ctx 4096,
-page 16, random block table from a 4096-page pool, scale 1/sqrt(128); the
-cache is prefilled through the GPU reshape_and_cache from N(0,1) BF16 K/V.
-A step is one fused decode launch (partials + last-workgroup LSE combine +
-inverse rotation + BF16 store). Cold cache by default: a 1 GiB buffer is
-rewritten between steps (outside the timed events) so the 256 MiB Infinity
-Cache holds nothing of the working set; each decode is bracketed by HIP
-events on the launch stream and value = algorithmic bytes / mean decode time.
+Headline workload (the metric's "@ctx4096"):
+single-sequence TQ4 paged decode -- batch 1, 32 q heads : 8 kv heads,
+head_dim 128, ctx 4096, page 16, random block table, scale 1/sqrt(128). A
+step is one fused decode launch (split-K partials + last-workgroup LSE
+combine + inverse rotation + BF16 store). The cache is prefilled through the
+GPU reshape_and_cache from N(0,1) BF16 K/V.
 
-Also reported: reshape_and_cache tokens/s on BASELINE config 2 (1024 BF16
-tokens, 4096-page pool, permuted pages), and the CPU baseline -- the C
-oracle's decode of the same workload on the host cores (kind "port").
+Cold reads without a flush kernel: SLICES independent config-3 sequences
+(each its own 256 random pages of one shared pool, its own q) are decoded in
+turn, so a sequence's 4.47 MB is read again only after SLICES-1 others
+(572 MB, more than the 256 MiB Infinity Cache) have been. The timed steps are
+captured once in a HIP graph and replayed back to back; HIP events on the
+launch stream bracket the replays, so ms_per_step is the average launch
+duration including the dispatch gap between consecutive kernels.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--cache cold|warm]
+Also reported: reshape_and_cache tokens/s on BASELINE configs[1] (1024 BF16
+tokens into a 4096-page pool, seeded page permutation), the batched decode
+step of configs[4] (64 sequences, ctx ~U[512, 8192]), and the CPU baseline:
+the C oracle's decode of the same sequence on the host cores (kind "port").
+
+Usage:
+  python bench.py [--gpus 1] [--steps K] [--warmup W]
+  python bench.py --pmc-run            # workload for rocprofv3 --pmc passes
+  python bench.py --summarize-pmc FETCH_DB WRITE_DB   # -> profiles/*traffic*
 """
 from __future__ import annotations
 
@@ -32,8 +41,15 @@ REPO = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, REPO)
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, published
+METRIC = "TQ4 paged decode µs + HBM GB/s (% peak) @ctx4096; reshape_and_cache tokens/s"
 
-B, HQ, HKV, D, S, CTX, POOL = 1, 32, 8, 128, 16, 4096, 4096
+B, HQ, HKV, D, S, CTX = 1, 32, 8, 128, 16, 4096
+PAGES = CTX // S
+SLICES = 128
+SEED = 0x71340003
+CALIB_BYTES = 64 << 20  # plain copy (x * 2) of known size for the PMC scale factors
+TRAFFIC_FILE = os.path.join(REPO, "profiles", "decode_config3_traffic.json")
+DECODE_KERNEL = "decode_kernel<128, 1>"
 
 
 def log(*a):
@@ -41,8 +57,8 @@ def log(*a):
 
 
 def decode_algorithmic_bytes(ctx_lens, hq, hkv, d, s):
-    """Bytes the contract forces across HBM for one decode step: K+V nibbles
-    and both FP32 scales of every live token, the block-table entries, the
+    """Bytes the contract forces across HBM for one decode: K+V nibbles and
+    both FP32 scales of every live token, the block-table entries, the
     context lengths, q and out (BF16)."""
     per_token = hkv * (d + 8)  # d/2 key + d/2 value bytes + 2 x 4-byte scales per kv head
     kv = sum(ctx_lens) * per_token
@@ -56,20 +72,157 @@ def writer_algorithmic_bytes(tokens, hkv, d, in_bytes):
     return tokens * (2 * hkv * d * in_bytes + hkv * d + 2 * hkv * 4 + 4)
 
 
+# ---------------------------------------------------------------- PMC summary
+def _pmc_per_dispatch(db, counter):
+    """Mean value of `counter` per dispatch, by kernel name (rocprofv3 db)."""
+    import sqlite3
+    con = sqlite3.connect(db)
+    cols = {r[1] for r in con.execute("pragma table_info(counters_collection)")}
+    name_col = "kernel_name" if "kernel_name" in cols else "name"
+    q = (f"select {name_col}, avg(value) , count(*) from counters_collection "
+         f"where counter_name = ? group by {name_col}")
+    rows = list(con.execute(q, (counter,)))
+    con.close()
+    return {r[0]: (float(r[1]), int(r[2])) for r in rows}
+
+
+def summarize_pmc(fetch_db, write_db):
+    """FETCH_SIZE / WRITE_SIZE (KiB per dispatch) of the decode kernel, each
+    scaled by what the counter reads for a plain copy of CALIB_BYTES."""
+    fetch = _pmc_per_dispatch(fetch_db, "FETCH_SIZE")
+    write = _pmc_per_dispatch(write_db, "WRITE_SIZE")
+
+    def pick(tab, key):
+        hits = [(k, v) for k, v in tab.items() if key in k]
+        if not hits:
+            raise SystemExit(f"no kernel matching {key!r} in {sorted(tab)}")
+        return hits[0]
+
+    dn, (dec_f, nf) = pick(fetch, "decode_kernel")
+    _, (dec_w, nw) = pick(write, "decode_kernel")
+    cn, (cp_f, _) = pick(fetch, "MulFunctor")
+    _, (cp_w, _) = pick(write, "MulFunctor")
+    f_scale = CALIB_BYTES / (cp_f * 1024.0)
+    w_scale = CALIB_BYTES / (cp_w * 1024.0)
+    fetch_b = dec_f * 1024.0 * f_scale
+    write_b = dec_w * 1024.0 * w_scale
+    out = {"kernel": dn, "dispatches": [nf, nw], "fetch_kib_raw": dec_f, "write_kib_raw": dec_w,
+           "calib_kernel": cn, "calib_bytes": CALIB_BYTES, "fetch_scale": f_scale,
+           "write_scale": w_scale, "fetch_bytes": fetch_b, "write_bytes": write_b,
+           "traffic_bytes": fetch_b + write_b,
+           "algorithmic_bytes": decode_algorithmic_bytes([CTX], HQ, HKV, D, S)}
+    os.makedirs(os.path.dirname(TRAFFIC_FILE), exist_ok=True)
+    with open(TRAFFIC_FILE, "w") as f:
+        json.dump(out, f, indent=1)
+    print(json.dumps(out))
+
+
+def read_traffic():
+    try:
+        with open(TRAFFIC_FILE) as f:
+            return json.load(f)
+    except (OSError, ValueError):
+        return None
+
+
+# -------------------------------------------------------------------- workload
+class Workload:
+    """SLICES config-3 sequences in one page pool, prefilled on the GPU."""
+
+    def __init__(self, tq4, torch, dev, slices):
+        self.tq4, self.torch = tq4, torch
+        rng = np.random.default_rng(SEED)
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(SEED)
+        self.slices = slices
+        self.pool = slices * PAGES
+        pool = self.pool
+        self.signs_np = np.where(rng.random(D) < 0.5, -1.0, 1.0).astype(np.float32)
+        self.signs = torch.from_numpy(self.signs_np).to(dev)
+        self.isl = 1.0 / math.sqrt(D)
+        self.scale = 1.0 / math.sqrt(D)
+        nbytes = pool * HKV * S * D // 2
+        self.kc = torch.zeros(nbytes, dtype=torch.int8, device=dev)
+        self.vc = torch.zeros(nbytes, dtype=torch.int8, device=dev)
+        self.sc = torch.zeros(2 * pool * HKV * S, dtype=torch.float32, device=dev)
+        perm = rng.permutation(pool).astype(np.int32).reshape(slices, PAGES)
+        self.tables = [torch.from_numpy(perm[i][None, :].copy()).to(dev) for i in range(slices)]
+        ar = torch.arange(S, device=dev, dtype=torch.int32)
+        for i in range(slices):
+            slots = (self.tables[i][0][:, None] * S + ar[None, :]).reshape(-1).contiguous()
+            k = torch.randn((CTX, HKV, D), generator=gen, device=dev).to(torch.bfloat16)
+            v = torch.randn((CTX, HKV, D), generator=gen, device=dev).to(torch.bfloat16)
+            tq4.reshape_and_cache_bf16(k, v, self.kc, self.vc, self.sc, slots,
+                                       pi_signs=self.signs, num_blocks=pool, block_size=S,
+                                       inv_sqrt_len=self.isl)
+        self.ctx = torch.tensor([CTX], dtype=torch.int32, device=dev)
+        self.q = [torch.randn((B, HQ, D), generator=gen, device=dev).to(torch.bfloat16)
+                  for _ in range(slices)]
+        self.out = torch.empty((B, HQ, D), dtype=torch.bfloat16, device=dev)
+        self.splits = tq4.auto_splits(B, HKV, PAGES, S)
+        self.ws = tq4.decode_workspace(B, HQ, HKV, D, self.splits)
+
+    def decode(self, i, out=None):
+        tq4 = self.tq4
+        tq4.paged_decode(self.q[i], self.kc, self.vc, self.sc, self.tables[i], self.ctx,
+                         self.signs, HKV, S, self.pool, out=self.out if out is None else out,
+                         workspace=self.ws, num_splits=self.splits, scale=self.scale,
+                         inv_sqrt_len=self.isl)
+
+
+def graph_time(torch, fns, steps, warmup):
+    """Capture fns (a list of launch closures) once in a HIP graph, replay it
+    until `steps` launches have run, and time the replays with events on the
+    launch stream. Returns (ms per launch, wall seconds of the timed region)."""
+    n = len(fns)
+    reps = max(1, steps // n)
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        for _ in range(max(1, warmup // n)):
+            for f in fns:
+                f()
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        for f in fns:
+            f()
+    g.replay()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    with torch.cuda.stream(stream):
+        e0.record(stream)
+        for _ in range(reps):
+            g.replay()
+        e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    return e0.elapsed_time(e1) / (reps * n), wall, reps * n
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--cache", choices=("cold", "warm"), default="cold")
-    ap.add_argument("--splits", type=int, default=0, help="0 = auto")
+    ap.add_argument("--steps", type=int, default=1024)
+    ap.add_argument("--warmup", type=int, default=128)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-extra", action="store_true", help="headline decode only")
+    ap.add_argument("--pmc-run", action="store_true",
+                    help="a few cold decodes plus a plain copy of known size, for rocprofv3 --pmc")
+    ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DB", "WRITE_DB"))
     args = ap.parse_args()
 
+    if args.summarize_pmc:
+        summarize_pmc(*args.summarize_pmc)
+        return
     if args.gpus != 1:
-        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the TQ4 path is "
-              "single-GPU in this build and no multi-GPU figure is produced.", file=sys.stderr)
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}): the TQ4 path is "
+              "built and measured on a single MI355X; no multi-GPU figure is produced.",
+              file=sys.stderr)
         sys.exit(2)
 
     import torch
@@ -78,143 +231,186 @@ def main():
     tq4 = __graft_entry__.package()
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    rng = np.random.default_rng(0x71340003)
-    gen = torch.Generator(device=dev)
-    gen.manual_seed(0x71340003)
 
-    # ---- cache: prefill ctx tokens of N(0,1) K/V through the GPU writer
-    signs_np = np.array([-1.0 if ((c * c + 3 * c + 1) % 7) < 3 else 1.0 for c in range(D)],
-                        np.float32)
-    signs = torch.from_numpy(signs_np).to(dev)
-    isl = 1.0 / math.sqrt(D)
-    scale = 1.0 / math.sqrt(D)
-    nbytes = POOL * HKV * S * D // 2
-    kc = torch.zeros(nbytes, dtype=torch.int8, device=dev)
-    vc = torch.zeros(nbytes, dtype=torch.int8, device=dev)
-    sc = torch.zeros(2 * POOL * HKV * S, dtype=torch.float32, device=dev)
-    pages = torch.from_numpy(rng.permutation(POOL)[: CTX // S].astype(np.int32)).to(dev)
-    slots = (pages[:, None] * S + torch.arange(S, device=dev, dtype=torch.int32)[None, :]).reshape(-1)
-    k_in = torch.randn((CTX, HKV, D), generator=gen, device=dev).to(torch.bfloat16)
-    v_in = torch.randn((CTX, HKV, D), generator=gen, device=dev).to(torch.bfloat16)
-    tq4.reshape_and_cache_bf16(k_in, v_in, kc, vc, sc, slots.contiguous(), pi_signs=signs,
-                               num_blocks=POOL, block_size=S, inv_sqrt_len=isl)
-    tables = pages[None, :].contiguous()
-    ctx = torch.tensor([CTX], dtype=torch.int32, device=dev)
-    q = torch.randn((B, HQ, D), generator=gen, device=dev).to(torch.bfloat16)
-    out = torch.empty_like(q)
-    splits = args.splits or tq4.auto_splits(B, HKV, tables.shape[1], S)
-    ws = tq4.decode_workspace(B, HQ, HKV, D, splits)
-    flush = torch.empty(1 << 30, dtype=torch.uint8, device=dev) if args.cache == "cold" else None
+    if args.pmc_run:
+        w = Workload(tq4, torch, dev, 32)
+        torch.cuda.synchronize()
+        for i in range(32):
+            w.decode(i)
+        src = torch.ones(CALIB_BYTES // 4, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        for _ in range(4):
+            torch.mul(src, 2.0, out=dst)  # the calibration copy: reads and writes CALIB_BYTES
+        torch.cuda.synchronize()
+        log("pmc workload done")
+        return
+
+    log(f"prefilling {SLICES} config-3 sequences ({SLICES * PAGES} pages)")
+    w = Workload(tq4, torch, dev, SLICES)
     torch.cuda.synchronize()
 
-    def decode():
-        tq4.paged_decode(q, kc, vc, sc, tables, ctx, signs, HKV, S, POOL, out=out, workspace=ws,
-                         num_splits=splits, scale=scale, inv_sqrt_len=isl)
+    # correctness gates: finite output, and the last graph replay (slice
+    # SLICES-1) bit-identical to an eager decode of the same slice
+    ref = torch.empty_like(w.out)
+    w.decode(SLICES - 1, out=ref)
+    torch.cuda.synchronize()
+    assert torch.isfinite(ref.float()).all(), "decode produced non-finite values"
 
-    def timed_steps(fn, steps, warmup):
-        for _ in range(warmup):
-            if flush is not None:
-                flush.zero_()
-            fn()
-        torch.cuda.synchronize()
-        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-              for _ in range(steps)]
-        t0 = time.perf_counter()
-        for e0, e1 in ev:
-            if flush is not None:
-                flush.zero_()
-            e0.record()
-            fn()
-            e1.record()
-        torch.cuda.synchronize()
-        wall = time.perf_counter() - t0
-        ms = np.array([e0.elapsed_time(e1) for e0, e1 in ev])
-        return ms, wall
-
-    log(f"decode: B={B} Hq={HQ} Hkv={HKV} d={D} ctx={CTX} splits={splits} cache={args.cache}")
-    ms, wall = timed_steps(decode, args.steps, args.warmup)
+    cold_ms, wall, nsteps = graph_time(torch, [lambda i=i: w.decode(i) for i in range(SLICES)],
+                                       args.steps, args.warmup)
+    torch.cuda.synchronize()
+    assert torch.equal(w.out.view(torch.int16), ref.view(torch.int16)), \
+        "graph replays changed the decode result"
+    warm_ms, _, _ = graph_time(torch, [lambda: w.decode(0)] * 64, 512, 64)
     dec_bytes = decode_algorithmic_bytes([CTX], HQ, HKV, D, S)
-    mean_ms = float(ms.mean())
-    gbs = dec_bytes / (mean_ms * 1e-3) / 1e9
-    log(f"decode: mean {mean_ms * 1e3:.2f} us  median {np.median(ms) * 1e3:.2f} us  "
-        f"min {ms.min() * 1e3:.2f} us  p99 {np.percentile(ms, 99) * 1e3:.2f} us  "
-        f"-> {gbs:.1f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f}% of HBM peak)")
+    gbs = dec_bytes / (cold_ms * 1e-3) / 1e9
+    log(f"decode cold: {cold_ms * 1e3:.2f} us/step -> {gbs:.1f} GB/s "
+        f"({100 * gbs / HBM_PEAK_GBS:.1f}% of HBM peak); warm {warm_ms * 1e3:.2f} us; "
+        f"splits={w.splits}")
 
-    # ---- reshape_and_cache rate, BASELINE config 2 (1024 BF16 tokens, permuted pages)
-    wt = 1024
-    w_pages = torch.from_numpy(rng.permutation(POOL)[: wt // S].astype(np.int32)).to(dev)
-    w_slots = (w_pages[:, None] * S + torch.arange(S, device=dev, dtype=torch.int32)[None, :]).reshape(-1).contiguous()
-    wk = torch.randn((wt, HKV, D), generator=gen, device=dev).to(torch.bfloat16)
-    wv = torch.randn((wt, HKV, D), generator=gen, device=dev).to(torch.bfloat16)
-    wkc, wvc, wsc = torch.zeros_like(kc), torch.zeros_like(vc), torch.zeros_like(sc)
+    extra = {}
+    if not args.no_extra:
+        extra = extra_workloads(tq4, torch, dev, w)
 
-    def write():
-        tq4.reshape_and_cache_bf16(wk, wv, wkc, wvc, wsc, w_slots, pi_signs=signs,
-                                   num_blocks=POOL, block_size=S, inv_sqrt_len=isl)
-
-    wms, _ = timed_steps(write, max(20, args.steps // 4), 5)
-    w_mean = float(wms.mean())
-    w_tps = wt / (w_mean * 1e-3)
-    w_gbs = writer_algorithmic_bytes(wt, HKV, D, 2) / (w_mean * 1e-3) / 1e9
-    log(f"reshape_and_cache: {wt} tokens mean {w_mean * 1e3:.2f} us -> {w_tps / 1e6:.1f} M tokens/s "
-        f"({w_gbs:.1f} GB/s)")
-
-    # ---- CPU baseline: the C oracle's decode of the same workload on host cores
     cpu = None
     if not args.no_cpu:
-        sys.path.insert(0, os.path.join(REPO, "tests"))
-        from oracle_bindings import Oracle
-        o = Oracle()
-        threads = min(16, os.cpu_count() or 1)
-        h_q = q.view(torch.int16).cpu().numpy().view(np.uint16)
-        h_kc, h_vc, h_sc = kc.cpu().numpy(), vc.cpu().numpy(), sc.cpu().numpy()
-        h_tab, h_ctx = tables.cpu().numpy(), ctx.cpu().numpy()
-        iters, t0 = 0, time.perf_counter()
-        while True:
-            o.paged_decode(h_q, h_kc, h_vc, h_sc, h_tab, h_ctx, signs_np, None, HQ, HKV, D, S,
-                           POOL, splits, np.float32(scale), np.float32(isl), 1, threads=threads)
-            iters += 1
-            el = time.perf_counter() - t0
-            if el >= args.cpu_seconds:
-                break
-        cpu_gbs = dec_bytes * iters / el / 1e9
-        cpu = {"value": round(cpu_gbs, 4), "unit": "GB/s", "cores": threads, "kind": "port",
-               "sample": f"{iters} config-3 decodes (B=1, 32q:8kv, d128, ctx4096, {splits} splits) "
-                         f"by oracle/tq4_oracle.c, {el:.1f} s, {threads} threads",
-               "us_per_decode": round(el / iters * 1e6, 1)}
+        cpu = cpu_baseline(torch, w, dec_bytes, args.cpu_seconds)
         log(f"cpu baseline: {cpu}")
 
+    traffic = read_traffic()
     result = {
-        "metric": "TQ4 paged decode µs + HBM GB/s (% peak) @ctx4096; reshape_and_cache tokens/s",
+        "metric": METRIC,
         "value": round(gbs, 2),
         "unit": "GB/s",
         "n_gpus": 1,
-        "steps": args.steps,
+        "steps": nsteps,
         "warmup": args.warmup,
-        "ms_per_step": round(mean_ms, 6),
+        "ms_per_step": round(cold_ms, 6),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "int4-cache/fp16-mfma/fp32-softmax",
+        "dtype": "int4 cache, fp16 MFMA operands, fp32 softmax/accumulate",
         "data": "synthetic: N(0,1) BF16 K/V quantised by the GPU writer, N(0,1) BF16 q, seeded",
-        "config": {"workload": "config3 single-sequence TQ4 paged decode",
-                   "batch": B, "q_heads": HQ, "kv_heads": HKV, "head_dim": D, "ctx": CTX,
-                   "page_size": S, "pool_pages": POOL, "splits": splits,
-                   "cache": args.cache, "parallelism": "single GPU"},
-        "decode_us": {"mean": round(mean_ms * 1e3, 3), "median": round(float(np.median(ms)) * 1e3, 3),
-                      "min": round(float(ms.min()) * 1e3, 3),
-                      "p99": round(float(np.percentile(ms, 99)) * 1e3, 3)},
+        "config": {"workload": "configs[2] single-sequence TQ4 paged decode", "batch": B,
+                   "q_heads": HQ, "kv_heads": HKV, "head_dim": D, "ctx": CTX, "page_size": S,
+                   "splits": w.splits, "cache": f"cold ({SLICES} rotated sequences)",
+                   "parallelism": "single GPU"},
+        "decode_us": {"cold": round(cold_ms * 1e3, 3), "warm": round(warm_ms * 1e3, 3)},
         "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
-        "reshape_and_cache": {"tokens": wt, "us": round(w_mean * 1e3, 3),
-                              "tokens_per_s": round(w_tps, 1), "GBps": round(w_gbs, 2)},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "decode_kernel<128,1> (fused)",
-                     "algorithmic_bytes": dec_bytes},
+                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                     "traffic": round(traffic["traffic_bytes"]) if traffic else None,
+                     "kernel": DECODE_KERNEL, "algorithmic_bytes": dec_bytes},
         "cpu_baseline": cpu,
         "wall_s_timed": round(wall, 3),
     }
+    result.update(extra)
     print(json.dumps(result), flush=True)
+
+
+def extra_workloads(tq4, torch, dev, w):
+    """reshape_and_cache tokens/s and the batched step."""
+    out = {}
+    rng = np.random.default_rng(0x71340002)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0x71340002)
+    # --- configs[1]: 1024 BF16 tokens, 4096-page pool, permuted pages; 32 input sets rotated
+    wt, pool, nin = 1024, 4096, 32
+    wkc = torch.zeros(pool * HKV * S * D // 2, dtype=torch.int8, device=dev)
+    wvc, wsc = torch.zeros_like(wkc), torch.zeros(2 * pool * HKV * S, device=dev)
+    ar = torch.arange(S, device=dev, dtype=torch.int32)
+    ins = []
+    for _ in range(nin):
+        pages = torch.from_numpy(rng.permutation(pool)[: wt // S].astype(np.int32)).to(dev)
+        slots = (pages[:, None] * S + ar[None, :]).reshape(-1).contiguous()
+        k = torch.randn((wt, HKV, D), generator=gen, device=dev).to(torch.bfloat16)
+        v = torch.randn((wt, HKV, D), generator=gen, device=dev).to(torch.bfloat16)
+        ins.append((k, v, slots))
+
+    def write(i):
+        k, v, slots = ins[i]
+        tq4.reshape_and_cache_bf16(k, v, wkc, wvc, wsc, slots, pi_signs=w.signs,
+                                   num_blocks=pool, block_size=S, inv_sqrt_len=w.isl)
+
+    wms, _, _ = graph_time(torch, [lambda i=i: write(i) for i in range(nin)], 512, 64)
+    wbytes = writer_algorithmic_bytes(wt, HKV, D, 2)
+    out["reshape_and_cache"] = {"workload": "configs[1] BF16 1024 tokens", "us": round(wms * 1e3, 3),
+                                "tokens_per_s": round(wt / (wms * 1e-3), 1),
+                                "GBps": round(wbytes / (wms * 1e-3) / 1e9, 2),
+                                "algorithmic_bytes": wbytes}
+    log(f"reshape_and_cache: {wms * 1e3:.2f} us -> {wt / (wms * 1e-3) / 1e6:.1f} M tokens/s")
+
+    # --- configs[4]: batched decode step, 64 sequences, ctx ~U[512, 8192]
+    r = np.random.default_rng(0x71340005)
+    ctxs = [int(x) for x in r.integers(512, 8193, 64)]
+    bsz = len(ctxs)
+    npages = [(c + 1 + S - 1) // S for c in ctxs]  # room for the step's new token
+    pool5 = int(sum(npages) * 1.1) + 16
+    maxb = max(npages)
+    perm = r.permutation(pool5).astype(np.int32)
+    tab = np.zeros((bsz, maxb), np.int32)
+    at = 0
+    for b, n in enumerate(npages):
+        tab[b, :n] = perm[at:at + n]
+        at += n
+    tables = torch.from_numpy(tab).to(dev)
+    kc5 = torch.randint(-128, 127, (pool5 * HKV * S * D // 2,), dtype=torch.int8, device=dev,
+                        generator=gen)
+    vc5 = torch.randint(-128, 127, kc5.shape, dtype=torch.int8, device=dev, generator=gen)
+    sc5 = torch.rand(2 * pool5 * HKV * S, device=dev, generator=gen) * 0.05 + 0.01
+    ctx_now = torch.tensor([c + 1 for c in ctxs], dtype=torch.int32, device=dev)
+    slot_np = np.array([tab[b, c // S] * S + c % S for b, c in enumerate(ctxs)], np.int32)
+    slots5 = torch.from_numpy(slot_np).to(dev)
+    q5 = torch.randn((bsz, HQ, D), generator=gen, device=dev).to(torch.bfloat16)
+    kn = torch.randn((bsz, HKV, D), generator=gen, device=dev).to(torch.bfloat16)
+    vn = torch.randn((bsz, HKV, D), generator=gen, device=dev).to(torch.bfloat16)
+    out5 = torch.empty_like(q5)
+    k5 = tq4.auto_splits(bsz, HKV, maxb, S)
+    ws5 = tq4.decode_workspace(bsz, HQ, HKV, D, k5)
+
+    def step():
+        tq4.reshape_scatter(kn, vn, kc5, vc5, sc5, slots5, w.signs, num_blocks=pool5,
+                            block_size=S, inv_sqrt_len=w.isl)
+        tq4.paged_decode(q5, kc5, vc5, sc5, tables, ctx_now, w.signs, HKV, S, pool5, out=out5,
+                         workspace=ws5, num_splits=k5, scale=w.scale, inv_sqrt_len=w.isl)
+
+    sms, _, _ = graph_time(torch, [step] * 8, 64, 16)
+    sbytes = decode_algorithmic_bytes([c + 1 for c in ctxs], HQ, HKV, D, S) + bsz * (
+        2 * HKV * D * 2 + HKV * D // 2 + 2 * HKV * 4 + 4) + bsz * HKV * 1024  # + value-strip RMW
+    out["batched_step"] = {"workload": "configs[4] 64 seqs ctx~U[512,8192]: scatter 64 tokens + "
+                                       "split-K decode", "us": round(sms * 1e3, 3),
+                           "tokens_per_s": round(bsz / (sms * 1e-3), 1),
+                           "GBps": round(sbytes / (sms * 1e-3) / 1e9, 2),
+                           "pct_hbm_peak": round(100 * sbytes / (sms * 1e-3) / 1e9 / HBM_PEAK_GBS, 2),
+                           "splits": k5, "algorithmic_bytes": sbytes, "cache": "warm (one step)"}
+    log(f"batched step: {sms * 1e3:.2f} us -> {sbytes / (sms * 1e-3) / 1e9:.0f} GB/s")
+    return out
+
+
+def cpu_baseline(torch, w, dec_bytes, seconds):
+    """The C oracle's decode of slice 0 on the host cores, bounded in time."""
+    sys.path.insert(0, os.path.join(REPO, "tests"))
+    from oracle_bindings import Oracle
+    o = Oracle()
+    threads = min(16, os.cpu_count() or 1)
+    h_q = w.q[0].view(torch.int16).cpu().numpy().view(np.uint16)
+    h_kc, h_vc, h_sc = w.kc.cpu().numpy(), w.vc.cpu().numpy(), w.sc.cpu().numpy()
+    h_tab, h_ctx = w.tables[0].cpu().numpy(), w.ctx.cpu().numpy()
+    iters, t0 = 0, time.perf_counter()
+    while True:
+        o.paged_decode(h_q, h_kc, h_vc, h_sc, h_tab, h_ctx, w.signs_np, None, HQ, HKV, D, S,
+                       w.pool, w.splits, np.float32(w.scale), np.float32(w.isl), 1,
+                       threads=threads)
+        iters += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    return {"value": round(dec_bytes * iters / el / 1e9, 4), "unit": "GB/s", "cores": threads,
+            "kind": "port",
+            "sample": f"{iters} configs[2] decodes (B=1, 32q:8kv, d128, ctx4096, {w.splits} "
+                      f"splits) by oracle/tq4_oracle.c in {el:.1f} s on {threads} threads",
+            "us_per_decode": round(el / iters * 1e6, 1)}
 
 
 if __name__ == "__main__":

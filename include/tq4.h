@@ -161,7 +161,11 @@ int tq4_decode_workspace_init(void* stream, void* workspace, size_t workspace_by
 
 /* Fused decode: partials, then the last-arriving workgroup of each (seq, kv
  * head) LSE-combines them, rotates back, gates and stores BF16 -- one launch.
- * Calls that overlap on one workspace race. num_splits 0 = auto.
+ * Splits that hold no live token of their sequence (those at or past
+ * ceil(ceil(context_len / block_size) / ceil(max_blocks_per_seq /
+ * num_splits))) write nothing and do not take part in the combine, so a
+ * ragged batch can use many splits. Calls that overlap on one workspace
+ * race. num_splits 0 = auto.
  * Modelled on turboquant_paged_attention_impl
  * (kernels/ops/turboquant/baseline/turboquant_paged_attention.cpp:773-793);
  * replaces the L2-spinlock accumulation

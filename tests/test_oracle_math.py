@@ -178,3 +178,43 @@ def test_writer_int8_equals_bf16_integers(oracle):
         imgs.append((kc, vc, sc.view(np.uint32)))
     for a, b in zip(*imgs):
         assert np.array_equal(a, b)
+
+
+@pytest.mark.parametrize("d", [64, 128, 256])
+def test_rotation_tables_compose_to_M(oracle, d):
+    """The INT8 rotation tables (T[s][g][c0][i], turboquant_oracle.hpp:157-195)
+    rebuild the dense rotation the way the reference's Cube applies them:
+    M[c1*32 + c0][g*32 + i] = T[parity(c1 & g)][g][c0][i] (the outer H_{d/32}
+    picks the table's sign); compared column by column with the dense M
+    from the butterfly definition. The signs come back out of the tables."""
+    rng = np.random.default_rng(d)
+    signs = np.where(rng.random(d) < 0.5, -1.0, 1.0).astype(np.float32)
+    groups = d // 32
+    tables = np.zeros(2 * groups * 32 * 32, np.int8)
+    oracle.lib.tq4o_build_tables_i8(d, signs.ctypes.data, tables.ctypes.data)
+    T = tables.reshape(2, groups, 32, 32).astype(np.int64)
+    M = np.zeros((d, d), np.int64)
+    for c1 in range(groups):
+        for g in range(groups):
+            par = bin(c1 & g).count("1") & 1
+            M[c1 * 32:(c1 + 1) * 32, g * 32:(g + 1) * 32] = T[par, g]
+    dense = np.stack([oracle.rotate_dense(np.eye(d, dtype=np.float32)[j], signs)
+                      for j in range(d)], axis=1)
+    assert np.array_equal(dense, M.astype(np.float64))
+    back = np.zeros(d, np.float32)
+    assert oracle.lib.tq4o_signs_from_tables_i8(d, tables.ctypes.data, back.ctypes.data) == 0
+    assert np.array_equal(back, signs)
+    tables[5] = -tables[5]  # a corrupted block is detected
+    assert oracle.lib.tq4o_signs_from_tables_i8(d, tables.ctypes.data, back.ctypes.data) == -1
+
+
+@pytest.mark.parametrize("d", [128, 256])
+def test_rotation_tables_match_reference(oracle, ref, d):
+    """Byte for byte against tq_oracle::build_tables on the canonical signs
+    (tests/common/turboquant_oracle.hpp:157-171), where oracle/_ref is built."""
+    signs = oracle.canonical_signs(d)
+    ours = np.zeros(2 * (d // 32) * 1024, np.int8)
+    oracle.lib.tq4o_build_tables_i8(d, signs.ctypes.data, ours.ctypes.data)
+    theirs = np.zeros_like(ours)
+    ref.lib.ref_tq_build_tables(d, theirs.ctypes.data)
+    assert np.array_equal(ours, theirs)
