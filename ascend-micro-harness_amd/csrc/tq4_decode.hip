@@ -69,7 +69,7 @@ constexpr float kTau = 8.0f;             // lazy-maximum headroom, log2 units
 constexpr float kShiftLimit = 100.0f;    // bound of the value-scale normalisation shift
 constexpr uint32_t kBadStrip = 0xFFFFFFFFu;
 constexpr uint32_t kFlagRotated = 1u;
-constexpr int kHdrFloats = 160;          // m_x[4][16], l_x[4][16], q_exp[16], flags
+constexpr int kHdrFloats = 416;          // m_x, l_x [4][16], q_exp[16], flags, 2^-sh[4], scale slots [4][64]
 
 // Eight codes of one dword as fp16 (1 + u/64), u = nibble ^ 8; halves in
 // nibble order 0,4,1,5,2,6,3,7 (every operand built against this table uses
@@ -130,9 +130,8 @@ template <int D>
 struct PairRegs {
     uint32_t k1[D / 32];  // T1 key row (token of row n), channels g*d/4 .. +d/4
     uint32_t k2[D / 32];  // T2 key row
-    uint32_t v[D / 16];   // value codes: channel 16b + n, 8 tokens of strip g>>1
-    f4_t ks1, ks2;        // key scales of the lane's 8 tokens (T1 then T2)
-    f4_t vs1, vs2;        // value scales of the same tokens
+    uint32_t v[D / 16];   // value strip g>>1: 16 B chunks, channels n*d/16 + 4q + 2*(g&1) + {0,1}
+    float sc;             // one scale: plane g&1, strip g>>1, token n
 };
 
 template <int D>
@@ -281,10 +280,11 @@ __host__ __device__ constexpr size_t region_floats(uint32_t G, uint32_t D)
     return 4ull * G * D;  // q staging [G][D], then the four waves' rows [4][G][D]
 }
 
-// Two waves per SIMD at d <= 128 (the register ring fits in 256 VGPRs); the
-// d = 256 ring needs the whole file.
+// Waves per SIMD the register ring allows without spilling: three at
+// d = 64, two at d = 128 (<= 256 VGPRs), one at d = 256.
 template <int D, int MODE>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 2 : 1, 2)))
+__global__ __launch_bounds__(kThreads)
+__attribute__((amdgpu_waves_per_eu(D == 64 ? 3 : (D == 128 ? 2 : 1), D == 64 ? 3 : 2)))
 void decode_kernel(DecodeParams p)
 {
     constexpr int CPL = D / 64;   // channels per lane in the row layout
@@ -295,11 +295,12 @@ void decode_kernel(DecodeParams p)
     extern __shared__ float smem[];
 
     const uint32_t G = p.G, S = p.S;
-    float* m_x = smem;                       // [4][16]
-    float* l_x = smem + 64;                  // [4][16]
+    float* m_x = smem;                       // [16][4] (row, wave)
+    float* l_x = smem + 64;                  // [16][4]
     int* q_exp = (int*)(smem + 128);         // [16]
     int* flag = (int*)(smem + 144);
     float* u_x = smem + 148;                 // [4] per-wave 2^-sh
+    float* sc_wave = smem + 160 + 64 * (threadIdx.x >> 6);  // [4][64] per-wave scale slot
     uint32_t* strip_lds = (uint32_t*)(smem + kHdrFloats);  // [TQ4 max split strips]
     float* region = smem + kHdrFloats + TQ4_MAX_SPLIT_STRIPS;
 
@@ -411,14 +412,19 @@ void decode_kernel(DecodeParams p)
         const int8_t* kb = p.key_cache + (size_t)(rk + t1) * (D / 2) + g4 * (D / 8);
         load_row_chunk<D>(r.k1, kb);
         load_row_chunk<D>(r.k2, kb + 4 * (D / 2));
-        const int8_t* vb8 = p.value_cache + (size_t)rv * (D / 2) + n * 8 + 4 * half;
+        // value strip: lane (n, half) takes 16 B chunks q = 0.. of channel
+        // group n -- both token halves of channels n*d/16 + 4q + 2*half + {0,1}
+        const int8_t* vb8 = p.value_cache + (size_t)rv * (D / 2) + n * (D / 2) + 16 * half;
 #pragma unroll
-        for (int b = 0; b < NB; ++b) r.v[b] = *(const uint32_t*)(vb8 + 128 * b);
-        const float* ksp = p.scale_cache + rv + 8 * half;
-        r.ks1 = *(const f4_t*)ksp;
-        r.ks2 = *(const f4_t*)(ksp + 4);
-        r.vs1 = *(const f4_t*)(ksp + plane_floats);
-        r.vs2 = *(const f4_t*)(ksp + plane_floats + 4);
+        for (int q = 0; q < NB / 4; ++q) {
+            const uint4 w = *(const uint4*)(vb8 + 32 * q);
+            r.v[4 * q + 0] = w.x;
+            r.v[4 * q + 1] = w.y;
+            r.v[4 * q + 2] = w.z;
+            r.v[4 * q + 3] = w.w;
+        }
+        // the pair's 64 scales, one per lane: plane `half`, strip sp, token n
+        r.sc = p.scale_cache[(size_t)half * plane_floats + rv + n];
     };
 
     // ---- the first pairs of this wave's ring go out before the q prologue.
@@ -512,16 +518,23 @@ void decode_kernel(DecodeParams p)
             c1 = mfma32(codes8(r.k1[j]), qop[j], c1);
             c2 = mfma32(codes8(r.k2[j]), qop[j], c2);
         }
+        // scales through the wave's LDS slot: key scales of this lane's 8
+        // tokens (strip sp, tokens 8*half..) at [32sp + 8half], values at +16
+        sc_wave[lane] = r.sc;
+        const f4_t ks1 = *(const f4_t*)(sc_wave + 32 * sp + 8 * half);
+        const f4_t ks2 = *(const f4_t*)(sc_wave + 32 * sp + 8 * half + 4);
+        const f4_t vs1 = *(const f4_t*)(sc_wave + 32 * sp + 16 + 8 * half);
+        const f4_t vs2 = *(const f4_t*)(sc_wave + 32 * sp + 16 + 8 * half + 4);
         float c[8], cfk[8], vs[8];
         bool live[8];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             c[i] = c1[i];
             c[4 + i] = c2[i];
-            cfk[i] = cf * r.ks1[i];
-            cfk[4 + i] = cf * r.ks2[i];
-            vs[i] = r.vs1[i];
-            vs[4 + i] = r.vs2[i];
+            cfk[i] = cf * ks1[i];
+            cfk[4 + i] = cf * ks2[i];
+            vs[i] = vs1[i];
+            vs[4 + i] = vs2[i];
         }
         if (masked) {
             // window token of value i: pair base + strip sp + 8*half + (i&3) + 4*(i>>2)
@@ -586,8 +599,22 @@ void decode_kernel(DecodeParams p)
         lpart += psum;
         // A operand in the codes8 token order: (T1[0], T2[0], T1[1], T2[1], ...)
         const h8_t P = h8_t{x[0], x[4], x[1], x[5], x[2], x[6], x[3], x[7]};
+        // B operands: block b = 4q + 2hb + e is channel n*d/16 + b. The lane
+        // pair (half 0, half 1) swaps so each holds its own 8-token half:
+        // permlane16_swap(x, y) leaves the even row's x plus the odd row's
+        // copy of the even row's y in its first result (block hb = 0), and
+        // the odd row's x copy plus the odd row's y in its second (hb = 1).
 #pragma unroll
-        for (int b = 0; b < NB; ++b) acc[b] = mfma32(P, codes8(r.v[b]), acc[b]);
+        for (int q = 0; q < NB / 4; ++q) {
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const auto sw = __builtin_amdgcn_permlane16_swap(r.v[4 * q + 2 * e],
+                                                                 r.v[4 * q + 2 * e + 1], false,
+                                                                 false);
+                acc[4 * q + e] = mfma32(P, codes8(sw[0]), acc[4 * q + e]);
+                acc[4 * q + 2 + e] = mfma32(P, codes8(sw[1]), acc[4 * q + 2 + e]);
+            }
+        }
         cr = mfma32(P, offset_col, cr);
     };
 
@@ -631,9 +658,9 @@ void decode_kernel(DecodeParams p)
     // removed) and (m, l, 2^-sh) in LDS; then every output float4 combines
     // the four copies with the row's common maximum.
     const float lsum = col_sum(lpart);
-    if (g4 == 0) {
-        m_x[wave * 16 + n] = row_live ? m_used : -INFINITY;
-        l_x[wave * 16 + n] = lsum;
+    if (g4 == 0) {  // [row][wave]: one 16-byte read gives a row's four waves
+        m_x[n * kWaves + wave] = row_live ? m_used : -INFINITY;
+        l_x[n * kWaves + wave] = lsum;
     }
     if (lane == 0) u_x[wave] = ldexpf(1.0f, -(int)sh);
     float* part = region;  // [kWaves][G][D]
@@ -641,24 +668,28 @@ void decode_kernel(DecodeParams p)
     for (int i = 0; i < 4; ++i) {
         const uint32_t r = 4 * g4 + i;
         if (r < G) {
-            float* dst = part + ((size_t)wave * G + r) * D + n;
+            float* dst = part + ((size_t)wave * G + r) * D + n * NB;  // channel n*d/16 + b
 #pragma unroll
-            for (int b = 0; b < NB; ++b) dst[16 * b] = acc[b][i] - cr[i];
+            for (int b = 0; b < NB; ++b) dst[b] = acc[b][i] - cr[i];
         }
     }
     lds_barrier();
-    // Per-wave weights of row r (exp2(m_w - M) * 2^-sh_w), the row's M and L.
+    // Per-wave weights of row r (exp2(m_w - M) * 2^-sh_w), the row's M and L;
+    // branch-free: a wave with no live token gets exp2(-inf) = 0.
     auto row_weights = [&](uint32_t r, float (&f)[kWaves], float& M, float& L) {
-        M = m_x[r];
-#pragma unroll
-        for (int w = 1; w < kWaves; ++w) M = fmaxf(M, m_x[w * 16 + r]);
+        const float4 m4 = *(const float4*)(m_x + r * kWaves);
+        const float4 l4 = *(const float4*)(l_x + r * kWaves);
+        const float4 u4 = *(const float4*)u_x;
+        const float mw[kWaves] = {m4.x, m4.y, m4.z, m4.w};
+        const float lw[kWaves] = {l4.x, l4.y, l4.z, l4.w};
+        const float uw[kWaves] = {u4.x, u4.y, u4.z, u4.w};
+        M = fmaxf(fmaxf(mw[0], mw[1]), fmaxf(mw[2], mw[3]));
         L = 0.0f;
 #pragma unroll
         for (int w = 0; w < kWaves; ++w) {
-            const float mw = m_x[w * 16 + r];
-            f[w] = (M == -INFINITY || mw == -INFINITY) ? 0.0f
-                                                        : __builtin_amdgcn_exp2f(mw - M) * u_x[w];
-            L += l_x[w * 16 + r] * f[w];
+            const float d = (mw[w] == -INFINITY) ? -INFINITY : mw[w] - M;
+            f[w] = __builtin_amdgcn_exp2f(d) * uw[w];
+            L += lw[w] * f[w];
         }
     };
     const uint32_t outs4 = G * D / 4;  // float4 outputs

@@ -48,26 +48,41 @@ __device__ __forceinline__ void load_row(const uint16_t* src, float (&x)[CPL])
     for (int j = 0; j < CPL; ++j) x[j] = bf16_to_f32(src[j]);
 }
 
-// Signs for the lane's CPL channels: pi_signs when given, else the first
-// column of the reference's rotation tables (T[0][g][c0][0] = sign[g*32+c0]).
+// Signs for the lane's CPL channels: pi_signs when given (CPL consecutive
+// floats, vector loads), else the first column of the reference's rotation
+// tables (T[0][g][c0][0] = sign[g*32+c0]). The source is chosen once per
+// launch (a uniform branch), never per channel.
 template <int CPL>
 __device__ __forceinline__ void load_signs(const float* pi_signs, const void* tables,
                                            int tables_bf16, int c0, float (&sign)[CPL])
 {
+    if (pi_signs != nullptr) {
+        const float* src = pi_signs + c0;
+        if constexpr (CPL % 4 == 0) {
+#pragma unroll
+            for (int j = 0; j < CPL; j += 4) {
+                const float4 v = *(const float4*)(src + j);
+                sign[j] = v.x;
+                sign[j + 1] = v.y;
+                sign[j + 2] = v.z;
+                sign[j + 3] = v.w;
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) sign[j] = src[j];
+        }
+        return;
+    }
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
         const int c = c0 + j;
-        float s;
-        if (pi_signs != nullptr) {
-            s = pi_signs[c];
-        } else if (tables_bf16) {
+        if (tables_bf16) {
             const uint16_t raw = ((const uint16_t*)tables)[(size_t)c * 32];
-            s = (raw & 0x8000u) ? -1.0f : 1.0f;
+            sign[j] = (raw & 0x8000u) ? -1.0f : 1.0f;
         } else {
             const int8_t raw = ((const int8_t*)tables)[(size_t)c * 32];
-            s = raw < 0 ? -1.0f : 1.0f;
+            sign[j] = raw < 0 ? -1.0f : 1.0f;
         }
-        sign[j] = s;
     }
 }
 
@@ -153,6 +168,14 @@ __global__ __launch_bounds__(kWriterThreads) void strip_writer(
     const int row = tid >> 4;        // token within the strip
     const int lane_in_row = tid & 15;
 
+    // The row and the signs do not depend on the slots: their loads go out
+    // together with the slot loads (one round trip, not two).
+    const In* src = (plane == 0 ? key : value) +
+                    ((size_t)((size_t)strip * kStrip + row) * H + head) * D + lane_in_row * CPL;
+    float v[CPL], sign[CPL];
+    load_row<CPL>(src, v);
+    load_signs<CPL>(pi_signs, tables, tables_bf16, lane_in_row * CPL, sign);
+
     // Slot contract for this strip: consecutive, strip-aligned, in range.
     const int32_t slot0 = slots[(size_t)strip * kStrip];
     const int32_t mine = slots[(size_t)strip * kStrip + row];
@@ -161,12 +184,6 @@ __global__ __launch_bounds__(kWriterThreads) void strip_writer(
     if (!__syncthreads_and(ok)) return;
     const uint32_t page = (uint32_t)slot0 / S;
     const uint32_t tip = (uint32_t)slot0 % S + (uint32_t)row;
-
-    const In* src = (plane == 0 ? key : value) +
-                    ((size_t)((size_t)strip * kStrip + row) * H + head) * D + lane_in_row * CPL;
-    float v[CPL], sign[CPL];
-    load_row<CPL>(src, v);
-    load_signs<CPL>(pi_signs, tables, tables_bf16, lane_in_row * CPL, sign);
     int q[CPL];
     const float scale =
         rotate_quantise<D, CPL>(v, sign, lane_in_row, inv_sqrt_len, kPolicyPrefill, q);
