@@ -37,12 +37,20 @@
 //     outgrows the fp16 headroom), so the accumulator rescale -- the only
 //     cross-lane step -- is off the common path.
 // The four waves' (m, l, acc) merge through LDS; the workgroup then exports
-// one partial record, or, in the fused entry, the last workgroup of each
-// (seq, kv head) to arrive (an agent-scope counter that resets itself)
-// combines all splits -- one q head per wave, every record load in flight at
-// once -- rotates back, gates and stores BF16. No spinlock: the reference's
-// L2-line lock (turboquant_splitk_reduce.cpp:279-350) is replaced by disjoint
-// records plus one counter increment per workgroup.
+// one partial record. In the fused entry every live split takes a ticket from
+// an agent-scope counter right after its prologue (the round trip hides under
+// the strip loads); the split holding the last ticket combines. Every other
+// split of its (seq, kv head) has started by then, so waiting for them is
+// safe: they only stream, merge and store. Their records travel with the
+// device-coherence bit, XOR-encoded so that an all-zero word means "not yet
+// written" (no arithmetic result has the encoded bit pattern). The combiner
+// exports its own record like the others, then polls all of them with
+// coherent loads -- no store acknowledgement, no second atomic; the combine
+// runs in split order whichever split combines -- rotates back, gates, stores
+// BF16 and zeroes the records it consumed for the next call. A sequence with
+// one live split finalises from LDS. No spinlock: the reference's L2-line lock
+// (turboquant_splitk_reduce.cpp:279-350) is replaced by disjoint records and
+// one ticket per workgroup.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -69,7 +77,9 @@ constexpr float kTau = 8.0f;             // lazy-maximum headroom, log2 units
 constexpr float kShiftLimit = 100.0f;    // bound of the value-scale normalisation shift
 constexpr uint32_t kBadStrip = 0xFFFFFFFFu;
 constexpr uint32_t kFlagRotated = 1u;
-constexpr int kHdrFloats = 416;          // m_x, l_x [4][16], q_exp[16], flags, 2^-sh[4], scale slots [4][64]
+constexpr int kHdrFloats = 416;          // m_x, l_x [16][4], q_exp[16], flags, 2^-sh[4], scale slots [4][64]
+constexpr uint32_t kRecMagic = 0x7FBADBADu;  // fused records hold bits ^ kRecMagic; 0 = not written
+constexpr uint32_t kPollLimit = 1u << 20;     // bound of the combiner's record polls
 
 // Eight codes of one dword as fp16 (1 + u/64), u = nibble ^ 8; halves in
 // nibble order 0,4,1,5,2,6,3,7 (every operand built against this table uses
@@ -167,112 +177,205 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t records_rsrc(const float* base
                                              0x00020000);
 }
 
-template <bool COHERENT>
-__device__ __forceinline__ void rec_store4(__amdgpu_buffer_rsrc_t r, uint32_t byte_off, float4 v)
+typedef uint32_t u2_t __attribute__((ext_vector_type(2)));
+
+// Stores and loads of N = 1, 2 or 4 consecutive record floats. ENC: the fused
+// encoding (bits ^ kRecMagic) and the device-coherence bit.
+template <int N, bool ENC>
+__device__ __forceinline__ void rec_store(__amdgpu_buffer_rsrc_t r, uint32_t byte_off,
+                                          const float* v)
 {
-    typedef uint32_t u4v __attribute__((ext_vector_type(4)));
-    const u4v u = u4v{__float_as_uint(v.x), __float_as_uint(v.y), __float_as_uint(v.z),
-                      __float_as_uint(v.w)};
-    __builtin_amdgcn_raw_buffer_store_b128(u, r, byte_off, 0, COHERENT ? kCachePolicySc1 : 0);
+    const uint32_t x = ENC ? kRecMagic : 0u;
+    const int pol = ENC ? kCachePolicySc1 : 0;
+    if constexpr (N == 4) {
+        const u4_t u = u4_t{__float_as_uint(v[0]) ^ x, __float_as_uint(v[1]) ^ x,
+                            __float_as_uint(v[2]) ^ x, __float_as_uint(v[3]) ^ x};
+        __builtin_amdgcn_raw_buffer_store_b128(u, r, byte_off, 0, pol);
+    } else if constexpr (N == 2) {
+        const u2_t u = u2_t{__float_as_uint(v[0]) ^ x, __float_as_uint(v[1]) ^ x};
+        __builtin_amdgcn_raw_buffer_store_b64(u, r, byte_off, 0, pol);
+    } else {
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v[0]) ^ x, r, byte_off, 0, pol);
+    }
 }
 
-template <bool COHERENT>
-__device__ __forceinline__ float2 rec_load2(__amdgpu_buffer_rsrc_t r, uint32_t byte_off)
+// Raw words (still encoded when ENC).
+template <int N, bool ENC>
+__device__ __forceinline__ void rec_load(__amdgpu_buffer_rsrc_t r, uint32_t byte_off,
+                                         uint32_t* w)
 {
-    const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, byte_off, 0, COHERENT ? kCachePolicySc1 : 0);
-    return make_float2(__uint_as_float(v[0]), __uint_as_float(v[1]));
+    const int pol = ENC ? kCachePolicySc1 : 0;
+    if constexpr (N == 4) {
+        const u4_t u = __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, pol);
+        w[0] = u[0];
+        w[1] = u[1];
+        w[2] = u[2];
+        w[3] = u[3];
+    } else if constexpr (N == 2) {
+        const u2_t u = __builtin_amdgcn_raw_buffer_load_b64(r, byte_off, 0, pol);
+        w[0] = u[0];
+        w[1] = u[1];
+    } else {
+        w[0] = __builtin_amdgcn_raw_buffer_load_b32(r, byte_off, 0, pol);
+    }
 }
 
-template <bool COHERENT>
-__device__ __forceinline__ float rec_load1(__amdgpu_buffer_rsrc_t r, uint32_t byte_off)
+// Combine layout of one wave over one (seq, q head) row: lane c = lane & 31
+// owns channels c*CC .. c*CC+CC-1 (CC = d/32); ks = lane >> 5 takes the
+// splits of parity ks of every chunk of 16, so a chunk costs each lane eight
+// (m, l) loads and eight CC-float loads, all in flight together. Slots past
+// K load split K-1 (in range, already required) and are selected out.
+//
+// LSE-combine the K partial records [m, l, 0, 0, acc[d]] at rr (stride d+4)
+// in split order, leaving acc / L in v (0 when L == 0).
+// (tests/common/l2_atomic_oracle.hpp:156-176; identity :100-108)
+// FUSED: the records are encoded; a chunk is reloaded until none of its words
+// is zero (bounded by kPollLimit), then zeroed for the next call.
+template <int D, bool FUSED>
+__device__ void combine_records(const float* rr, uint32_t K, int lane, float (&v)[D / 32])
 {
-    return __uint_as_float(
-        __builtin_amdgcn_raw_buffer_load_b32(r, byte_off, 0, COHERENT ? kCachePolicySc1 : 0));
-}
-
-// LSE-combine the K partial records of one (seq, q head) row -- split k at
-// rr + k*(D+4) = [m, l, 0, 0, acc[D]] -- for the D/64 channels lane*D/64..
-// of one wave lane, leaving acc / L (0 when L == 0). Every record load of a
-// chunk of splits is in flight together (one round trip per chunk).
-template <int D, bool COHERENT>
-__device__ void combine_row(const float* rr, uint32_t K, int lane, float (&out)[D / 64])
-{
-    constexpr int CPL = D / 64;
+    constexpr int CC = D / 32;
+    constexpr int LD = CC >= 4 ? 4 : CC;  // floats per load
     constexpr int RS = D + 4;
-    constexpr int KC = 16;
     const __amdgpu_buffer_rsrc_t rsrc = records_rsrc(rr);
-    float M = -INFINITY, L = 0.0f, a[CPL];
+    const int c = lane & 31, ks = lane >> 5;
+    const uint32_t x = FUSED ? kRecMagic : 0u;
+    float M = -INFINITY, L = 0.0f, a[CC];
 #pragma unroll
-    for (int c = 0; c < CPL; ++c) a[c] = 0.0f;
-    for (uint32_t k0 = 0; k0 < K; k0 += KC) {
-        const uint32_t kn = K - k0 < (uint32_t)KC ? K - k0 : (uint32_t)KC;
-        float mk[KC], lk[KC], ak[KC][CPL];
+    for (int j = 0; j < CC; ++j) a[j] = 0.0f;
+    for (uint32_t k0 = 0; k0 < K; k0 += 16) {
+        uint32_t roff[8];
+        bool vi[8];
 #pragma unroll
-        for (int i = 0; i < KC; ++i) {
-            // unconditional (index clamped to the chunk's last split) so the
-            // whole chunk issues back to back; surplus copies are ignored
-            const uint32_t off = ((k0 + min((uint32_t)i, kn - 1)) * RS) * 4u;
-            const float2 ml = rec_load2<COHERENT>(rsrc, off);
-            mk[i] = ml.x;
-            lk[i] = ml.y;
-            if constexpr (CPL == 1) {
-                ak[i][0] = rec_load1<COHERENT>(rsrc, off + (4 + lane) * 4);
-            } else {
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t k = k0 + ks + 2 * i;
+            vi[i] = k < K;
+            roff[i] = (vi[i] ? k : K - 1) * RS * 4u;
+        }
+        uint32_t hw[8][2], aw[8][CC];
+        for (uint32_t it = 0;; ++it) {
+            asm volatile("" ::: "memory");  // every poll reloads
 #pragma unroll
-                for (int c = 0; c < CPL; c += 2) {
-                    const float2 v = rec_load2<COHERENT>(rsrc, off + (4 + lane * CPL + c) * 4);
-                    ak[i][c] = v.x;
-                    ak[i][c + 1] = v.y;
+            for (int i = 0; i < 8; ++i) {
+                rec_load<2, FUSED>(rsrc, roff[i], hw[i]);
+#pragma unroll
+                for (int j = 0; j < CC; j += LD)
+                    rec_load<LD, FUSED>(rsrc, roff[i] + 4u * (4 + c * CC + j), &aw[i][j]);
+            }
+            if constexpr (!FUSED) break;
+            uint32_t mn = 0xffffffffu;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                mn = min(mn, min(hw[i][0], hw[i][1]));
+#pragma unroll
+                for (int j = 0; j < CC; ++j) mn = min(mn, aw[i][j]);
+            }
+            if (!__any(mn == 0u) || it + 1 >= kPollLimit) break;
+        }
+        if constexpr (FUSED) {
+            // Zero what was consumed, so the next call starts from "not
+            // written" (slots past K zero split K-1 again). Issued at once:
+            // the stores complete under the arithmetic below.
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                __builtin_amdgcn_raw_buffer_store_b64(u2_t{0u, 0u}, rsrc, roff[i], 0,
+                                                      kCachePolicySc1);
+#pragma unroll
+                for (int j = 0; j < CC; j += LD) {
+                    const uint32_t off = roff[i] + 4u * (4 + c * CC + j);
+                    if constexpr (LD == 4)
+                        __builtin_amdgcn_raw_buffer_store_b128(u4_t{0u, 0u, 0u, 0u}, rsrc, off, 0,
+                                                               kCachePolicySc1);
+                    else
+                        __builtin_amdgcn_raw_buffer_store_b64(u2_t{0u, 0u}, rsrc, off, 0,
+                                                              kCachePolicySc1);
                 }
             }
         }
-        // log2 domain: w = exp(m_k - M) = exp2((m_k - M) * log2(e))
-        float Mc = M;
+        float mk[8], Mc = -INFINITY;
 #pragma unroll
-        for (int i = 0; i < KC; ++i) {
-            mk[i] *= kLog2e;
-            if ((uint32_t)i < kn) Mc = fmaxf(Mc, mk[i]);
+        for (int i = 0; i < 8; ++i) {
+            mk[i] = __uint_as_float(hw[i][0] ^ x) * kLog2e;
+            Mc = fmaxf(Mc, vi[i] ? mk[i] : -INFINITY);
         }
-        const float s = M == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(M - Mc);
-        L *= s;
+        Mc = fmaxf(Mc, xor_lanes(Mc, 32));  // the other parity
+        const float Mn = fmaxf(M, Mc);
+        const float sc = M == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(M - Mn);
+        float lw = 0.0f;
 #pragma unroll
-        for (int c = 0; c < CPL; ++c) a[c] *= s;
+        for (int j = 0; j < CC; ++j) a[j] *= sc;
 #pragma unroll
-        for (int i = 0; i < KC; ++i) {
-            if ((uint32_t)i < kn) {
-                const float w = __builtin_amdgcn_exp2f(mk[i] - Mc);
-                L += lk[i] * w;
+        for (int i = 0; i < 8; ++i) {
+            const float w = __builtin_amdgcn_exp2f(mk[i] - Mn);
+            lw += vi[i] ? __uint_as_float(hw[i][1] ^ x) * w : 0.0f;
 #pragma unroll
-                for (int c = 0; c < CPL; ++c) a[c] += w * ak[i][c];
-            }
+            for (int j = 0; j < CC; ++j)
+                a[j] += vi[i] ? __uint_as_float(aw[i][j] ^ x) * w : 0.0f;
         }
-        M = Mc;
+        L = L * sc + (lw + xor_lanes(lw, 32));
+        M = Mn;
     }
+    // the two split parities
 #pragma unroll
-    for (int c = 0; c < CPL; ++c) out[c] = L == 0.0f ? 0.0f : a[c] / L;
+    for (int j = 0; j < CC; ++j) a[j] += xor_lanes(a[j], 32);
+    const float inv = L == 0.0f ? 0.0f : __builtin_amdgcn_rcpf(L);
+#pragma unroll
+    for (int j = 0; j < CC; ++j) v[j] = a[j] * inv;
 }
 
-// Egress of one normalised row held by one wave (lane owns channels
-// lane*D/64 ..): optionally Pi^T and 1/sqrt(d), optionally the gate, BF16 RNE.
+// Egress of one normalised row in the combine layout (lane c = lane & 31
+// owns channels c*CC ..; both halves hold the row): optionally Pi^T and
+// 1/sqrt(d), optionally the gate, BF16 RNE; lanes 0..31 store.
 template <int D>
-__device__ void egress_regs(float (&v)[D / 64], const float* pi_signs, const float* gate,
-                            uint16_t* out, float inv_sqrt_len, uint32_t stage, int lane)
+__device__ void egress_row(float (&v)[D / 32], const float (&sg)[D / 32], const float (&gt)[D / 32],
+                           uint16_t* out_row, float inv_sqrt_len, uint32_t stage, int lane)
 {
-    constexpr int CPL = D / 64;
+    constexpr int CC = D / 32;
+    const int c = lane & 31;
     if (stage >= 1) {
-        float sg[CPL];
+        rotate_egress<D, CC>(v, sg, c);
 #pragma unroll
-        for (int j = 0; j < CPL; ++j) sg[j] = pi_signs[lane * CPL + j];
-        rotate_egress<D, CPL>(v, sg, lane);
-#pragma unroll
-        for (int j = 0; j < CPL; ++j) v[j] *= inv_sqrt_len;
+        for (int j = 0; j < CC; ++j) v[j] *= inv_sqrt_len;
         if (stage == 2) {
 #pragma unroll
-            for (int j = 0; j < CPL; ++j) v[j] = v[j] / (1.0f + expf(-gate[lane * CPL + j]));
+            for (int j = 0; j < CC; ++j) v[j] = v[j] / (1.0f + expf(-gt[j]));
         }
     }
+    uint32_t pk[CC / 2];
 #pragma unroll
-    for (int j = 0; j < CPL; ++j) out[lane * CPL + j] = (uint16_t)f32_to_bf16(v[j]);
+    for (int j = 0; j < CC / 2; ++j)
+        pk[j] = f32_to_bf16(v[2 * j]) | (f32_to_bf16(v[2 * j + 1]) << 16);
+    if (lane < 32) {
+        uint16_t* dst = out_row + c * CC;
+        if constexpr (CC == 8)
+            *(uint4*)dst = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+        else if constexpr (CC == 4)
+            *(uint2*)dst = make_uint2(pk[0], pk[1]);
+        else
+            *(uint32_t*)dst = pk[0];
+    }
+}
+
+// The combine layout's signs and gate values of one lane.
+template <int D>
+__device__ __forceinline__ void load_lane_floats(const float* src, int lane, float (&x)[D / 32])
+{
+    constexpr int CC = D / 32;
+    const float* p = src + (lane & 31) * CC;
+    if constexpr (CC >= 4) {
+#pragma unroll
+        for (int j = 0; j < CC; j += 4) {
+            const float4 f = *(const float4*)(p + j);
+            x[j] = f.x;
+            x[j + 1] = f.y;
+            x[j + 2] = f.z;
+            x[j + 3] = f.w;
+        }
+    } else {
+        const float2 f = *(const float2*)p;
+        x[0] = f.x;
+        x[1] = f.y;
+    }
 }
 
 __host__ __device__ constexpr size_t region_floats(uint32_t G, uint32_t D)
@@ -362,13 +465,16 @@ void decode_kernel(DecodeParams p)
             if (split >= k_live) {
                 if (k_live == 0 && split == 0) {
                     // empty context: the normalised context is 0 (l = 0)
+                    float es[D / 32], gt[D / 32];
+                    if (p.output_stage >= 1) load_lane_floats<D>(p.pi_signs, lane, es);
                     for (uint32_t g = wave; g < G; g += kWaves) {
-                        float v[CPL];
+                        float v[D / 32];
 #pragma unroll
-                        for (int j = 0; j < CPL; ++j) v[j] = 0.0f;
+                        for (int j = 0; j < D / 32; ++j) v[j] = 0.0f;
                         const size_t qh = (size_t)seq * p.Hq + kvh * G + g;
-                        egress_regs<D>(v, p.pi_signs, p.gate ? p.gate + qh * D : nullptr,
-                                       p.out + qh * D, p.inv_sqrt_len, p.output_stage, lane);
+                        if (p.output_stage == 2) load_lane_floats<D>(p.gate + qh * D, lane, gt);
+                        egress_row<D>(v, es, gt, p.out + qh * D, p.inv_sqrt_len, p.output_stage,
+                                      lane);
                     }
                 }
                 return;
@@ -389,6 +495,14 @@ void decode_kernel(DecodeParams p)
     // lgkmcnt left at their maxima) keeps the compiler's wait analysis from
     // later waiting on them -- and so on the strip loads queued after them.
     __builtin_amdgcn_s_waitcnt(0x0F70);
+    // Fused entry: this split's ticket. Its round trip overlaps the strip
+    // loads; the value is first needed at the merge.
+    uint32_t ticket = 0;
+    if constexpr (MODE == 1) {
+        if (p.K > 1 && tid == 0)
+            ticket = __hip_atomic_fetch_add(p.counters + (size_t)seq * p.Hkv + kvh, 1u,
+                                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
     const uint32_t np_total = (ltok + 2 * kStrip - 1) / (2 * kStrip);
     const uint32_t np_full = bad ? 0u : ltok / (2 * kStrip);
     const uint32_t nws = pc * spp;  // strips in the window
@@ -663,6 +777,17 @@ void decode_kernel(DecodeParams p)
         l_x[n * kWaves + wave] = lsum;
     }
     if (lane == 0) u_x[wave] = ldexpf(1.0f, -(int)sh);
+    if constexpr (MODE == 1) {
+        if (p.K > 1 && tid == 0) {
+            // The last ticket combines; every live split of this (seq, kv
+            // head) took its ticket before it, so all of them are running.
+            const int last = ticket == k_live - 1;
+            if (last)
+                __hip_atomic_store(p.counters + (size_t)seq * p.Hkv + kvh, 0u, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+            *flag = last;
+        }
+    }
     float* part = region;  // [kWaves][G][D]
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -707,32 +832,9 @@ void decode_kernel(DecodeParams p)
         return v;
     };
 
-    const bool local = (MODE == 1) && p.K == 1;
-    if (local) {
-        // ---- one split: normalise into the wave-0 slice, then the egress.
-        for (uint32_t e4 = tid; e4 < outs4; e4 += kThreads) {
-            float f[kWaves], M, L;
-            row_weights(4 * e4 / D, f, M, L);
-            float4 v = combined4(e4, f);
-            const float inv = L == 0.0f ? 0.0f : 1.0f / L;
-            v = L == 0.0f ? make_float4(0.0f, 0.0f, 0.0f, 0.0f)
-                          : make_float4(v.x * inv, v.y * inv, v.z * inv, v.w * inv);
-            *(float4*)(part + 4 * e4) = v;  // read above only by this thread
-        }
-        lds_barrier();
-        for (uint32_t g = wave; g < G; g += kWaves) {
-            float v[CPL];
-#pragma unroll
-            for (int j = 0; j < CPL; ++j) v[j] = part[g * D + lane * CPL + j];
-            const size_t qh = (size_t)seq * p.Hq + kvh * G + g;
-            egress_regs<D>(v, p.pi_signs, p.gate ? p.gate + qh * D : nullptr, p.out + qh * D,
-                           p.inv_sqrt_len, p.output_stage, lane);
-        }
-        return;
-    }
-
-    // ---- export one record per q head: [m (natural log), l, 0, 0, acc].
-    {
+    constexpr int CC = D / 32;
+    if constexpr (MODE == 0) {
+        // ---- export one record per q head: [m (natural log), l, 0, 0, acc].
         const __amdgpu_buffer_rsrc_t rsrc = records_rsrc(
             p.records + (((size_t)seq * p.Hq + (size_t)kvh * G) * p.K + split) * RS);
         const uint32_t row_bytes = p.K * RS * 4u;
@@ -740,36 +842,75 @@ void decode_kernel(DecodeParams p)
             const uint32_t r = 4 * e4 / D, ch = 4 * e4 % D;
             float f[kWaves], M, L;
             row_weights(r, f, M, L);
-            rec_store4<MODE == 1>(rsrc, r * row_bytes + (4 + ch) * 4u, combined4(e4, f));
-            if (ch == 0)
-                rec_store4<MODE == 1>(rsrc, r * row_bytes,
-                                      make_float4(M == -INFINITY ? kMasked : M * kLn2, L, 0.0f, 0.0f));
+            const float4 v = combined4(e4, f);
+            const float vv[4] = {v.x, v.y, v.z, v.w};
+            rec_store<4, false>(rsrc, r * row_bytes + (4 + ch) * 4u, vv);
+            if (ch == 0) {
+                const float h[4] = {M == -INFINITY ? kMasked : M * kLn2, L, 0.0f, 0.0f};
+                rec_store<4, false>(rsrc, r * row_bytes, h);
+            }
         }
-    }
-    if constexpr (MODE == 0) return;
-
-    // ---- the last workgroup of this (seq, kv head) to arrive combines. The
-    // records went out as device-coherent stores; waiting for their
-    // completion before the increment publishes them (release), and the last
-    // arriver reads them with device-coherent loads (acquire).
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (tid == 0) {
-        uint32_t* ctr = p.counters + (size_t)seq * p.Hkv + kvh;
-        const uint32_t old =
-            __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const int last = old == k_live - 1;
-        if (last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        *flag = last;
-    }
-    __syncthreads();
-    if (!*flag) return;
-    for (uint32_t g = wave; g < G; g += kWaves) {
-        const size_t qh = (size_t)seq * p.Hq + kvh * G + g;
-        float v[CPL];
-        combine_row<D, true>(p.records + qh * p.K * RS, k_live, lane, v);
-        egress_regs<D>(v, p.pi_signs, p.gate ? p.gate + qh * D : nullptr, p.out + qh * D,
-                       p.inv_sqrt_len, p.output_stage, lane);
+        return;
+    } else {
+        // One live split (K == 1, or a sequence shorter than one split's
+        // window) finalises from LDS; otherwise every split exports and the
+        // last ticket combines.
+        const bool local = p.K == 1 || k_live == 1;
+        const bool combiner = local || *flag;
+        float es[CC];
+        if (!local) {
+            // ---- export this split's encoded record.
+            const __amdgpu_buffer_rsrc_t rsrc = records_rsrc(
+                p.records + (((size_t)seq * p.Hq + (size_t)kvh * G) * p.K + split) * RS);
+            const uint32_t row_bytes = p.K * RS * 4u;
+            for (uint32_t e4 = tid; e4 < outs4; e4 += kThreads) {
+                const uint32_t r = 4 * e4 / D, ch = 4 * e4 % D;
+                float f[kWaves], M, L;
+                row_weights(r, f, M, L);
+                const float4 v = combined4(e4, f);
+                const float vv[4] = {v.x, v.y, v.z, v.w};
+                rec_store<4, true>(rsrc, r * row_bytes + (4 + ch) * 4u, vv);
+                if (ch == 0) {
+                    const float h[4] = {M == -INFINITY ? kMasked : M * kLn2, L, 0.0f, 0.0f};
+                    rec_store<4, true>(rsrc, r * row_bytes, h);
+                }
+            }
+            if (!combiner) return;
+            // ---- the combiner: poll and combine every record, its own
+            // included (the sign and gate loads ride with the first poll)
+            if (p.output_stage >= 1) load_lane_floats<D>(p.pi_signs, lane, es);
+            for (uint32_t g = wave; g < G; g += kWaves) {
+                const size_t qh = (size_t)seq * p.Hq + kvh * G + g;
+                float gt[CC];
+                if (p.output_stage == 2) load_lane_floats<D>(p.gate + qh * D, lane, gt);
+                float v[CC];
+                combine_records<D, true>(p.records + qh * p.K * RS, k_live, lane, v);
+                egress_row<D>(v, es, gt, p.out + qh * D, p.inv_sqrt_len, p.output_stage, lane);
+            }
+            return;
+        }
+        if (p.output_stage >= 1) load_lane_floats<D>(p.pi_signs, lane, es);
+        // ---- one live split: normalise into the wave-0 slice (each thread
+        // reads and writes only its own float4), then the egress.
+        for (uint32_t e4 = tid; e4 < outs4; e4 += kThreads) {
+            float f[kWaves], M, L;
+            row_weights(4 * e4 / D, f, M, L);
+            float4 v = combined4(e4, f);
+            const float inv = L == 0.0f ? 0.0f : 1.0f / L;
+            v = L == 0.0f ? make_float4(0.0f, 0.0f, 0.0f, 0.0f)
+                          : make_float4(v.x * inv, v.y * inv, v.z * inv, v.w * inv);
+            *(float4*)(part + 4 * e4) = v;
+        }
+        lds_barrier();
+        for (uint32_t g = wave; g < G; g += kWaves) {
+            const size_t qh = (size_t)seq * p.Hq + kvh * G + g;
+            float gt[CC];
+            if (p.output_stage == 2) load_lane_floats<D>(p.gate + qh * D, lane, gt);
+            float v[CC];
+#pragma unroll
+            for (int j = 0; j < CC; ++j) v[j] = part[g * D + (lane & 31) * CC + j];
+            egress_row<D>(v, es, gt, p.out + qh * D, p.inv_sqrt_len, p.output_stage, lane);
+        }
     }
 }
 
@@ -778,16 +919,19 @@ void decode_kernel(DecodeParams p)
 template <int D>
 __global__ __launch_bounds__(kThreads) void combine_kernel(DecodeParams p)
 {
-    constexpr int CPL = D / 64;
+    constexpr int CC = D / 32;
     const size_t total = (size_t)p.B * p.Hq;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    float es[CC], gt[CC];
+    if (p.output_stage >= 1) load_lane_floats<D>(p.pi_signs, lane, es);
     for (int i = 0; i < 4; ++i) {
         const size_t row = (size_t)blockIdx.x * 16 + wave + kWaves * i;
         if (row >= total) break;
-        float v[CPL];
-        combine_row<D, false>(p.records + row * p.K * (D + 4), p.K, lane, v);
-        egress_regs<D>(v, p.pi_signs, p.gate ? p.gate + row * D : nullptr, p.out + row * D,
-                       p.inv_sqrt_len, p.output_stage, lane);
+        if (p.output_stage == 2) load_lane_floats<D>(p.gate + row * D, lane, gt);
+        float v[CC];
+        combine_records<D, false>(p.records + row * p.K * (D + 4), p.K, lane, v);
+        egress_row<D>(v, es, gt, p.out + row * D, p.inv_sqrt_len, p.output_stage, lane);
     }
 }
 

@@ -147,7 +147,7 @@ int tq4_reshape_scatter(void* stream, uint32_t block_dim, const uint16_t* key,
 #define TQ4_MAX_SPLIT_STRIPS 2048u
 
 /* Workspace bytes for num_splits (partial records plus the per-(seq, kv
- * head) arrival counters of the fused entry). */
+ * head) tickets of the fused entry). */
 size_t tq4_decode_workspace_bytes(uint32_t num_seqs, uint32_t num_heads, uint32_t num_kv_heads,
                                   uint32_t head_size, uint32_t num_splits);
 
@@ -155,12 +155,18 @@ size_t tq4_decode_workspace_bytes(uint32_t num_seqs, uint32_t num_heads, uint32_
 uint32_t tq4_decode_auto_splits(uint32_t num_seqs, uint32_t num_kv_heads,
                                 uint32_t max_blocks_per_seq, uint32_t block_size);
 
-/* Zero a workspace (a fill kernel, no memset node). The fused entry needs its
- * arrival counters zero before the first call and leaves them zero. */
+/* Zero a workspace (a fill kernel, no memset node). The fused entry needs a
+ * zeroed workspace before its first call and leaves it zeroed after every
+ * call (its counters, and its records, which it consumes and clears); a
+ * workspace that tq4_paged_decode_partials has written since must be zeroed
+ * again before tq4_paged_decode uses it. */
 int tq4_decode_workspace_init(void* stream, void* workspace, size_t workspace_bytes);
 
-/* Fused decode: partials, then the last-arriving workgroup of each (seq, kv
- * head) LSE-combines them, rotates back, gates and stores BF16 -- one launch.
+/* Fused decode: partials, then one workgroup of each (seq, kv head) -- the
+ * last of its splits to start -- waits for the others' records, LSE-combines
+ * them in split order, rotates back, gates and stores BF16 -- one launch.
+ * The wait is bounded and only on workgroups already running, so the launch
+ * completes whatever the number of workgroups in flight.
  * Splits that hold no live token of their sequence (those at or past
  * ceil(ceil(context_len / block_size) / ceil(max_blocks_per_seq /
  * num_splits))) write nothing and do not take part in the combine, so a

@@ -18,7 +18,7 @@ import numpy as np
 import pytest
 
 from gpu_helpers import bf16_out_error, canary_bytes, canary_floats, dev, host
-from oracle_bindings import FLAG_QUERY_ROTATED, IN_BF16, f32_to_bf16
+from oracle_bindings import FLAG_QUERY_ROTATED, IN_BF16, bf16_to_f32, f32_to_bf16
 
 pytestmark = pytest.mark.gpu
 
@@ -83,7 +83,7 @@ def run_decode(tq4, oracle, rng, ctx_lens, Hq, H, d, S, P, K, stage=1, gate=None
 
 def check_out(got, want, label=""):
     mx, mr = bf16_out_error(got, want)
-    assert np.all(np.isfinite(got.astype(np.float32))), f"{label}: non-finite output"
+    assert np.all(np.isfinite(bf16_to_f32(got))), f"{label}: non-finite output"
     assert mx <= MAX_ABS and mr <= MEAN_REL, f"{label}: max-abs {mx:.3g} mean-rel {mr:.3g}"
     return mx, mr
 
