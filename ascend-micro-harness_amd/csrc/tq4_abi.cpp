@@ -59,6 +59,7 @@ const char* tq4_status_string(int status)
         case TQ4_ERR_ROTATION: return "neither pi_signs nor tables given";
         case TQ4_ERR_LAUNCH: return "the HIP runtime refused the launch";
         case TQ4_ERR_RANGE: return "a size exceeds the kernels' index range";
+        case TQ4_ERR_CODEBOOK: return "codebook leaf: bits must be 2 or 4, mode 0..5, elements a multiple of 8";
         default: return "unknown status";
     }
 }
@@ -325,3 +326,41 @@ int tq4_splitk_combine(void* stream, const float* workspace, const float* pi_sig
 }
 
 }  // extern "C"
+
+// ------------------------------------------------------------- codebooks
+int tq4_icdf_quantize(void* stream, int in_bf16, const uint16_t* in, uint8_t* out, uint32_t tiles)
+{
+    if (tiles == 0) return TQ4_OK;
+    if (!in || !out) return TQ4_ERR_NULL_POINTER;
+    return launched(tq4::launch_icdf_quantize((hipStream_t)stream, in_bf16 ? 1 : 0, in, out,
+                                              (uint64_t)tiles * 1024u));
+}
+
+int tq4_lloydmax_quantize(void* stream, const void* src, float* dst, uint8_t* codes,
+                          uint32_t* guards, uint32_t bits, uint32_t mode, uint32_t n,
+                          uint32_t rows)
+{
+    (void)guards;
+    const uint64_t count = (uint64_t)n * rows;
+    if ((bits != 2 && bits != 4) || mode > 5 || count % 8 || (mode == 3 && bits != 4))
+        return TQ4_ERR_CODEBOOK;
+    if (count == 0) return TQ4_OK;
+    if (!src) return TQ4_ERR_NULL_POINTER;
+    const hipStream_t st = (hipStream_t)stream;
+    switch (mode) {
+        case 0:
+        case 1:
+        case 2:
+            if (!codes) return TQ4_ERR_NULL_POINTER;
+            return launched(tq4::launch_codebook_quantize(st, mode == 2 ? 1u : 0u, bits,
+                                                          (const float*)src, dst, codes, count));
+        case 3:
+            if (!codes) return TQ4_ERR_NULL_POINTER;
+            return launched(
+                tq4::launch_icdf_quantize(st, 0, (const uint16_t*)src, codes, count));
+        default:
+            if (!dst) return TQ4_ERR_NULL_POINTER;
+            return launched(
+                tq4::launch_codebook_dequantize(st, bits, (const uint8_t*)src, dst, count));
+    }
+}

@@ -44,6 +44,15 @@ hipError_t launch_decode(hipStream_t stream, const DecodeParams& p, int mode);
 hipError_t launch_combine(hipStream_t stream, const DecodeParams& p);
 hipError_t launch_fill_zero(hipStream_t stream, void* ptr, size_t bytes);
 
+// Codebook leaves (count = elements, a multiple of 8).
+hipError_t launch_icdf_quantize(hipStream_t stream, int in_bf16, const uint16_t* in, uint8_t* out,
+                                uint64_t count);
+hipError_t launch_codebook_quantize(hipStream_t stream, uint32_t book, uint32_t bits,
+                                    const float* src, float* recon, uint8_t* codes,
+                                    uint64_t count);
+hipError_t launch_codebook_dequantize(hipStream_t stream, uint32_t bits, const uint8_t* codes,
+                                      float* recon, uint64_t count);
+
 // Byte offset of the counter region inside a workspace of K splits.
 size_t decode_records_bytes(uint32_t B, uint32_t Hq, uint32_t D, uint32_t K);
 

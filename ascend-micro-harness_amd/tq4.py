@@ -14,6 +14,8 @@ Reference launchers mirrored (paths relative to the reference checkout):
   paged_decode_partials   kernels/ops/turboquant/turboquant_paged_decode_attention.cpp:1727-1766
   paged_decode            kernels/ops/turboquant/baseline/turboquant_paged_attention.cpp:773-793
   splitk_combine          tests/common/l2_atomic_oracle.hpp:156-176 (host merge in the reference)
+  icdf_quantize           kernels/camodel/icdf_quantize.cpp:161-172
+  lloydmax_quantize       kernels/camodel/lloydmax_quantize.cpp:96-99
 """
 from __future__ import annotations
 
@@ -77,6 +79,10 @@ def lib():
     L.tq4_paged_decode_partials.argtypes = [_P] * 9 + [_SZ] + [_U32] * 8 + [_F32, _F32, _U32]
     L.tq4_splitk_combine.restype = _I32
     L.tq4_splitk_combine.argtypes = [_P] * 5 + [_U32] * 4 + [_F32, _U32]
+    L.tq4_icdf_quantize.restype = _I32
+    L.tq4_icdf_quantize.argtypes = [_P, _I32, _P, _P, _U32]
+    L.tq4_lloydmax_quantize.restype = _I32
+    L.tq4_lloydmax_quantize.argtypes = [_P] * 5 + [_U32] * 4
     _lib = L
     return L
 
@@ -268,9 +274,47 @@ def splitk_combine(workspace, pi_signs, num_seqs, num_heads, head_size, num_spli
     return out
 
 
+# ------------------------------------------------------------ codebooks
+def icdf_quantize(x, out=None, stream=None):
+    """FP16 or BF16 values (a multiple of 1024) -> packed signed INT4 codes of
+    RNE(14 sigmoid(x) - 7), element 2j in the low nibble of byte j."""
+    _dev(x, "x")
+    if x.dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError("icdf_quantize: x must be float16 or bfloat16")
+    if x.numel() % 1024:
+        raise ValueError("icdf_quantize: the element count must be a multiple of 1024")
+    if out is None:
+        out = torch.empty(x.numel() // 2, dtype=torch.uint8, device=x.device)
+    st = lib().tq4_icdf_quantize(_stream(stream), 1 if x.dtype == torch.bfloat16 else 0,
+                                 _ptr(x), _ptr(out), x.numel() // 1024)
+    _check(st, "icdf_quantize")
+    return out
+
+
+def lloydmax_quantize(src, bits=4, mode=0, dst=None, codes=None, stream=None):
+    """The Lloyd-Max leaf and its companions (mode as tq4_lloydmax_quantize):
+    0/1 Lloyd-Max, 2 Gaussian-CDF compander, 3 ICDF (FP16 src), 4/5 decode of
+    packed codes. Returns (dst, codes)."""
+    _dev(src, "src")
+    if mode >= 4:
+        n = src.numel() * 8 // bits
+    else:
+        n = src.numel()
+    if mode <= 2 and codes is None:
+        codes = torch.empty(n * bits // 8, dtype=torch.uint8, device=src.device)
+    if mode == 3 and codes is None:
+        codes = torch.empty(n // 2, dtype=torch.uint8, device=src.device)
+    if mode != 3 and dst is None:
+        dst = torch.empty(n, dtype=torch.float32, device=src.device)
+    st = lib().tq4_lloydmax_quantize(_stream(stream), _ptr(src), _ptr(dst), _ptr(codes), None,
+                                     bits, mode, n, 1)
+    _check(st, "lloydmax_quantize")
+    return dst, codes
+
+
 __all__ = [
     "TQ4Error", "lib", "status_string", "reshape_and_cache_a8", "reshape_and_cache_bf16",
     "reshape_scatter", "decode_workspace_bytes", "auto_splits", "decode_workspace",
-    "paged_decode", "paged_decode_partials", "splitk_combine", "TQ4_DECODE_QUERY_ROTATED",
-    "TQ4_MAX_SPLITS",
+    "paged_decode", "paged_decode_partials", "splitk_combine", "icdf_quantize",
+    "lloydmax_quantize", "TQ4_DECODE_QUERY_ROTATED", "TQ4_MAX_SPLITS",
 ]

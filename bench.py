@@ -385,6 +385,27 @@ def extra_workloads(tq4, torch, dev, w):
                            "pct_hbm_peak": round(100 * sbytes / (sms * 1e-3) / 1e9 / HBM_PEAK_GBS, 2),
                            "splits": k5, "algorithmic_bytes": sbytes, "cache": "warm (one step)"}
     log(f"batched step: {sms * 1e3:.2f} us -> {sbytes / (sms * 1e-3) / 1e9:.0f} GB/s")
+
+    # --- codebook leaves (HBM streams): Lloyd-Max 4-bit over 32M FP32 values
+    # (in + centroids + codes), ICDF over 64M FP16 values (in + codes)
+    nl = 1 << 25
+    xl = torch.randn(nl, generator=gen, device=dev)
+    rl = torch.empty_like(xl)
+    cl = torch.empty(nl // 2, dtype=torch.uint8, device=dev)
+    lms, _, _ = graph_time(torch, [lambda: tq4.lloydmax_quantize(xl, 4, 0, dst=rl, codes=cl)],
+                           20, 4)
+    lbytes = nl * (4 + 4) + nl // 2
+    xi = torch.randn(2 * nl, generator=gen, device=dev).to(torch.float16)
+    ci = torch.empty(nl, dtype=torch.uint8, device=dev)
+    ims, _, _ = graph_time(torch, [lambda: tq4.icdf_quantize(xi, out=ci)], 20, 4)
+    ibytes = 2 * nl * 2 + nl
+    out["codebook"] = {
+        "lloydmax4_32M_fp32": {"us": round(lms * 1e3, 2), "GBps": round(lbytes / (lms * 1e-3) / 1e9, 1),
+                               "algorithmic_bytes": lbytes},
+        "icdf_64M_fp16": {"us": round(ims * 1e3, 2), "GBps": round(ibytes / (ims * 1e-3) / 1e9, 1),
+                          "algorithmic_bytes": ibytes}}
+    log(f"codebook: Lloyd-Max {lbytes / (lms * 1e-3) / 1e9:.0f} GB/s, "
+        f"ICDF {ibytes / (ims * 1e-3) / 1e9:.0f} GB/s")
     return out
 
 

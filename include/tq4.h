@@ -45,7 +45,8 @@ typedef enum {
     TQ4_ERR_OUTPUT_STAGE = -7,  /* output_stage > 2, or stage 2 without gate */
     TQ4_ERR_ROTATION = -8,      /* neither pi_signs nor tables given */
     TQ4_ERR_LAUNCH = -9,        /* the HIP runtime refused the launch */
-    TQ4_ERR_RANGE = -10         /* a size exceeds what the kernels index */
+    TQ4_ERR_RANGE = -10,        /* a size exceeds what the kernels index */
+    TQ4_ERR_CODEBOOK = -11      /* codebook leaf: bits, mode or element count */
 } tq4_status;
 
 /* Human-readable name of a tq4_status. */
@@ -209,6 +210,41 @@ int tq4_splitk_combine(void* stream, const float* workspace, const float* pi_sig
                        const float* gate, uint16_t* out, uint32_t num_seqs, uint32_t num_heads,
                        uint32_t head_size, uint32_t num_splits, float inv_sqrt_len,
                        uint32_t output_stage);
+
+/* ----------------------------------------------------------------------
+ * Codebook quantiser leaves: standalone elementwise kernels over plain
+ * device arrays (no cache layout). Codes pack low bits first: code i sits at
+ * bit (i*bits) % 8 of byte i*bits/8.
+ */
+
+/* ICDF: FP16 (in_bf16 = 0) or BF16 values -> signed INT4
+ * RNE(14 / (1 + exp(-x)) - 7) saturated to [-8, 7] (NaN -> 0), two per byte,
+ * element 2j in bits [3:0] of byte j. `tiles` tiles of 1024 elements in,
+ * 512 bytes out each. Replaces launch_camodel_icdf_quantize_fp16 / _bf16
+ * (kernels/camodel/icdf_quantize.cpp:161-172); semantics of
+ * routines/routine_vector_icdf_quantize.hpp:10-30. */
+int tq4_icdf_quantize(void* stream, int in_bf16, const uint16_t* in, uint8_t* out,
+                      uint32_t tiles);
+
+/* The Lloyd-Max leaf and its companions over n*rows elements (a multiple of
+ * 8; bits 2 or 4). mode:
+ *   0, 1  Lloyd-Max: FP32 src -> codes = #{thresholds <= x} (NaN -> 0) and,
+ *         when dst is not NULL, dst = the centroid of each code
+ *         (include/routines/routine_vector_lloydmax_quantize.hpp:8-37);
+ *   2     the Gaussian-CDF compander floor(2^b / (1 + exp(-(1.5976 +
+ *         0.070565 x^2) x))) with the normal-quantile centroids
+ *         (tests/common/lloydmax_oracle.hpp:19-28);
+ *   3     the ICDF leaf on FP16 src (bits 4 only; codes as tq4_icdf_quantize,
+ *         dst unused);
+ *   4, 5  decode: src holds packed Lloyd-Max codes, dst = their centroids.
+ * Modes 0/1 and 4/5 differ in the reference only by where the codebook table
+ * lives on chip; here they are the same kernels. `guards` (the reference
+ * rig's on-chip canary dump) is ignored and may be NULL.
+ * Replaces launch_camodel_lloydmax_quantize
+ * (kernels/camodel/lloydmax_quantize.cpp:96-99). */
+int tq4_lloydmax_quantize(void* stream, const void* src, float* dst, uint8_t* codes,
+                          uint32_t* guards, uint32_t bits, uint32_t mode, uint32_t n,
+                          uint32_t rows);
 
 #ifdef __cplusplus
 }

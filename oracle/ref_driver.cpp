@@ -16,6 +16,8 @@
 //   tests/common/aic_splitk_decode_fixture.hpp    splitk_decode_test
 //   include/turboquant_splitk_contract.hpp        turboquant_splitk
 //   kernels/ops/turboquant/turboquant_decode_tail.hpp  turboquant_decode_tail
+//   tests/cpu/icdf_fixture.hpp                    icdf (ICDF leaf fixture + oracle)
+//   tests/common/lloydmax_oracle.hpp              lloyd (Lloyd-Max / Gaussian-CDF)
 
 #include "tests/common/turboquant_oracle.hpp"
 #include "tests/common/turboquant_scatter_oracle.hpp"
@@ -24,6 +26,8 @@
 #include "tests/common/aic_splitk_decode_fixture.hpp"
 #include "include/turboquant_splitk_contract.hpp"
 #include "kernels/ops/turboquant/turboquant_decode_tail.hpp"
+#include "tests/cpu/icdf_fixture.hpp"
+#include "tests/common/lloydmax_oracle.hpp"
 
 #include <cstdint>
 #include <cstring>
@@ -349,6 +353,52 @@ int ref_aic_partial(int n, int batch, int heads, int page_size, int live, int fi
     } catch (const std::exception&) {
         return -2;
     }
+}
+
+// ------------------------------------------------------------- codebooks
+// icdf::make_fixture(bf16, tiles): tiles*1024 input half/bf16 words and the
+// oracle's tiles*512 packed bytes; -2 if the fixture's own property checks fail.
+int ref_icdf_fixture(int bf16, uint32_t tiles, uint16_t* in_bits, uint8_t* packed)
+{
+    try {
+        const icdf::Fixture fx = icdf::make_fixture(bf16 != 0, tiles);
+        icdf::assert_properties(fx);
+        std::memcpy(in_bits, fx.in_bits.data(), fx.in_bits.size() * 2);
+        std::memcpy(packed, fx.oracle_packed.data(), fx.oracle_packed.size());
+        return 0;
+    } catch (const std::exception&) {
+        return -2;
+    }
+}
+
+// lloyd::fixture(n, rows, boundaries, bits): n*rows FP32 values
+void ref_lloyd_fixture(unsigned n, unsigned rows, int boundaries, unsigned bits, float* x)
+{
+    const auto v = lloyd::fixture(n, rows, boundaries != 0, bits);
+    std::memcpy(x, v.data(), v.size() * 4);
+}
+
+unsigned ref_lloyd_code(unsigned bits, float x, int sigmoid)
+{
+    return lloyd::code(bits, x, sigmoid != 0);
+}
+
+float ref_lloyd_centroid(unsigned bits, unsigned q, int sigmoid)
+{
+    return lloyd::centroid(bits, q, sigmoid != 0);
+}
+
+float ref_lloyd_threshold(unsigned bits, unsigned i)
+{
+    return bits == 2 ? ascend_micro::LloydMaxCodebook<2>::thresholds[i]
+                     : ascend_micro::LloydMaxCodebook<4>::thresholds[i];
+}
+
+void ref_lloyd_pack(const unsigned* q, unsigned n, unsigned bits, uint8_t* out)
+{
+    const std::vector<unsigned> v(q, q + n);
+    const auto p = lloyd::pack(v, bits);
+    std::memcpy(out, p.data(), p.size());
 }
 
 }  // extern "C"

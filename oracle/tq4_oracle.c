@@ -825,3 +825,155 @@ int tq4o_decode_reference_f64(const uint16_t* q, const int8_t* key_cache,
     }
     return 0;
 }
+
+/* ==================================================================== codebooks
+ * The reference's codebook quantiser leaves (standalone vector routines):
+ *   ICDF (scaled sigmoid, signed int4)  routines/routine_vector_icdf_quantize.hpp:10-30,
+ *                                       oracle tests/cpu/icdf_fixture.hpp:122-142,222-232
+ *   Lloyd-Max (2/4-bit, unsigned codes) include/routines/routine_vector_lloydmax_quantize.hpp:8-37
+ *   Gaussian-CDF compander              tests/common/lloydmax_oracle.hpp:19-28,
+ *                                       include/routines/routine_vector_gaussian_cdf_quantize.hpp:6-19
+ *   packing (low bits first)            tests/common/lloydmax_oracle.hpp:58-62
+ * Pins: the reference's fixtures through oracle/_ref (tests/golden/cb_*),
+ * plus the closed forms -- centroids are the N(0,1) conditional means of
+ * their cells, thresholds the centroid midpoints, the CDF centroids the
+ * quantiles (i + 1/2) / 2^b. */
+
+static const float kLm2Centroids[4] = {-1.510418f, -0.452794f, 0.452794f, 1.510418f};
+static const float kLm2Thresholds[3] = {-0.981606f, 0.f, 0.981606f};
+static const float kLm4Centroids[16] = {
+    -2.732589571f, -2.069017227f, -1.618046386f, -1.256231197f, -0.942340456f, -0.656759119f,
+    -0.388048299f, -0.128395030f, 0.128395030f,  0.388048299f,  0.656759119f,  0.942340456f,
+    1.256231197f,  1.618046386f,  2.069017227f,  2.732589571f};
+static const float kLm4Thresholds[15] = {
+    -2.400803399f, -1.843531806f, -1.437138792f, -1.099285827f, -0.799549788f,
+    -0.522403709f, -0.258221665f, 0.f,           0.258221665f,  0.522403709f,
+    0.799549788f,  1.099285827f,  1.437138792f,  1.843531806f,  2.400803399f};
+static const float kCdf2Centroids[4] = {-1.1503493804f, -0.318639364f, 0.318639364f,
+                                        1.1503493804f};
+static const float kCdf4Centroids[16] = {
+    -1.8627318674f, -1.3180108973f, -1.0099901692f, -0.7764217611f, -0.5791321623f,
+    -0.4022500653f, -0.2372021093f, -0.0784124127f, 0.0784124127f,  0.2372021093f,
+    0.4022500653f,  0.5791321623f,  0.7764217611f,  1.0099901692f,  1.3180108973f,
+    1.8627318674f};
+
+float tq4o_codebook_centroid(uint32_t book, uint32_t bits, uint32_t q)
+{
+    if (book == TQ4O_BOOK_LLOYDMAX) return bits == 2 ? kLm2Centroids[q & 3] : kLm4Centroids[q & 15];
+    return bits == 2 ? kCdf2Centroids[q & 3] : kCdf4Centroids[q & 15];
+}
+
+float tq4o_lloydmax_threshold(uint32_t bits, uint32_t i)
+{
+    return bits == 2 ? kLm2Thresholds[i] : kLm4Thresholds[i];
+}
+
+/* lloydmax_code<Bits>: the number of thresholds t with x >= t (ties to the
+ * upper bin; NaN compares false everywhere and gives 0)
+ * (include/routines/routine_vector_lloydmax_quantize.hpp:31-37) */
+uint32_t tq4o_lloydmax_code(uint32_t bits, float x)
+{
+    const uint32_t n = bits == 2 ? 3u : 15u;
+    uint32_t q = 0;
+    for (uint32_t i = 0; i < n; ++i) q += x >= tq4o_lloydmax_threshold(bits, i);
+    return q;
+}
+
+/* sigmoid_code<Bits>: floor(2^b / (1 + exp(-(1.5976 + 0.070565 x^2) x))),
+ * clamped to [0, 2^b - 1], in the reference oracle's FP32 operation order
+ * (tests/common/lloydmax_oracle.hpp:21-28) */
+uint32_t tq4o_gaussian_cdf_code(uint32_t bits, float x)
+{
+    const float xx = x * x;
+    const float cubic = 0.070565f * xx;
+    const float slope = cubic + 1.5976f;
+    const float z = slope * x;
+    const float e = expf(-z);
+    const float d = e + 1.f;
+    const float v = (float)(1u << bits) / d;
+    const float f = floorf(v);
+    const float lo = f > 0.f ? f : 0.f; /* std::max(0.f, f): NaN gives 0 */
+    const uint32_t u = (uint32_t)lo;
+    const uint32_t top = (1u << bits) - 1u;
+    return u < top ? u : top;
+}
+
+/* lloyd::pack: code i at bit (i*bits) % 8 of byte i*bits/8 */
+void tq4o_codebook_pack(const uint32_t* q, uint64_t n, uint32_t bits, uint8_t* out)
+{
+    memset(out, 0, (size_t)(n * bits / 8));
+    for (uint64_t i = 0; i < n; ++i) out[i * bits / 8] |= (uint8_t)(q[i] << (i * bits % 8));
+}
+
+int tq4o_codebook_quantize(uint32_t book, uint32_t bits, const float* x, uint64_t n, float* recon,
+                           uint8_t* packed)
+{
+    if ((bits != 2 && bits != 4) || book > TQ4O_BOOK_GAUSSIAN_CDF || n % (8 / bits)) return -1;
+    uint32_t* q = (uint32_t*)malloc((size_t)(n ? n : 1) * sizeof(uint32_t));
+    if (!q) return -2;
+    for (uint64_t i = 0; i < n; ++i) {
+        q[i] = book == TQ4O_BOOK_LLOYDMAX ? tq4o_lloydmax_code(bits, x[i])
+                                          : tq4o_gaussian_cdf_code(bits, x[i]);
+        if (recon) recon[i] = tq4o_codebook_centroid(book, bits, q[i]);
+    }
+    if (packed) tq4o_codebook_pack(q, n, bits, packed);
+    free(q);
+    return 0;
+}
+
+/* lloydmax_dequantize_vf: unpack, then the centroid of each code
+ * (include/routines/routine_vector_lloydmax_quantize.hpp:223-255) */
+int tq4o_codebook_dequantize(uint32_t book, uint32_t bits, const uint8_t* packed, uint64_t n,
+                             float* recon)
+{
+    if ((bits != 2 && bits != 4) || book > TQ4O_BOOK_GAUSSIAN_CDF || n % (8 / bits)) return -1;
+    for (uint64_t i = 0; i < n; ++i) {
+        const uint32_t q = (packed[i * bits / 8] >> (i * bits % 8)) & ((1u << bits) - 1u);
+        recon[i] = tq4o_codebook_centroid(book, bits, q);
+    }
+    return 0;
+}
+
+/* IEEE binary16 bits -> float (exact) */
+float tq4o_f16_to_f32(uint16_t h)
+{
+    const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    const uint32_t e = (h >> 10) & 0x1fu, m = h & 0x3ffu;
+    if (e == 31) return bits_to_f32(sign | 0x7f800000u | (m << 13));
+    if (e == 0) {
+        const float mag = (float)m * 5.9604644775390625e-08f; /* m * 2^-24, exact */
+        return sign ? -mag : mag;
+    }
+    return bits_to_f32(sign | ((e + 112u) << 23) | (m << 13));
+}
+
+/* The ICDF leaf's code of one value: y = 14 / (1 + exp(-x)) - 7 evaluated in
+ * double, rounded to nearest even, saturated to [-8, 7]
+ * (tests/cpu/icdf_fixture.hpp:122-142). NaN gives 0. */
+int tq4o_icdf_code(double x)
+{
+    if (x != x) return 0;
+    const double y = 14.0 / (1.0 + exp(-x)) - 7.0;
+    const double f = floor(y), r = y - f;
+    long long q;
+    if (r > 0.5) q = (long long)f + 1;
+    else if (r < 0.5) q = (long long)f;
+    else q = ((long long)f % 2 == 0) ? (long long)f : (long long)f + 1;
+    if (q > 7) q = 7;
+    if (q < -8) q = -8;
+    return (int)q;
+}
+
+/* FP16 / BF16 -> packed signed int4, element 2j in bits [3:0] of byte j and
+ * element 2j+1 in bits [7:4] (tests/cpu/icdf_fixture.hpp:222-232) */
+int tq4o_icdf_quantize(int in_bf16, const uint16_t* in, uint64_t n, uint8_t* packed)
+{
+    if (n % 2) return -1;
+    for (uint64_t j = 0; j < n / 2; ++j) {
+        const float a = in_bf16 ? tq4o_bf16_to_f32(in[2 * j]) : tq4o_f16_to_f32(in[2 * j]);
+        const float b = in_bf16 ? tq4o_bf16_to_f32(in[2 * j + 1]) : tq4o_f16_to_f32(in[2 * j + 1]);
+        const int q0 = tq4o_icdf_code((double)a), q1 = tq4o_icdf_code((double)b);
+        packed[j] = (uint8_t)(((q1 & 0xf) << 4) | (q0 & 0xf));
+    }
+    return 0;
+}

@@ -130,6 +130,26 @@ int64_t tq4o_reshape_and_cache_mt(int in_dtype, const void* key, const void* val
                                   uint32_t block_size, uint32_t num_blocks, float inv_sqrt_len,
                                   int policy, uint32_t threads);
 
+/* ------------------------------------------------------------- codebooks
+ * The reference's codebook quantiser leaves: ICDF (scaled sigmoid -> signed
+ * int4), Lloyd-Max and the Gaussian-CDF compander (2/4-bit unsigned codes,
+ * packed low bits first). Pins: tests/golden/cb_* from the reference's own
+ * fixtures and oracles, and the closed forms of the codebooks. */
+#define TQ4O_BOOK_LLOYDMAX 0u
+#define TQ4O_BOOK_GAUSSIAN_CDF 1u
+float tq4o_codebook_centroid(uint32_t book, uint32_t bits, uint32_t q);
+float tq4o_lloydmax_threshold(uint32_t bits, uint32_t i);
+uint32_t tq4o_lloydmax_code(uint32_t bits, float x);
+uint32_t tq4o_gaussian_cdf_code(uint32_t bits, float x);
+void tq4o_codebook_pack(const uint32_t* q, uint64_t n, uint32_t bits, uint8_t* out);
+int tq4o_codebook_quantize(uint32_t book, uint32_t bits, const float* x, uint64_t n, float* recon,
+                           uint8_t* packed);
+int tq4o_codebook_dequantize(uint32_t book, uint32_t bits, const uint8_t* packed, uint64_t n,
+                             float* recon);
+float tq4o_f16_to_f32(uint16_t h);
+int tq4o_icdf_code(double x);
+int tq4o_icdf_quantize(int in_bf16, const uint16_t* in, uint64_t n, uint8_t* packed);
+
 #ifdef __cplusplus
 }
 #endif

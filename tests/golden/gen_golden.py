@@ -20,6 +20,11 @@ provenance. Reference functions used (paths relative to the reference checkout):
          egress_reference, gate_vector          tests/common/l2_atomic_oracle.hpp
   rot_*  rot_oracle::staged, dense_left, dense_right
                                                 tests/common/rotate_butterfly_oracle.hpp
+  cb_*   icdf::make_fixture (inputs + packed bytes of the ICDF leaf's oracle)
+                                                tests/cpu/icdf_fixture.hpp
+         lloyd::fixture, lloyd::code, lloyd::centroid, lloyd::pack, thresholds
+                                                tests/common/lloydmax_oracle.hpp,
+                                                include/routines/routine_vector_lloydmax_quantize.hpp
   tail_* turboquant_splitk::Partition, turboquant_decode_tail::ActiveInStrip,
          LiveStripsInWindow                     include/turboquant_splitk_contract.hpp,
                                                 kernels/ops/turboquant/turboquant_decode_tail.hpp
@@ -233,6 +238,35 @@ def main():
     live = np.array([r.lib.ref_live_strips_in_window(*map(int, c)) for c in live_cases], np.int32)
     files["tail_partition"] = save("tail_partition", partition=part, bases=bases, seq_lens=seqs,
                                    active=active, live_cases=live_cases, live=live)
+
+    # ---- codebook leaves: ICDF (FP16/BF16 fixtures with the oracle's bytes),
+    # Lloyd-Max and the Gaussian-CDF compander (codes, centroids, packing)
+    for bf16, tag in ((0, "fp16"), (1, "bf16")):
+        tiles = 4
+        in_bits = np.zeros(tiles * 1024, np.uint16)
+        packed = np.zeros(tiles * 512, np.uint8)
+        assert r.lib.ref_icdf_fixture(bf16, tiles, ptr(in_bits), ptr(packed)) == 0
+        files[f"cb_icdf_{tag}"] = save(f"cb_icdf_{tag}", in_bits=in_bits, packed=packed)
+    for bits in (2, 4):
+        cb = {}
+        for n, rows, bnd in ((128, 1, 1), (256, 8, 1), (256, 8, 0)):
+            x = np.zeros(n * rows, np.float32)
+            r.lib.ref_lloyd_fixture(n, rows, bnd, bits, ptr(x))
+            key = f"n{n}_r{rows}_b{bnd}"
+            cb[f"x_{key}"] = x
+            for sig, book in ((0, "lm"), (1, "cdf")):
+                q = np.array([r.lib.ref_lloyd_code(bits, float(v), sig) for v in x], np.uint32)
+                pk = np.zeros(x.size * bits // 8, np.uint8)
+                r.lib.ref_lloyd_pack(ptr(q), q.size, bits, ptr(pk))
+                cb[f"codes_{book}_{key}"] = q
+                cb[f"packed_{book}_{key}"] = pk
+        cb["centroids_lm"] = np.array([r.lib.ref_lloyd_centroid(bits, i, 0) for i in range(1 << bits)],
+                                      np.float32)
+        cb["centroids_cdf"] = np.array([r.lib.ref_lloyd_centroid(bits, i, 1) for i in range(1 << bits)],
+                                       np.float32)
+        cb["thresholds_lm"] = np.array([r.lib.ref_lloyd_threshold(bits, i)
+                                        for i in range((1 << bits) - 1)], np.float32)
+        files[f"cb_lloyd_b{bits}"] = save(f"cb_lloyd_b{bits}", **cb)
 
     manifest = {}
     for name, path in files.items():

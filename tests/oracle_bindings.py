@@ -98,6 +98,53 @@ class Oracle:
         L.tq4o_record_floats.argtypes = [U32]
         L.tq4o_f32_to_bf16.restype = C.c_uint16
         L.tq4o_f32_to_bf16.argtypes = [F32]
+        L.tq4o_codebook_centroid.restype = F32
+        L.tq4o_codebook_centroid.argtypes = [U32, U32, U32]
+        L.tq4o_lloydmax_threshold.restype = F32
+        L.tq4o_lloydmax_threshold.argtypes = [U32, U32]
+        L.tq4o_lloydmax_code.restype = U32
+        L.tq4o_lloydmax_code.argtypes = [U32, F32]
+        L.tq4o_gaussian_cdf_code.restype = U32
+        L.tq4o_gaussian_cdf_code.argtypes = [U32, F32]
+        L.tq4o_codebook_pack.argtypes = [P, U64, U32, P]
+        L.tq4o_codebook_quantize.restype = I32
+        L.tq4o_codebook_quantize.argtypes = [U32, U32, P, U64, P, P]
+        L.tq4o_codebook_dequantize.restype = I32
+        L.tq4o_codebook_dequantize.argtypes = [U32, U32, P, U64, P]
+        L.tq4o_f16_to_f32.restype = F32
+        L.tq4o_f16_to_f32.argtypes = [C.c_uint16]
+        L.tq4o_icdf_code.restype = I32
+        L.tq4o_icdf_code.argtypes = [C.c_double]
+        L.tq4o_icdf_quantize.restype = I32
+        L.tq4o_icdf_quantize.argtypes = [I32, P, U64, P]
+
+    # ------------------------------------------------------------ codebooks
+    def codebook_quantize(self, book, bits, x):
+        """(recon float32[n], packed uint8[n*bits/8]) of the Lloyd-Max (book 0)
+        or Gaussian-CDF (book 1) leaf."""
+        x = np.ascontiguousarray(x, np.float32).reshape(-1)
+        recon = np.zeros_like(x)
+        packed = np.zeros(x.size * bits // 8, np.uint8)
+        assert self.lib.tq4o_codebook_quantize(book, bits, ptr(x), x.size, ptr(recon),
+                                               ptr(packed)) == 0
+        return recon, packed
+
+    def codebook_codes(self, book, bits, x):
+        fn = self.lib.tq4o_lloydmax_code if book == 0 else self.lib.tq4o_gaussian_cdf_code
+        return np.array([fn(bits, float(v)) for v in np.asarray(x, np.float32).reshape(-1)],
+                        np.uint32)
+
+    def codebook_dequantize(self, book, bits, packed, n):
+        packed = np.ascontiguousarray(packed, np.uint8)
+        recon = np.zeros(n, np.float32)
+        assert self.lib.tq4o_codebook_dequantize(book, bits, ptr(packed), n, ptr(recon)) == 0
+        return recon
+
+    def icdf_quantize(self, in_bits, bf16):
+        in_bits = np.ascontiguousarray(in_bits, np.uint16).reshape(-1)
+        out = np.zeros(in_bits.size // 2, np.uint8)
+        assert self.lib.tq4o_icdf_quantize(int(bf16), ptr(in_bits), in_bits.size, ptr(out)) == 0
+        return out
 
     # ------------------------------------------------------------ rotation
     def canonical_signs(self, d):
@@ -253,3 +300,13 @@ class Ref:
         L.ref_splitk_fixture.argtypes = [I32] * 7 + [P] * 8
         L.ref_aic_partial.restype = I32
         L.ref_aic_partial.argtypes = [I32] * 8 + [U32, U32, P, P, P]
+        L.ref_icdf_fixture.restype = I32
+        L.ref_icdf_fixture.argtypes = [I32, U32, P, P]
+        L.ref_lloyd_fixture.argtypes = [U32, U32, I32, U32, P]
+        L.ref_lloyd_code.restype = U32
+        L.ref_lloyd_code.argtypes = [U32, F32, I32]
+        L.ref_lloyd_centroid.restype = F32
+        L.ref_lloyd_centroid.argtypes = [U32, U32, I32]
+        L.ref_lloyd_threshold.restype = F32
+        L.ref_lloyd_threshold.argtypes = [U32, U32]
+        L.ref_lloyd_pack.argtypes = [P, U32, U32, P]

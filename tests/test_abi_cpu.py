@@ -32,7 +32,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 def test_status_strings_and_version(lib):
     assert lib.tq4_status_string(0) == b"ok"
-    for st in range(-10, 0):
+    for st in range(-11, 0):
         assert lib.tq4_status_string(st) != b"unknown status"
     assert lib.tq4_version() >> 16 == 1
 
@@ -88,3 +88,22 @@ def test_scatter_refusals(lib):
     assert f(None, 0, d, d, d, d, d, d, d, None, None, 1, 2, 48, 16, 4, 0, 2, 0.1) == -2
     assert f(None, 0, d, d, d, d, d, d, None, None, None, 1, 2, 128, 16, 4, 0, 2, 0.1) == -1
     assert f(None, 0, d, d, d, d, d, d, d, None, None, 1, 2, 128, 16, 4, 0, 0, 0.1) == 0
+
+
+def test_codebook_refusals(lib):
+    d = C.c_void_p(16)
+    f = lib.tq4_lloydmax_quantize
+    f.argtypes = [C.c_void_p] * 5 + [C.c_uint32] * 4
+    assert f(None, d, d, d, None, 3, 0, 128, 1) == -11   # bits
+    assert f(None, d, d, d, None, 4, 6, 128, 1) == -11   # mode
+    assert f(None, d, d, d, None, 4, 0, 12, 1) == -11    # not a multiple of 8
+    assert f(None, d, d, d, None, 2, 3, 128, 1) == -11   # ICDF is 4-bit only
+    assert f(None, None, d, d, None, 4, 0, 128, 1) == -1
+    assert f(None, d, d, None, None, 4, 2, 128, 1) == -1  # codes needed
+    assert f(None, d, None, d, None, 4, 4, 128, 1) == -1  # decode needs dst
+    assert f(None, d, d, d, None, 4, 0, 0, 1) == 0        # nothing to do
+    g = lib.tq4_icdf_quantize
+    g.argtypes = [C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_uint32]
+    assert g(None, 0, None, d, 1) == -1
+    assert g(None, 1, d, d, 0) == 0
+
