@@ -18,6 +18,14 @@ bool head_size_ok(uint32_t d) { return d == 64 || d == 128 || d == 256; }
 
 int launched(hipError_t e) { return e == hipSuccess ? TQ4_OK : TQ4_ERR_LAUNCH; }
 
+// Fused-decode workspace tail: the work-queue counter of the persistent
+// kernel (one 256-byte block), then one split-ticket word per (seq, kv head).
+constexpr size_t kQueueBytes = 256;
+size_t ticket_bytes(uint32_t num_seqs, uint32_t num_kv_heads)
+{
+    return ((size_t)num_seqs * num_kv_heads * sizeof(uint32_t) + 255) & ~(size_t)255;
+}
+
 int writer_checks(const void* key, const void* value, const int8_t* key_cache,
                   const int8_t* value_cache, const float* scale_cache, const int32_t* slots,
                   const float* pi_signs, const int32_t* tables, uint32_t num_tokens,
@@ -133,7 +141,7 @@ size_t tq4_decode_workspace_bytes(uint32_t num_seqs, uint32_t num_heads, uint32_
 {
     if (num_splits == 0) num_splits = TQ4_MAX_SPLITS;
     return tq4::decode_records_bytes(num_seqs, num_heads, head_size, num_splits) +
-           (((size_t)num_seqs * num_kv_heads * sizeof(uint32_t) + 255) & ~(size_t)255);
+           kQueueBytes + ticket_bytes(num_seqs, num_kv_heads);
 }
 
 uint32_t tq4_decode_auto_splits(uint32_t num_seqs, uint32_t num_kv_heads,
@@ -261,11 +269,12 @@ int tq4_paged_decode(void* stream, const uint16_t* q, const int8_t* key_cache,
         if (!workspace || workspace_bytes < need || ((uintptr_t)workspace & 15u))
             return TQ4_ERR_WORKSPACE;
         p.records = (float*)workspace;
-        // The counters sit at the END of the workspace so their place does not
-        // depend on num_splits: a workspace zeroed once serves every split count.
-        p.counters = (uint32_t*)((char*)workspace + workspace_bytes -
-                                 (((size_t)num_seqs * num_kv_heads * sizeof(uint32_t) + 255) &
-                                  ~(size_t)255));
+        // The tickets sit at the END of the workspace and the work-queue
+        // counter just before them, so their place does not depend on
+        // num_splits: a workspace zeroed once serves every split count.
+        char* end = (char*)workspace + workspace_bytes;
+        p.counters = (uint32_t*)(end - ticket_bytes(num_seqs, num_kv_heads));
+        p.queue = (uint32_t*)(end - ticket_bytes(num_seqs, num_kv_heads) - kQueueBytes);
     }
     return launched(tq4::launch_decode((hipStream_t)stream, p, 1));
 }

@@ -80,6 +80,7 @@ constexpr uint32_t kFlagRotated = 1u;
 constexpr int kHdrFloats = 416;          // m_x, l_x [16][4], q_exp[16], flags, 2^-sh[4], scale slots [4][64]
 constexpr uint32_t kRecMagic = 0x7FBADBADu;  // fused records hold bits ^ kRecMagic; 0 = not written
 constexpr uint32_t kPollLimit = 1u << 20;     // bound of the combiner's record polls
+constexpr uint32_t kPersistentMaxSeqs = 8192; // the persistent kernel stages one word per sequence
 
 // Eight codes of one dword as fp16 (1 + u/64), u = nibble ^ 8; halves in
 // nibble order 0,4,1,5,2,6,3,7 (every operand built against this table uses
@@ -383,12 +384,11 @@ __host__ __device__ constexpr size_t region_floats(uint32_t G, uint32_t D)
     return 4ull * G * D;  // q staging [G][D], then the four waves' rows [4][G][D]
 }
 
-// Waves per SIMD the register ring allows without spilling: three at
-// d = 64, two at d = 128 (<= 256 VGPRs), one at d = 256.
+// One (seq, kv head, split) work item: MODE 0 exports the partial record,
+// MODE 1 is the fused path (ticket, export or local finish, combine).
 template <int D, int MODE>
-__global__ __launch_bounds__(kThreads)
-__attribute__((amdgpu_waves_per_eu(D == 64 ? 3 : (D == 128 ? 2 : 1), D == 64 ? 3 : 2)))
-void decode_kernel(DecodeParams p)
+__device__ __forceinline__ void decode_item(const DecodeParams& p, const uint32_t seq,
+                                            const uint32_t kvh, const uint32_t split)
 {
     constexpr int CPL = D / 64;   // channels per lane in the row layout
     constexpr int NJ = D / 32;    // score MFMAs per token set (one per key dword)
@@ -411,10 +411,6 @@ void decode_kernel(DecodeParams p)
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
     const int n = lane & 15, g4 = lane >> 4;
     const int half = g4 & 1, sp = g4 >> 1;  // value/scale lanes: strip sp of the pair, tokens 8*half..
-    const uint32_t item = blockIdx.x;
-    const uint32_t split = item % p.K;
-    const uint32_t kvh = (item / p.K) % p.Hkv;
-    const uint32_t seq = item / (p.K * p.Hkv);
 
     // ---- phase 0: every small load -- context length, q rows, rotation
     // signs, the split's block-table window -- is issued before any strip
@@ -914,6 +910,102 @@ void decode_kernel(DecodeParams p)
     }
 }
 
+// Waves per SIMD the register ring allows without spilling: three at
+// d = 64, two at d = 128 (<= 256 VGPRs), one at d = 256.
+#define TQ4_DECODE_ATTRS                                                                   \
+    __launch_bounds__(kThreads)                                                            \
+    __attribute__((amdgpu_waves_per_eu(D == 64 ? 3 : (D == 128 ? 2 : 1), D == 64 ? 3 : 2)))
+
+// One workgroup per (seq, kv head, split), splits fastest.
+template <int D, int MODE>
+__global__ TQ4_DECODE_ATTRS void decode_kernel(DecodeParams p)
+{
+    const uint32_t item = blockIdx.x;
+    decode_item<D, MODE>(p, item / (p.K * p.Hkv), (item / p.K) % p.Hkv, item % p.K);
+}
+
+// Persistent fused decode for launches with more work items than
+// workgroup slots. The items are the LIVE (seq, kv head, split) triples only
+// -- a sequence contributes num_kv_heads * max(1, its live splits) -- in
+// (seq, kv head, split) order, enumerated by every workgroup from the
+// context lengths (an inclusive prefix over sequences, staged in LDS). A
+// workgroup takes item blockIdx.x, then one item at a time from an
+// agent-scope queue counter, fetched as the current item starts so the round
+// trip hides under it. Each of the n_items fetches returns a distinct value
+// and the one that returns n_items - 1 is the last: it resets the counter
+// (every workgroup's final fetch is its failing one, so the fetches number
+// exactly n_items). Nothing waits on a workgroup that has not started: the
+// combiner of a (seq, kv head) waits only for splits that took their ticket
+// before it, each in the hands of a running workgroup that only streams and
+// exports before it fetches again.
+template <int D>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D == 256 ? 1 : 2, 2)))
+void decode_persistent_kernel(DecodeParams p)
+{
+    extern __shared__ float smem[];
+    uint32_t* live = (uint32_t*)(smem + kHdrFloats + TQ4_MAX_SPLIT_STRIPS + region_floats(p.G, D));
+    uint32_t* next_lds = (uint32_t*)(smem + 145);
+    const int tid = threadIdx.x, lane = tid & 63;
+    const uint32_t width = (p.max_blocks + p.K - 1) / p.K;
+    const uint64_t capacity = (uint64_t)p.max_blocks * p.S;
+    for (uint32_t s = tid; s < p.B; s += kThreads) {
+        const int32_t c = p.context_lens[s];
+        uint64_t ctx = c < 0 ? 0u : (uint64_t)c;
+        if (ctx > capacity) ctx = capacity;
+        const uint32_t pages = (uint32_t)((ctx + p.S - 1) / p.S);
+        const uint32_t kl = (pages + width - 1) / width;
+        live[s] = p.Hkv * (kl > 0 ? kl : 1u);
+    }
+    __syncthreads();
+    if (tid < 64) {  // inclusive prefix, 64 sequences per step
+        uint32_t carry = 0;
+        for (uint32_t b = 0; b < p.B; b += 64) {
+            const uint32_t i = b + lane;
+            uint32_t v = i < p.B ? live[i] : 0u;
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const uint32_t u = __shfl_up(v, o, 64);
+                if (lane >= o) v += u;
+            }
+            v += carry;
+            if (i < p.B) live[i] = v;
+            carry = __shfl(v, 63, 64);
+        }
+    }
+    __syncthreads();
+    const uint32_t n_items = live[p.B - 1];
+    uint32_t item = blockIdx.x;
+    while (item < n_items) {
+        uint32_t fetched = 0;
+        if (tid == 0)
+            fetched = __hip_atomic_fetch_add(p.queue, 1u, __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT);
+        // its sequence: the first s with live[s] > item
+        uint32_t seq = 0;
+        for (uint32_t b = 0; b < p.B; b += 64) {
+            const uint32_t i = b + lane;
+            const uint64_t m = __ballot(i < p.B && live[i] > item);
+            if (m != 0) {
+                seq = b + (uint32_t)__builtin_ctzll(m);
+                break;
+            }
+        }
+        seq = __builtin_amdgcn_readfirstlane(seq);
+        const uint32_t base = seq > 0 ? live[seq - 1] : 0u;
+        const uint32_t kl = (live[seq] - base) / p.Hkv;
+        const uint32_t r = item - base;
+        decode_item<D, 1>(p, seq, r / kl, r % kl);
+        if (tid == 0) {
+            if (fetched == n_items - 1)
+                __hip_atomic_store(p.queue, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            *next_lds = gridDim.x + fetched;
+        }
+        __syncthreads();
+        item = __builtin_amdgcn_readfirstlane(*next_lds);
+        __syncthreads();
+    }
+}
+
 // Stand-alone combine: 16 consecutive (seq, q head) rows per workgroup, four
 // per wave.
 template <int D>
@@ -942,17 +1034,43 @@ __global__ void fill_zero_kernel(uint32_t* ptr, size_t words)
         ptr[i] = 0u;
 }
 
+// Workgroup slots of the persistent kernel on the current device (CUs x
+// resident workgroups per CU at this LDS size), 0 if it cannot run.
+template <int D>
+uint32_t persistent_slots(size_t lds)
+{
+    int dev = 0, cus = 0, per_cu = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        return 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_persistent_kernel<D>,
+                                                     kThreads, lds) != hipSuccess)
+        return 0;
+    return cus > 0 && per_cu > 0 ? (uint32_t)cus * (uint32_t)per_cu : 0u;
+}
+
 template <int D>
 hipError_t launch_decode_t(hipStream_t stream, const DecodeParams& p, int mode)
 {
     const size_t blocks = (size_t)p.B * p.Hkv * p.K;
     const size_t lds = (kHdrFloats + TQ4_MAX_SPLIT_STRIPS + region_floats(p.G, D)) * sizeof(float);
-    if (mode == 0)
+    if (mode == 0) {
         hipLaunchKernelGGL((decode_kernel<D, 0>), dim3((uint32_t)blocks), dim3(kThreads), lds,
                            stream, p);
-    else
-        hipLaunchKernelGGL((decode_kernel<D, 1>), dim3((uint32_t)blocks), dim3(kThreads), lds,
-                           stream, p);
+        return hipGetLastError();
+    }
+    // Fused: persistent when the split grid outnumbers the resident slots.
+    if (p.queue != nullptr && p.K > 1 && p.B <= kPersistentMaxSeqs) {
+        const size_t lds_p = lds + (size_t)p.B * sizeof(uint32_t);
+        const uint32_t slots = persistent_slots<D>(lds_p);
+        if (slots > 0 && blocks > slots) {
+            hipLaunchKernelGGL((decode_persistent_kernel<D>), dim3(slots), dim3(kThreads), lds_p,
+                               stream, p);
+            return hipGetLastError();
+        }
+    }
+    hipLaunchKernelGGL((decode_kernel<D, 1>), dim3((uint32_t)blocks), dim3(kThreads), lds, stream,
+                       p);
     return hipGetLastError();
 }
 

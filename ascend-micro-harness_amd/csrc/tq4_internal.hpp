@@ -32,7 +32,8 @@ struct DecodeParams {
     const float* pi_signs;
     const float* gate;
     float* records;       // [B][Hq][K][D+4] partial records (may be null when K == 1 fused)
-    uint32_t* counters;   // [B][Hkv] arrival counters (fused only)
+    uint32_t* counters;   // [B][Hkv] split tickets (fused only)
+    uint32_t* queue;      // work-queue counter of the persistent fused kernel (or null)
     uint16_t* out;        // [B][Hq][D] bf16 (fused / combine)
     uint32_t B, Hq, Hkv, G, D, S, P, max_blocks, K;
     float scale, inv_sqrt_len;

@@ -196,3 +196,64 @@ def test_fused_repeated_calls_reset_counters(tq4, oracle):
     for o in outs:
         check_out(o, want, "repeat")
         assert np.array_equal(o, outs[0])
+
+
+def test_persistent_ragged_batch(tq4, oracle):
+    """More (seq, kv head, split) items than resident workgroups: the fused
+    entry runs its persistent form (live items only, a work queue). Ragged
+    lengths incl. empty and one-token contexts."""
+    rng = np.random.default_rng(0x5E11)
+    ctx = [0, 1, 17, 4103, 2000, 15, 16, 33] + [int(x) for x in rng.integers(1, 3000, 56)]
+    got, want, _ = run_decode(tq4, oracle, rng, ctx, 16, 4, 128, 16,
+                              sum((c + 15) // 16 for c in ctx) + 8, 16)
+    check_out(got, want, "persistent ragged")
+
+
+def test_persistent_fewer_live_items_than_slots(tq4, oracle):
+    """A large split grid whose live items are fewer than the resident
+    workgroups: the surplus workgroups leave at once, nobody fetches."""
+    rng = np.random.default_rng(0x5E12)
+    ctx = [int(x) for x in rng.integers(0, 40, 48)] + [900]
+    got, want, _ = run_decode(tq4, oracle, rng, ctx, 8, 8, 128, 16,
+                              sum((c + 15) // 16 for c in ctx) + 8, 64)
+    check_out(got, want, "persistent sparse")
+
+
+def test_persistent_repeat_and_graph(tq4, oracle):
+    """The queue counter resets itself: calls in a row and HIP-graph replays
+    on one workspace all give the first call's bits."""
+    import torch
+    rng = np.random.default_rng(0x5E13)
+    ctx = [int(x) for x in rng.integers(200, 2500, 40)]
+    P = sum((c + 15) // 16 for c in ctx) + 8
+    kc, vc, sc, tables, signs, isl = build_cache(oracle, rng, ctx, 4, 128, 16, P)
+    q = f32_to_bf16(rng.standard_normal((len(ctx), 16, 128)).astype(np.float32))
+    scale = np.float32(1 / math.sqrt(128))
+    want16, want = oracle.paged_decode(q, kc, vc, sc, tables, np.array(ctx, np.int32), signs,
+                                       None, 16, 4, 128, 16, P, 12, scale, isl, 1, threads=8)
+    args = [dev(q), dev(kc), dev(vc), dev(sc), dev(tables), dev(np.array(ctx, np.int32)),
+            dev(signs)]
+    ws = tq4.decode_workspace(len(ctx), 16, 4, 128, 12)
+    out = torch.empty_like(args[0])
+    call = lambda: tq4.paged_decode(*args, 4, 16, P, out=out, workspace=ws, num_splits=12,
+                                    scale=float(scale), inv_sqrt_len=float(isl))
+    call()
+    first = host(out).copy()
+    check_out(first, want, "persistent first")
+    for _ in range(3):
+        call()
+        assert np.array_equal(host(out), first)
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        call()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g):
+        call()
+    for _ in range(3):
+        g.replay()
+        assert np.array_equal(host(out), first)
+        call()
+        assert np.array_equal(host(out), first)
