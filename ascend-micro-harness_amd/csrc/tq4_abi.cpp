@@ -147,14 +147,15 @@ size_t tq4_decode_workspace_bytes(uint32_t num_seqs, uint32_t num_heads, uint32_
 uint32_t tq4_decode_auto_splits(uint32_t num_seqs, uint32_t num_kv_heads,
                                 uint32_t max_blocks_per_seq, uint32_t block_size)
 {
-    // Splits of ~64 strips (32 MFMA pairs over four waves), enough
-    // workgroups to fill every CU's two slots (256 CUs), but never fewer than
-    // 16 strips per split (the combine and the prologue stay a small share),
-    // and at most 64 splits (one or two record chunks per combine). Splits
-    // past a short sequence's end cost a single context-length load.
+    // Splits of ~128 strips (64 MFMA pairs over four waves: the per-item
+    // prologue and combine stay a small share, and a large batch runs the
+    // persistent kernel over few, long items), but enough workgroups to fill
+    // every CU's two slots (256 CUs) when the batch is small, never fewer
+    // than 16 strips per split, and at most 64 splits (one to four record
+    // chunks per combine).
     const uint64_t strips = (uint64_t)max_blocks_per_seq * (block_size / kStrip);
     const uint64_t items = (uint64_t)num_seqs * num_kv_heads;
-    uint64_t k = (strips + 63) / 64;
+    uint64_t k = (strips + 127) / 128;
     const uint64_t fill = items == 0 ? 1 : (512 + items - 1) / items;
     if (k < fill) k = fill;
     const uint64_t by_len = strips / 16 > 0 ? strips / 16 : 1;
