@@ -80,7 +80,7 @@ constexpr uint32_t kFlagRotated = 1u;
 constexpr int kHdrFloats = 416;          // m_x, l_x [16][4], q_exp[16], flags, 2^-sh[4], scale slots [4][64]
 constexpr uint32_t kRecMagic = 0x7FBADBADu;  // fused records hold bits ^ kRecMagic; 0 = not written
 constexpr uint32_t kPollLimit = 1u << 20;     // bound of the combiner's record polls
-constexpr uint32_t kPersistentMaxSeqs = 8192; // the persistent kernel stages one word per sequence
+constexpr uint32_t kPersistentMaxSeqs = 4096; // the persistent kernel stages two words per sequence
 
 // Eight codes of one dword as fp16 (1 + u/64), u = nibble ^ 8; halves in
 // nibble order 0,4,1,5,2,6,3,7 (every operand built against this table uses
@@ -925,25 +925,28 @@ __global__ TQ4_DECODE_ATTRS void decode_kernel(DecodeParams p)
 }
 
 // Persistent fused decode for launches with more work items than
-// workgroup slots. The items are the LIVE (seq, kv head, split) triples only
-// -- a sequence contributes num_kv_heads * max(1, its live splits) -- in
-// (seq, kv head, split) order, enumerated by every workgroup from the
-// context lengths (an inclusive prefix over sequences, staged in LDS). A
-// workgroup takes item blockIdx.x, then one item at a time from an
-// agent-scope queue counter, fetched as the current item starts so the round
-// trip hides under it. Each of the n_items fetches returns a distinct value
-// and the one that returns n_items - 1 is the last: it resets the counter
-// (every workgroup's final fetch is its failing one, so the fetches number
-// exactly n_items). Nothing waits on a workgroup that has not started: the
-// combiner of a (seq, kv head) waits only for splits that took their ticket
-// before it, each in the hands of a running workgroup that only streams and
-// exports before it fetches again.
+// workgroup slots. The items are the LIVE (seq, kv head, split) triples only.
+// Every split but a sequence's last covers exactly the partition width, so
+// the queue lists those equal items first -- (seq, kv head, split) order --
+// and the last, shorter splits after them (one per (seq, kv head), or the
+// zero-context item of an empty sequence), where their spread of sizes packs
+// the tail. Every workgroup derives the order from the context lengths (a
+// prefix over sequences, staged in LDS). A workgroup takes item blockIdx.x,
+// then one item at a time from an agent-scope queue counter, fetched as the
+// current item starts so the round trip hides under it. Each of the n_items
+// fetches returns a distinct value and the one that returns n_items - 1 is
+// the last: it resets the counter (every workgroup's final fetch is its
+// failing one, so the fetches number exactly n_items). Nothing waits on a
+// workgroup that has not started: the combiner of a (seq, kv head) waits only
+// for splits that took their ticket before it, each in the hands of a running
+// workgroup that only streams and exports before it fetches again.
 template <int D>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D == 256 ? 1 : 2, 2)))
 void decode_persistent_kernel(DecodeParams p)
 {
     extern __shared__ float smem[];
-    uint32_t* live = (uint32_t*)(smem + kHdrFloats + TQ4_MAX_SPLIT_STRIPS + region_floats(p.G, D));
+    uint32_t* full = (uint32_t*)(smem + kHdrFloats + TQ4_MAX_SPLIT_STRIPS + region_floats(p.G, D));
+    uint32_t* splits = full + p.B;  // max(1, live splits) per sequence
     uint32_t* next_lds = (uint32_t*)(smem + 145);
     const int tid = threadIdx.x, lane = tid & 63;
     const uint32_t width = (p.max_blocks + p.K - 1) / p.K;
@@ -953,48 +956,61 @@ void decode_persistent_kernel(DecodeParams p)
         uint64_t ctx = c < 0 ? 0u : (uint64_t)c;
         if (ctx > capacity) ctx = capacity;
         const uint32_t pages = (uint32_t)((ctx + p.S - 1) / p.S);
-        const uint32_t kl = (pages + width - 1) / width;
-        live[s] = p.Hkv * (kl > 0 ? kl : 1u);
+        uint32_t kl = (pages + width - 1) / width;
+        kl = kl > 0 ? kl : 1u;
+        splits[s] = kl;
+        full[s] = p.Hkv * (kl - 1);
     }
     __syncthreads();
-    if (tid < 64) {  // inclusive prefix, 64 sequences per step
+    if (tid < 64) {  // inclusive prefix of the full items, 64 sequences per step
         uint32_t carry = 0;
         for (uint32_t b = 0; b < p.B; b += 64) {
             const uint32_t i = b + lane;
-            uint32_t v = i < p.B ? live[i] : 0u;
+            uint32_t v = i < p.B ? full[i] : 0u;
 #pragma unroll
             for (int o = 1; o < 64; o <<= 1) {
                 const uint32_t u = __shfl_up(v, o, 64);
                 if (lane >= o) v += u;
             }
             v += carry;
-            if (i < p.B) live[i] = v;
+            if (i < p.B) full[i] = v;
             carry = __shfl(v, 63, 64);
         }
     }
     __syncthreads();
-    const uint32_t n_items = live[p.B - 1];
+    const uint32_t n_full = full[p.B - 1];
+    const uint32_t n_items = n_full + p.B * p.Hkv;
     uint32_t item = blockIdx.x;
     while (item < n_items) {
         uint32_t fetched = 0;
         if (tid == 0)
             fetched = __hip_atomic_fetch_add(p.queue, 1u, __ATOMIC_RELAXED,
                                              __HIP_MEMORY_SCOPE_AGENT);
-        // its sequence: the first s with live[s] > item
-        uint32_t seq = 0;
-        for (uint32_t b = 0; b < p.B; b += 64) {
-            const uint32_t i = b + lane;
-            const uint64_t m = __ballot(i < p.B && live[i] > item);
-            if (m != 0) {
-                seq = b + (uint32_t)__builtin_ctzll(m);
-                break;
+        uint32_t seq, kvh, split;
+        if (item < n_full) {
+            // a full split: its sequence is the first s with full[s] > item
+            uint32_t sq = 0;
+            for (uint32_t b = 0; b < p.B; b += 64) {
+                const uint32_t i = b + lane;
+                const uint64_t m = __ballot(i < p.B && full[i] > item);
+                if (m != 0) {
+                    sq = b + (uint32_t)__builtin_ctzll(m);
+                    break;
+                }
             }
+            seq = __builtin_amdgcn_readfirstlane(sq);
+            const uint32_t r = item - (seq > 0 ? full[seq - 1] : 0u);
+            const uint32_t per = splits[seq] - 1;
+            kvh = r / per;
+            split = r % per;
+        } else {
+            // a last split
+            const uint32_t r = item - n_full;
+            seq = r / p.Hkv;
+            kvh = r % p.Hkv;
+            split = splits[seq] - 1;
         }
-        seq = __builtin_amdgcn_readfirstlane(seq);
-        const uint32_t base = seq > 0 ? live[seq - 1] : 0u;
-        const uint32_t kl = (live[seq] - base) / p.Hkv;
-        const uint32_t r = item - base;
-        decode_item<D, 1>(p, seq, r / kl, r % kl);
+        decode_item<D, 1>(p, seq, kvh, split);
         if (tid == 0) {
             if (fetched == n_items - 1)
                 __hip_atomic_store(p.queue, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1061,7 +1077,7 @@ hipError_t launch_decode_t(hipStream_t stream, const DecodeParams& p, int mode)
     }
     // Fused: persistent when the split grid outnumbers the resident slots.
     if (p.queue != nullptr && p.K > 1 && p.B <= kPersistentMaxSeqs) {
-        const size_t lds_p = lds + (size_t)p.B * sizeof(uint32_t);
+        const size_t lds_p = lds + 2 * (size_t)p.B * sizeof(uint32_t);
         const uint32_t slots = persistent_slots<D>(lds_p);
         if (slots > 0 && blocks > slots) {
             hipLaunchKernelGGL((decode_persistent_kernel<D>), dim3(slots), dim3(kThreads), lds_p,

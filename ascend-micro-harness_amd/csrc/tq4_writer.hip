@@ -7,8 +7,9 @@
 //                    read-modify-write of the value strip
 //                    (turboquant_reshape_scatter_aiv.cpp:598-731)
 //
-// Work decomposition (MI355X): one 256-lane workgroup owns one
-// (strip, head, plane) panel of 16 rows x d channels. A row lives on 16
+// Work decomposition (MI355X): one 256-lane workgroup owns one strip of two
+// heads (one for an odd head count), both planes: four (two) panels of 16
+// rows x d channels, one row of each per 16-lane group. A row lives on 16
 // lanes with CPL = d/16 consecutive channels per lane, so the 16-point
 // Hadamard stages below CPL are in-register and the rest are lane exchanges
 // inside the row; a strip's 16 rows are the workgroup's 16 row groups.
@@ -139,18 +140,12 @@ __device__ __forceinline__ void store_key_codes(int8_t* dst, const int (&q)[CPL]
     }
 }
 
-// Pack 8 LDS nibble bytes (one per token, value in the low nibble) into one
-// word: byte k = t[2k] | t[2k+1] << 4.
-__device__ __forceinline__ uint32_t pack8(uint32_t lo4, uint32_t hi4)
-{
-    const uint32_t a = lo4 | (lo4 >> 4);  // bytes 0 and 2 hold the two pairs
-    const uint32_t b = hi4 | (hi4 >> 4);
-    return (a & 0xffu) | ((a >> 8) & 0xff00u) | ((b & 0xffu) << 16) | ((b << 8) & 0xff000000u);
-}
-
 // ------------------------------------------------------------ strip writer
-// grid.x = strips * H * 2; block = (strip, head, plane), plane fastest.
-template <int D, typename In>
+// grid.x = strips * (H / NH); a workgroup owns one strip of NH heads, both
+// planes: every lane runs 2*NH independent row jobs (plane fastest), all of
+// whose loads go out before the first rotation, and the launch has 2*NH
+// times fewer waves to dispatch than one workgroup per (strip, head, plane).
+template <int D, typename In, int NH>
 __global__ __launch_bounds__(kWriterThreads) void strip_writer(
     const In* __restrict__ key, const In* __restrict__ value, int8_t* __restrict__ key_cache,
     int8_t* __restrict__ value_cache, float* __restrict__ scale_cache,
@@ -159,21 +154,30 @@ __global__ __launch_bounds__(kWriterThreads) void strip_writer(
     float inv_sqrt_len)
 {
     constexpr int CPL = D / 16;
-    __shared__ uint32_t lds_codes[D * kStrip / 4];  // [channel][token] bytes
+    constexpr int NJ = 2 * NH;
+    constexpr int TS = 20;       // token stride of the transpose buffer, in words
+    // per value job: [channel / 8][token, padded to TS] words of 8 channel
+    // codes; 20-word rows put the 64 lanes of a wave (16 lanes x 4 tokens)
+    // on distinct banks
+    __shared__ __align__(16) uint32_t lds_t[NH][D / 8][TS];
 
-    const uint32_t plane = blockIdx.x & 1u;
-    const uint32_t head = (blockIdx.x >> 1) % H;
-    const uint32_t strip = (blockIdx.x >> 1) / H;
+    const uint32_t groups = H / NH;
+    const uint32_t head0 = (blockIdx.x % groups) * NH;
+    const uint32_t strip = blockIdx.x / groups;
     const int tid = threadIdx.x;
     const int row = tid >> 4;        // token within the strip
     const int lane_in_row = tid & 15;
 
-    // The row and the signs do not depend on the slots: their loads go out
+    // The rows and the signs do not depend on the slots: their loads go out
     // together with the slot loads (one round trip, not two).
-    const In* src = (plane == 0 ? key : value) +
-                    ((size_t)((size_t)strip * kStrip + row) * H + head) * D + lane_in_row * CPL;
-    float v[CPL], sign[CPL];
-    load_row<CPL>(src, v);
+    float v[NJ][CPL], sign[CPL];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+        const In* src = ((j & 1) == 0 ? key : value) +
+                        ((size_t)((size_t)strip * kStrip + row) * H + head0 + j / 2) * D +
+                        lane_in_row * CPL;
+        load_row<CPL>(src, v[j]);
+    }
     load_signs<CPL>(pi_signs, tables, tables_bf16, lane_in_row * CPL, sign);
 
     // Slot contract for this strip: consecutive, strip-aligned, in range.
@@ -184,29 +188,61 @@ __global__ __launch_bounds__(kWriterThreads) void strip_writer(
     if (!__syncthreads_and(ok)) return;
     const uint32_t page = (uint32_t)slot0 / S;
     const uint32_t tip = (uint32_t)slot0 % S + (uint32_t)row;
-    int q[CPL];
-    const float scale =
-        rotate_quantise<D, CPL>(v, sign, lane_in_row, inv_sqrt_len, kPolicyPrefill, q);
-
-    if (lane_in_row == 0)
-        scale_cache[(((size_t)plane * P + page) * H + head) * S + tip] = scale;
-
-    const size_t head_base = ((size_t)page * H + head) * S;  // in tokens
-    if (plane == 0) {
-        store_key_codes<CPL>(key_cache + (head_base + tip) * (D / 2) + lane_in_row * (CPL / 2), q);
-        return;
-    }
-    // Value plane: transpose through LDS, then one contiguous strip store.
-    uint8_t* lds = (uint8_t*)lds_codes;
+    int q[NJ][CPL];
+    float scale[NJ];
 #pragma unroll
-    for (int j = 0; j < CPL; ++j) lds[(lane_in_row * CPL + j) * kStrip + row] = (uint8_t)(q[j] & 0xf);
+    for (int j = 0; j < NJ; ++j)
+        scale[j] = rotate_quantise<D, CPL>(v[j], sign, lane_in_row, inv_sqrt_len, kPolicyPrefill,
+                                           q[j]);
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+        const uint32_t plane = j & 1, head = head0 + j / 2;
+        const size_t head_base = ((size_t)page * H + head) * S;  // in tokens
+        if (lane_in_row == 0) scale_cache[(((size_t)plane * P + page) * H + head) * S + tip] = scale[j];
+        if (plane == 0) {
+            store_key_codes<CPL>(key_cache + (head_base + tip) * (D / 2) + lane_in_row * (CPL / 2),
+                                 q[j]);
+        } else {
+            // value plane: this token's codes of 8 channels per word, into
+            // the transpose buffer (one 32-bit LDS store per word; at d = 64
+            // two lanes share a word, a 16-bit store each)
+            if constexpr (CPL >= 8) {
+#pragma unroll
+                for (int k = 0; k < CPL / 8; ++k) {
+                    uint32_t w = 0;
+#pragma unroll
+                    for (int c = 0; c < 8; ++c) w |= ((uint32_t)q[j][8 * k + c] & 0xfu) << (4 * c);
+                    lds_t[j / 2][lane_in_row * (CPL / 8) + k][row] = w;
+                }
+            } else {
+                uint32_t w = 0;
+#pragma unroll
+                for (int c = 0; c < CPL; ++c) w |= ((uint32_t)q[j][c] & 0xfu) << (4 * c);
+                ((uint16_t*)&lds_t[j / 2][lane_in_row >> 1][row])[lane_in_row & 1] = (uint16_t)w;
+            }
+        }
+    }
     __syncthreads();
-    uint32_t* strip_words = (uint32_t*)(value_cache + (head_base + (tip & ~(uint32_t)15)) * (D / 2));
-    for (int w = tid; w < D * 2; w += kWriterThreads) {
-        const int channel = w >> 1, half = w & 1;
-        const uint32_t lo4 = lds_codes[(channel * kStrip + half * 8) / 4];
-        const uint32_t hi4 = lds_codes[(channel * kStrip + half * 8) / 4 + 1];
-        strip_words[w] = pack8(lo4, hi4);
+    // ... then each value strip leaves as d*8 contiguous bytes: output word
+    // (channel, half) holds that channel's codes of tokens 8*half .. +7, one
+    // nibble from each of 8 consecutive buffer words (two 16-byte reads)
+#pragma unroll
+    for (int h = 0; h < NH; ++h) {
+        const size_t head_base = ((size_t)page * H + head0 + h) * S;
+        uint32_t* strip_words =
+            (uint32_t*)(value_cache + (head_base + (tip & ~(uint32_t)15)) * (D / 2));
+        for (int w = tid; w < D * 2; w += kWriterThreads) {
+            const int channel = w >> 1, half = w & 1;
+            const uint32_t* src = &lds_t[h][channel >> 3][8 * half];
+            const uint4 a = *(const uint4*)src;
+            const uint4 b = *(const uint4*)(src + 4);
+            const uint32_t t8[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+            const uint32_t sh = 4u * (uint32_t)(channel & 7);
+            uint32_t out = 0;
+#pragma unroll
+            for (int t = 0; t < 8; ++t) out |= ((t8[t] >> sh) & 0xfu) << (4 * t);
+            strip_words[w] = out;
+        }
     }
 }
 
@@ -327,10 +363,17 @@ static hipError_t launch_strip_writer_t(hipStream_t stream, const In* key, const
                                         const void* tables, int tables_bf16, uint32_t strips,
                                         uint32_t H, uint32_t S, uint32_t P, float inv_sqrt_len)
 {
-    const uint64_t blocks = (uint64_t)strips * H * 2u;
-    hipLaunchKernelGGL((strip_writer<D, In>), dim3((uint32_t)blocks), dim3(kWriterThreads), 0,
-                       stream, key, value, key_cache, value_cache, scale_cache, slots, pi_signs,
-                       tables, tables_bf16, H, S, P, inv_sqrt_len);
+    if (H % 2 == 0) {
+        const uint64_t blocks = (uint64_t)strips * (H / 2);
+        hipLaunchKernelGGL((strip_writer<D, In, 2>), dim3((uint32_t)blocks), dim3(kWriterThreads),
+                           0, stream, key, value, key_cache, value_cache, scale_cache, slots,
+                           pi_signs, tables, tables_bf16, H, S, P, inv_sqrt_len);
+    } else {
+        const uint64_t blocks = (uint64_t)strips * H;
+        hipLaunchKernelGGL((strip_writer<D, In, 1>), dim3((uint32_t)blocks), dim3(kWriterThreads),
+                           0, stream, key, value, key_cache, value_cache, scale_cache, slots,
+                           pi_signs, tables, tables_bf16, H, S, P, inv_sqrt_len);
+    }
     return hipGetLastError();
 }
 
