@@ -7,9 +7,9 @@
 //                    read-modify-write of the value strip
 //                    (turboquant_reshape_scatter_aiv.cpp:598-731)
 //
-// Work decomposition (MI355X): one 256-lane workgroup owns one strip of two
-// heads (one for an odd head count), both planes: four (two) panels of 16
-// rows x d channels, one row of each per 16-lane group. A row lives on 16
+// Work decomposition (MI355X): one 256-lane workgroup owns one strip of one
+// head, both planes: two panels of 16 rows x d channels, one row of each per
+// 16-lane group (two independent row jobs per lane). A row lives on 16
 // lanes with CPL = d/16 consecutive channels per lane, so the 16-point
 // Hadamard stages below CPL are in-register and the rest are lane exchanges
 // inside the row; a strip's 16 rows are the workgroup's 16 row groups.
@@ -363,17 +363,13 @@ static hipError_t launch_strip_writer_t(hipStream_t stream, const In* key, const
                                         const void* tables, int tables_bf16, uint32_t strips,
                                         uint32_t H, uint32_t S, uint32_t P, float inv_sqrt_len)
 {
-    if (H % 2 == 0) {
-        const uint64_t blocks = (uint64_t)strips * (H / 2);
-        hipLaunchKernelGGL((strip_writer<D, In, 2>), dim3((uint32_t)blocks), dim3(kWriterThreads),
-                           0, stream, key, value, key_cache, value_cache, scale_cache, slots,
-                           pi_signs, tables, tables_bf16, H, S, P, inv_sqrt_len);
-    } else {
-        const uint64_t blocks = (uint64_t)strips * H;
-        hipLaunchKernelGGL((strip_writer<D, In, 1>), dim3((uint32_t)blocks), dim3(kWriterThreads),
-                           0, stream, key, value, key_cache, value_cache, scale_cache, slots,
-                           pi_signs, tables, tables_bf16, H, S, P, inv_sqrt_len);
-    }
+    // One head per workgroup (two row jobs per lane) measured faster than
+    // two (four jobs): with one wave per SIMD nothing hides the rotation's
+    // dependent lane exchanges.
+    const uint64_t blocks = (uint64_t)strips * H;
+    hipLaunchKernelGGL((strip_writer<D, In, 1>), dim3((uint32_t)blocks), dim3(kWriterThreads), 0,
+                       stream, key, value, key_cache, value_cache, scale_cache, slots, pi_signs,
+                       tables, tables_bf16, H, S, P, inv_sqrt_len);
     return hipGetLastError();
 }
 
