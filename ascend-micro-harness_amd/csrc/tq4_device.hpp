@@ -82,12 +82,15 @@ __device__ __forceinline__ void butterfly(float (&v)[CPL], int stride, int lane_
             v[j + stride] = a - b;
         }
     } else {
+        // p - v is p + (-v) exactly (IEEE subtraction is the addition of the
+        // negation), so the upper lanes flip v's sign bit and every lane adds:
+        // one XOR and one DPP-fed add instead of an add, a subtract and a select.
         const int m = stride / CPL;
-        const bool upper = (lane_in_row & m) != 0;
+        const uint32_t flip = (lane_in_row & m) != 0 ? 0x80000000u : 0u;
 #pragma unroll
         for (int j = 0; j < CPL; ++j) {
             const float p = xor_lanes(v[j], m);
-            v[j] = upper ? p - v[j] : p + v[j];
+            v[j] = p + __uint_as_float(__float_as_uint(v[j]) ^ flip);
         }
     }
 }
