@@ -81,6 +81,7 @@ constexpr int kHdrFloats = 416;          // m_x, l_x [16][4], q_exp[16], flags, 
 constexpr uint32_t kRecMagic = 0x7FBADBADu;  // fused records hold bits ^ kRecMagic; 0 = not written
 constexpr uint32_t kPollLimit = 1u << 20;     // bound of the combiner's record polls
 constexpr uint32_t kPersistentMaxSeqs = 4096; // the persistent kernel stages two words per sequence
+constexpr int kStripSlots = TQ4_MAX_SPLIT_STRIPS + 4;  // staged window rows + padding
 
 // Eight codes of one dword as fp16 (1 + u/64), u = nibble ^ 8; halves in
 // nibble order 0,4,1,5,2,6,3,7 (every operand built against this table uses
@@ -223,16 +224,17 @@ __device__ __forceinline__ void rec_load(__amdgpu_buffer_rsrc_t r, uint32_t byte
 
 // Combine layout of one wave over one (seq, q head) row: lane c = lane & 31
 // owns channels c*CC .. c*CC+CC-1 (CC = d/32); ks = lane >> 5 takes the
-// splits of parity ks of every chunk of 16, so a chunk costs each lane eight
-// (m, l) loads and eight CC-float loads, all in flight together. Slots past
-// K load split K-1 (in range, already required) and are selected out.
+// splits of parity ks of every round of 2*NS, so a round costs each lane NS
+// (m, l) loads and NS CC-float loads, all in flight together (one memory
+// round trip per round; NS = 16 covers 32 splits at once). Slots past K
+// load split K-1 (in range, already required) and are selected out.
 //
 // LSE-combine the K partial records [m, l, 0, 0, acc[d]] at rr (stride d+4)
 // in split order, leaving acc / L in v (0 when L == 0).
 // (tests/common/l2_atomic_oracle.hpp:156-176; identity :100-108)
 // FUSED: the records are encoded; a chunk is reloaded until none of its words
 // is zero (bounded by kPollLimit), then zeroed for the next call.
-template <int D, bool FUSED>
+template <int D, bool FUSED, int NS = 8>
 __device__ void combine_records(const float* rr, uint32_t K, int lane, float (&v)[D / 32])
 {
     constexpr int CC = D / 32;
@@ -244,20 +246,20 @@ __device__ void combine_records(const float* rr, uint32_t K, int lane, float (&v
     float M = -INFINITY, L = 0.0f, a[CC];
 #pragma unroll
     for (int j = 0; j < CC; ++j) a[j] = 0.0f;
-    for (uint32_t k0 = 0; k0 < K; k0 += 16) {
-        uint32_t roff[8];
-        bool vi[8];
+    for (uint32_t k0 = 0; k0 < K; k0 += 2 * NS) {
+        uint32_t roff[NS];
+        bool vi[NS];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
+        for (int i = 0; i < NS; ++i) {
             const uint32_t k = k0 + ks + 2 * i;
             vi[i] = k < K;
             roff[i] = (vi[i] ? k : K - 1) * RS * 4u;
         }
-        uint32_t hw[8][2], aw[8][CC];
+        uint32_t hw[NS][2], aw[NS][CC];
         for (uint32_t it = 0;; ++it) {
             asm volatile("" ::: "memory");  // every poll reloads
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
+            for (int i = 0; i < NS; ++i) {
                 rec_load<2, FUSED>(rsrc, roff[i], hw[i]);
 #pragma unroll
                 for (int j = 0; j < CC; j += LD)
@@ -266,7 +268,7 @@ __device__ void combine_records(const float* rr, uint32_t K, int lane, float (&v
             if constexpr (!FUSED) break;
             uint32_t mn = 0xffffffffu;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
+            for (int i = 0; i < NS; ++i) {
                 mn = min(mn, min(hw[i][0], hw[i][1]));
 #pragma unroll
                 for (int j = 0; j < CC; ++j) mn = min(mn, aw[i][j]);
@@ -278,7 +280,7 @@ __device__ void combine_records(const float* rr, uint32_t K, int lane, float (&v
             // written" (slots past K zero split K-1 again). Issued at once:
             // the stores complete under the arithmetic below.
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
+            for (int i = 0; i < NS; ++i) {
                 __builtin_amdgcn_raw_buffer_store_b64(u2_t{0u, 0u}, rsrc, roff[i], 0,
                                                       kCachePolicySc1);
 #pragma unroll
@@ -293,9 +295,9 @@ __device__ void combine_records(const float* rr, uint32_t K, int lane, float (&v
                 }
             }
         }
-        float mk[8], Mc = -INFINITY;
+        float mk[NS], Mc = -INFINITY;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
+        for (int i = 0; i < NS; ++i) {
             mk[i] = __uint_as_float(hw[i][0] ^ x) * kLog2e;
             Mc = fmaxf(Mc, vi[i] ? mk[i] : -INFINITY);
         }
@@ -306,7 +308,7 @@ __device__ void combine_records(const float* rr, uint32_t K, int lane, float (&v
 #pragma unroll
         for (int j = 0; j < CC; ++j) a[j] *= sc;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
+        for (int i = 0; i < NS; ++i) {
             const float w = __builtin_amdgcn_exp2f(mk[i] - Mn);
             lw += vi[i] ? __uint_as_float(hw[i][1] ^ x) * w : 0.0f;
 #pragma unroll
@@ -404,8 +406,8 @@ __device__ __forceinline__ void decode_item(const DecodeParams& p, const uint32_
     int* flag = (int*)(smem + 144);
     float* u_x = smem + 148;                 // [4] per-wave 2^-sh
     float* sc_wave = smem + 160 + 64 * (threadIdx.x >> 6);  // [4][64] per-wave scale slot
-    uint32_t* strip_lds = (uint32_t*)(smem + kHdrFloats);  // [TQ4 max split strips]
-    float* region = smem + kHdrFloats + TQ4_MAX_SPLIT_STRIPS;
+    uint32_t* strip_lds = (uint32_t*)(smem + kHdrFloats);  // [TQ4 max split strips + padding]
+    float* region = smem + kHdrFloats + kStripSlots;
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
@@ -485,6 +487,9 @@ __device__ __forceinline__ void decode_item(const DecodeParams& p, const uint32_
         if (!ok && t < live_pages) bad = 1;
         const uint32_t row = (phys * p.Hkv + kvh) * S;
         for (uint32_t s = 0; s < spp; ++s) strip_lds[t * spp + s] = ok ? row + kStrip * s : kBadStrip;
+        // one padding row past the window: the second strip of a partial
+        // last pair reads it (its tokens are masked)
+        if (t == pc - 1) strip_lds[pc * spp] = ok ? row : 0u;
     }
     bad = __syncthreads_or(bad);
     // Every phase-0 load is complete here; saying so (vmcnt(0), expcnt and
@@ -537,12 +542,20 @@ __device__ __forceinline__ void decode_item(const DecodeParams& p, const uint32_
         r.sc = p.scale_cache[(size_t)half * plane_floats + rv + n];
     };
 
-    // ---- the first pairs of this wave's ring go out before the q prologue.
-    const uint32_t nfw = np_full > (uint32_t)wave ? (np_full - wave + kWaves - 1) / kWaves : 0u;
-    auto gp_of = [&](uint32_t j) { return (uint32_t)wave + kWaves * min(j, nfw - 1); };
+    // ---- this wave's pairs are gp = wave + 4j. Without an invalid page at
+    // most the window's last pair is partial (np_total - np_full <= 1); it
+    // is gp = np_full, the LAST pair of wave np_full % 4, so the ring
+    // prefetches it like the others (with clamped, "safe" indices) and only
+    // its processing is masked. The first pairs go out before the q prologue.
+    const bool tail_in_ring = !bad && np_total > np_full;
+    const uint32_t np_ring = bad ? 0u : np_total;
+    const uint32_t nw = np_ring > (uint32_t)wave ? (np_ring - wave + kWaves - 1) / kWaves : 0u;
+    const bool tail_mine = tail_in_ring && (np_full & (kWaves - 1)) == (uint32_t)wave;
+    const uint32_t nfw = tail_mine ? nw - 1 : nw;  // this wave's full pairs
+    auto gp_of = [&](uint32_t j) { return (uint32_t)wave + kWaves * min(j, nw - 1); };
     PairRegs<D> b0, b1;
     [[maybe_unused]] PairRegs<D> b2;
-    if (nfw > 0) {
+    if (nw > 0) {
         fetch(b0, gp_of(0), false);
         if constexpr (NBUF == 3) fetch(b1, gp_of(1), false);
     }
@@ -728,8 +741,22 @@ __device__ __forceinline__ void decode_item(const DecodeParams& p, const uint32_
         cr = mfma32(P, offset_col, cr);
     };
 
-    // ---- full pairs: the three-deep (two-deep at d = 256) register ring.
-    if (nfw > 0) {
+    // ---- the three-deep (two-deep at d = 256) register ring: full pairs,
+    // then this wave's masked tail pair, already in flight (its second strip
+    // may lie past the window: the staged window has one padding row).
+    auto pick = [](const PairRegs<D>& x, const PairRegs<D>& y, bool take_y) {
+        PairRegs<D> r;
+#pragma unroll
+        for (int i = 0; i < D / 32; ++i) {
+            r.k1[i] = take_y ? y.k1[i] : x.k1[i];
+            r.k2[i] = take_y ? y.k2[i] : x.k2[i];
+        }
+#pragma unroll
+        for (int i = 0; i < D / 16; ++i) r.v[i] = take_y ? y.v[i] : x.v[i];
+        r.sc = take_y ? y.sc : x.sc;
+        return r;
+    };
+    if (nw > 0) {
         if constexpr (NBUF == 3) {
             uint32_t j = 0;
             for (; j + 3 <= nfw; j += 3) {
@@ -740,8 +767,13 @@ __device__ __forceinline__ void decode_item(const DecodeParams& p, const uint32_
                 fetch(b1, gp_of(j + 4), false);
                 process(b2, gp_of(j + 2), false);
             }
+            fetch(b2, gp_of(j + 2), false);  // pair j+2 (clamped): the tail when nfw = j + 2
             if (j < nfw) process(b0, gp_of(j), false);
             if (j + 1 < nfw) process(b1, gp_of(j + 1), false);
+            if (tail_mine) {  // the tail is pair nfw, in b0, b1 or b2
+                const uint32_t r = nfw - j;
+                process(pick(pick(b0, b1, r == 1), b2, r == 2), gp_of(nfw), true);
+            }
         } else {
             uint32_t j = 0;
             for (; j + 2 <= nfw; j += 2) {
@@ -750,14 +782,14 @@ __device__ __forceinline__ void decode_item(const DecodeParams& p, const uint32_
                 fetch(b0, gp_of(j + 2), false);
                 process(b1, gp_of(j + 1), false);
             }
+            fetch(b1, gp_of(j + 1), false);  // pair j+1 (clamped): the tail when nfw = j + 1
             if (j < nfw) process(b0, gp_of(j), false);
+            if (tail_mine) process(pick(b0, b1, nfw - j == 1), gp_of(nfw), true);
         }
     }
-    // ---- the partial tail pair (and every pair of a window holding an
-    // invalid page): masked, one pair at a time.
-    if (np_total > np_full) {
-        const uint32_t first = np_full + ((uint32_t)(wave + kWaves) - (np_full & 3u)) % kWaves;
-        for (uint32_t gp = first; gp < np_total; gp += kWaves) {
+    // ---- a window holding an invalid page: every pair masked, one at a time.
+    if (bad) {
+        for (uint32_t gp = wave; gp < np_total; gp += kWaves) {
             PairRegs<D> bm;
             fetch(bm, gp, true);
             process(bm, gp, true);
@@ -880,7 +912,10 @@ __device__ __forceinline__ void decode_item(const DecodeParams& p, const uint32_
                 float gt[CC];
                 if (p.output_stage == 2) load_lane_floats<D>(p.gate + qh * D, lane, gt);
                 float v[CC];
-                combine_records<D, true>(p.records + qh * p.K * RS, k_live, lane, v);
+                if (k_live > 16)
+                    combine_records<D, true, 16>(p.records + qh * p.K * RS, k_live, lane, v);
+                else
+                    combine_records<D, true, 8>(p.records + qh * p.K * RS, k_live, lane, v);
                 egress_row<D>(v, es, gt, p.out + qh * D, p.inv_sqrt_len, p.output_stage, lane);
             }
             return;
@@ -910,11 +945,11 @@ __device__ __forceinline__ void decode_item(const DecodeParams& p, const uint32_
     }
 }
 
-// Waves per SIMD the register ring allows without spilling: three at
-// d = 64, two at d = 128 (<= 256 VGPRs), one at d = 256.
+// Waves per SIMD the register ring allows without spilling: two at d = 64
+// and d = 128 (<= 256 VGPRs), one at d = 256.
 #define TQ4_DECODE_ATTRS                                                                   \
     __launch_bounds__(kThreads)                                                            \
-    __attribute__((amdgpu_waves_per_eu(D == 64 ? 3 : (D == 128 ? 2 : 1), D == 64 ? 3 : 2)))
+    __attribute__((amdgpu_waves_per_eu(D == 256 ? 1 : 2, 2)))
 
 // One workgroup per (seq, kv head, split), splits fastest.
 template <int D, int MODE>
@@ -945,7 +980,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D == 2
 void decode_persistent_kernel(DecodeParams p)
 {
     extern __shared__ float smem[];
-    uint32_t* full = (uint32_t*)(smem + kHdrFloats + TQ4_MAX_SPLIT_STRIPS + region_floats(p.G, D));
+    uint32_t* full = (uint32_t*)(smem + kHdrFloats + kStripSlots + region_floats(p.G, D));
     uint32_t* splits = full + p.B;  // max(1, live splits) per sequence
     uint32_t* next_lds = (uint32_t*)(smem + 145);
     const int tid = threadIdx.x, lane = tid & 63;
@@ -1069,7 +1104,7 @@ template <int D>
 hipError_t launch_decode_t(hipStream_t stream, const DecodeParams& p, int mode)
 {
     const size_t blocks = (size_t)p.B * p.Hkv * p.K;
-    const size_t lds = (kHdrFloats + TQ4_MAX_SPLIT_STRIPS + region_floats(p.G, D)) * sizeof(float);
+    const size_t lds = (kHdrFloats + kStripSlots + region_floats(p.G, D)) * sizeof(float);
     if (mode == 0) {
         hipLaunchKernelGGL((decode_kernel<D, 0>), dim3((uint32_t)blocks), dim3(kThreads), lds,
                            stream, p);
