@@ -18,6 +18,8 @@
 //   kernels/ops/turboquant/turboquant_decode_tail.hpp  turboquant_decode_tail
 //   tests/cpu/icdf_fixture.hpp                    icdf (ICDF leaf fixture + oracle)
 //   tests/common/lloydmax_oracle.hpp              lloyd (Lloyd-Max / Gaussian-CDF)
+//   tests/common/fused_decode_opt_fixture.hpp     fused_decode_opt_test (KV4/FP8
+//                                                 NZ cache fixture, FP64 expected)
 
 #include "tests/common/turboquant_oracle.hpp"
 #include "tests/common/turboquant_scatter_oracle.hpp"
@@ -28,6 +30,7 @@
 #include "kernels/ops/turboquant/turboquant_decode_tail.hpp"
 #include "tests/cpu/icdf_fixture.hpp"
 #include "tests/common/lloydmax_oracle.hpp"
+#include "tests/common/fused_decode_opt_fixture.hpp"
 
 #include <cstdint>
 #include <cstring>
@@ -401,4 +404,88 @@ void ref_lloyd_pack(const unsigned* q, unsigned n, unsigned bits, uint8_t* out)
     std::memcpy(out, p.data(), p.size());
 }
 
+// ------------------------------------------------- fused_decode_opt_test (KV4/FP8)
+// sizes[0..5]: query floats, cache bytes (key = value), scale floats, table
+// ints, length ints, physical pages.
+int ref_fdo_dims(int n, int b, int h, int g, int block, long long* sizes)
+{
+    try {
+        const fused_decode_opt_test::Fixture f(n, b, h, g, block);
+        sizes[0] = (long long)f.query.size();
+        sizes[1] = (long long)f.key.size();
+        sizes[2] = (long long)f.scales.size();
+        sizes[3] = (long long)f.table.size();
+        sizes[4] = (long long)f.lengths.size();
+        sizes[5] = f.physical_pages;
+        return f.pages;
+    } catch (const std::exception&) {
+        return -1;
+    }
+}
+
+int ref_fdo_fixture(int n, int b, int h, int g, int block, int element, float* query, uint8_t* key,
+                    uint8_t* value, float* scales, int32_t* table, int32_t* lengths,
+                    float* expected, uint16_t* expected_bits)
+{
+    try {
+        const auto e = element ? fused_decode_opt_test::Element::kBf16
+                               : fused_decode_opt_test::Element::kFp16;
+        const fused_decode_opt_test::Fixture f(n, b, h, g, block, e);
+        std::memcpy(query, f.query.data(), f.query.size() * 4);
+        std::memcpy(key, f.key.data(), f.key.size());
+        std::memcpy(value, f.value.data(), f.value.size());
+        std::memcpy(scales, f.scales.data(), f.scales.size() * 4);
+        std::memcpy(table, f.table.data(), f.table.size() * 4);
+        std::memcpy(lengths, f.lengths.data(), f.lengths.size() * 4);
+        std::memcpy(expected, f.expected.data(), f.expected.size() * 4);
+        for (std::size_t i = 0; i < f.expected.size(); ++i)
+            expected_bits[i] = fused_decode_opt_test::reference_bits(e, f.expected[i]);
+        return 0;
+    } catch (const std::exception&) {
+        return -1;
+    }
+}
+
+// The raw-query entry's inputs for one fixture: the original-basis query and
+// the gate logits (element bits), the sign vector, and the expected rows of
+// output stage `stage` (float).
+int ref_fdo_raw(int n, int b, int h, int g, int block, int element, unsigned stage,
+                uint16_t* raw_query, uint16_t* gate_bits, float* pi_signs, float* expected)
+{
+    try {
+        const auto e = element ? fused_decode_opt_test::Element::kBf16
+                               : fused_decode_opt_test::Element::kFp16;
+        const fused_decode_opt_test::Fixture f(n, b, h, g, block, e);
+        const fused_decode_opt_test::RawQueryBasis basis;
+        const auto raw = f.raw_query(basis);
+        std::memcpy(raw_query, raw.data(), raw.size() * 2);
+        const auto gl = f.gate_logits();
+        std::memcpy(gate_bits, gl.data(), gl.size() * 2);
+        std::memcpy(pi_signs, basis.signs.data(), basis.signs.size() * 4);
+        const std::size_t rows = f.query.size() / 256;
+        for (std::size_t r = 0; r < rows; ++r) {
+            const auto row = f.expected_row(basis, r, stage);
+            std::memcpy(expected + r * 256, row.data(), 256 * 4);
+        }
+        return 0;
+    } catch (const std::exception&) {
+        return -1;
+    }
+}
+
+float ref_fdo_gain()
+{
+    return vllm_ascend::turboquant::TurboQuantModeTraits<
+        vllm_ascend::turboquant::TurboQuantMode::KV4_FP8>::kGain;
+}
+
+unsigned long long ref_nz_byte(unsigned long long slot, unsigned long long kv_head,
+                               unsigned long long column, unsigned long long kv_heads,
+                               unsigned long long packed_bytes)
+{
+    return vllm_ascend::turboquant::NzTiledPackedByte(slot, kv_head, column, kv_heads,
+                                                       packed_bytes);
+}
+
 }  // extern "C"
+

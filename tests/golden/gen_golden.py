@@ -25,6 +25,10 @@ provenance. Reference functions used (paths relative to the reference checkout):
          lloyd::fixture, lloyd::code, lloyd::centroid, lloyd::pack, thresholds
                                                 tests/common/lloydmax_oracle.hpp,
                                                 include/routines/routine_vector_lloydmax_quantize.hpp
+  fd_*   fused_decode_opt_test::Fixture (KV4/FP8 NZ cache, inputs and FP64
+         expected rows in both element formats), RawQueryBasis, raw_query,
+         gate_logits, expected_row (output stages 1, 2)
+                                                tests/common/fused_decode_opt_fixture.hpp
   tail_* turboquant_splitk::Partition, turboquant_decode_tail::ActiveInStrip,
          LiveStripsInWindow                     include/turboquant_splitk_contract.hpp,
                                                 kernels/ops/turboquant/turboquant_decode_tail.hpp
@@ -268,6 +272,50 @@ def main():
                                         for i in range((1 << bits) - 1)], np.float32)
         files[f"cb_lloyd_b{bits}"] = save(f"cb_lloyd_b{bits}", **cb)
 
+    # ---- FD: the KV4/FP8 fused decode fixture (the reference's NPU ladder rungs)
+    for (n, b, h, g, block) in [(79, 1, 1, 16, 64), (257, 1, 1, 16, 64), (1055, 1, 4, 16, 64),
+                                (512, 1, 4, 16, 64), (192, 2, 2, 3, 64), (128, 1, 1, 1, 128)]:
+        sz = np.zeros(6, np.int64)
+        pages = r.lib.ref_fdo_dims(n, b, h, g, block, ptr(sz))
+        assert pages > 0
+        fd = {"geometry": np.array([n, b, h, g, block, pages, sz[5]], np.int32)}
+        for el, tag in ((0, "fp16"), (1, "bf16")):
+            q = np.zeros(sz[0], np.float32)
+            kk = np.zeros(sz[1], np.uint8)
+            vv = np.zeros(sz[1], np.uint8)
+            sc = np.zeros(sz[2], np.float32)
+            tb = np.zeros(sz[3], np.int32)
+            ln = np.zeros(sz[4], np.int32)
+            ex = np.zeros(sz[0], np.float32)
+            eb = np.zeros(sz[0], np.uint16)
+            assert r.lib.ref_fdo_fixture(n, b, h, g, block, el, *[ptr(x) for x in
+                                         (q, kk, vv, sc, tb, ln, ex, eb)]) == 0
+            if el == 0:
+                fd.update(query=q, key=kk, value=vv, scales=sc, block_table=tb,
+                          context_lens=ln[:b], expected=ex)
+            else:  # the element changes no input and no FP32 expected value
+                assert np.array_equal(q, fd["query"]) and np.array_equal(ex, fd["expected"])
+            fd[f"expected_bits_{tag}"] = eb
+            raw = np.zeros(sz[0], np.uint16)
+            gate = np.zeros(sz[0], np.uint16)
+            signs = np.zeros(256, np.float32)
+            for stage in (1, 2):
+                er = np.zeros(sz[0], np.float32)
+                assert r.lib.ref_fdo_raw(n, b, h, g, block, el, stage, ptr(raw), ptr(gate),
+                                         ptr(signs), ptr(er)) == 0
+                fd[f"expected_stage{stage}"] = er  # identical for both elements
+            fd[f"raw_query_{tag}"] = raw
+            fd[f"gate_{tag}"] = gate
+            fd["pi_signs"] = signs
+        fd["gain"] = np.array([r.lib.ref_fdo_gain()], np.float32)
+        name = f"fd_n{n}_b{b}_h{h}_g{g}_p{block}"
+        files[name] = save(name, **fd)
+    nz = np.array([[s_, k_, c_, hh] for hh in (1, 3, 4) for s_ in (0, 1, 63, 64, 65, 127, 200)
+                   for k_ in range(hh) for c_ in (0, 1, 31, 32, 63, 64, 127)], np.uint64)
+    nz_bytes = np.array([r.lib.ref_nz_byte(int(a), int(b_), int(c), int(hh), 128)
+                         for a, b_, c, hh in nz], np.uint64)
+    files["fd_nz_layout"] = save("fd_nz_layout", args=nz, byte=nz_bytes)
+
     manifest = {}
     for name, path in files.items():
         data = open(path, "rb").read()
@@ -276,7 +324,8 @@ def main():
     manifest["_provenance"] = (
         "generated by tests/golden/gen_golden.py from the reference's header-only CPU oracles "
         "compiled in place into oracle/_ref (tests/common/*.hpp, include/turboquant_splitk_contract.hpp, "
-        "kernels/ops/turboquant/turboquant_decode_tail.hpp)")
+        "kernels/ops/turboquant/turboquant_decode_tail.hpp, "
+        "kernels/ops/turboquant/vllm_integration_layer/op_kernel/common/turboquant_layout.h)")
     with open(os.path.join(HERE, "manifest.json"), "w") as f:
         json.dump(manifest, f, indent=1, sort_keys=True)
     for name, meta in sorted(manifest.items()):

@@ -54,6 +54,13 @@ def bf16_to_f32(b):
     return (np.asarray(b, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
 
 
+class Kv4Geom(C.Structure):
+    """tq4o_kv4fp8_geom (oracle/kv4fp8_oracle.h)."""
+    _fields_ = [(n, U32) for n in ("tokens", "heads", "kv_heads", "head_size", "block_size",
+                                   "max_blocks", "num_blocks", "splits", "fused_context_limit")] + \
+        [("scale", F32), ("inv_sqrt_len", F32), ("output_stage", U32), ("element_type", U32)]
+
+
 class Oracle:
     def __init__(self, path=ORACLE_SO):
         if not os.path.exists(path):
@@ -117,6 +124,59 @@ class Oracle:
         L.tq4o_icdf_code.argtypes = [C.c_double]
         L.tq4o_icdf_quantize.restype = I32
         L.tq4o_icdf_quantize.argtypes = [I32, P, U64, P]
+        L.tq4o_nz_byte.restype = U64
+        L.tq4o_nz_byte.argtypes = [U64] * 5
+        L.tq4o_fp8_e4m3_encode.restype = C.c_uint8
+        L.tq4o_fp8_e4m3_encode.argtypes = [F32]
+        L.tq4o_fp8_e4m3_decode.restype = F32
+        L.tq4o_fp8_e4m3_decode.argtypes = [C.c_uint8]
+        L.tq4o_f32_to_f16.restype = C.c_uint16
+        L.tq4o_f32_to_f16.argtypes = [F32]
+        L.tq4o_elem_to_f32.restype = F32
+        L.tq4o_elem_to_f32.argtypes = [U32, C.c_uint16]
+        L.tq4o_f32_to_elem.restype = C.c_uint16
+        L.tq4o_f32_to_elem.argtypes = [U32, F32]
+        L.tq4o_kv4fp8_apply_pi.argtypes = [P, P, F32, U32]
+        L.tq4o_kv4fp8_rotate_query.argtypes = [U32, P, P, F32, U64, U32, P]
+        L.tq4o_kv4fp8_partial_floats.restype = U32
+        L.tq4o_kv4fp8_partial_floats.argtypes = [U32]
+        L.tq4o_kv4fp8_decode.restype = I32
+        L.tq4o_kv4fp8_decode.argtypes = [P] * 12 + [I32]
+
+    # ------------------------------------------------------------ KV4/FP8
+    def kv4fp8_decode(self, query, key, value, scales, table, lengths, *, heads, kv_heads,
+                      block_size, max_blocks, num_blocks, splits=1, fused_context_limit=0,
+                      scale=0.0625, inv_sqrt_len=0.0625, output_stage=0, element_type=0,
+                      pi_signs=None, gate=None, want_partials=False, threads=8):
+        """Output element bits [tokens, heads, 256], the FP32 rows before the
+        cast, and (want_partials) the split partials [tokens, heads, splits, 272]."""
+        tokens = int(np.asarray(lengths).size)
+        g = Kv4Geom(tokens, heads, kv_heads, 256, block_size, max_blocks, num_blocks, splits,
+                    fused_context_limit, scale, inv_sqrt_len, output_stage, element_type)
+        out = np.zeros((tokens, heads, 256), np.uint16)
+        out_f32 = np.zeros((tokens, heads, 256), np.float32)
+        ws = np.zeros((tokens, heads, splits, 272), np.float32) if want_partials else None
+        a = [np.ascontiguousarray(x) if x is not None else None
+             for x in (query, key, value, scales, table, lengths, pi_signs, gate)]
+        st = self.lib.tq4o_kv4fp8_decode(C.byref(g), *[ptr(x) for x in a], ptr(ws), ptr(out),
+                                         ptr(out_f32), threads)
+        if st != 0:
+            raise ValueError(f"tq4o_kv4fp8_decode refused: {st}")
+        return (out, out_f32, ws) if want_partials else (out, out_f32)
+
+    def kv4fp8_rotate_query(self, raw_bits, signs, inv_sqrt_len, element_type):
+        raw = np.ascontiguousarray(raw_bits, np.uint16)
+        out = np.zeros(raw.shape, np.float32)
+        n = raw.shape[-1]
+        self.lib.tq4o_kv4fp8_rotate_query(element_type, ptr(raw),
+                                          ptr(np.ascontiguousarray(signs, np.float32)),
+                                          inv_sqrt_len, raw.size // n, n, ptr(out))
+        return out
+
+    def fp8_round(self, x):
+        x = np.asarray(x, np.float32).reshape(-1)
+        return np.array([self.lib.tq4o_fp8_e4m3_decode(self.lib.tq4o_fp8_e4m3_encode(float(v)))
+                         for v in x], np.float32)
 
     # ------------------------------------------------------------ codebooks
     def codebook_quantize(self, book, bits, x):
@@ -310,3 +370,12 @@ class Ref:
         L.ref_lloyd_threshold.restype = F32
         L.ref_lloyd_threshold.argtypes = [U32, U32]
         L.ref_lloyd_pack.argtypes = [P, U32, U32, P]
+        L.ref_fdo_dims.restype = I32
+        L.ref_fdo_dims.argtypes = [I32] * 5 + [P]
+        L.ref_fdo_fixture.restype = I32
+        L.ref_fdo_fixture.argtypes = [I32] * 6 + [P] * 8
+        L.ref_fdo_raw.restype = I32
+        L.ref_fdo_raw.argtypes = [I32] * 6 + [U32, P, P, P, P]
+        L.ref_fdo_gain.restype = F32
+        L.ref_nz_byte.restype = C.c_ulonglong
+        L.ref_nz_byte.argtypes = [C.c_ulonglong] * 5
