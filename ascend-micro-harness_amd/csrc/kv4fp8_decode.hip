@@ -1,0 +1,581 @@
+// kv4fp8_decode.hip -- decode over the KV4/FP8 64-token NZ-tiled cache
+// (include/tq4_kv4fp8.h) for gfx950.
+//
+// Reference: the "fused decode opt" operator,
+// kernels/ops/turboquant/vllm_integration_layer/op_kernel/ (opk/ below):
+// turboquant_fused_decode.cpp:479-568 (tasks), vector/turboquant_vector_service.h
+// (query operand 1033-1058, tile softmax 594-679, partials 1181-1201, split
+// reduce 253-320, normalise/cast 144-185), vector/routine_vector_cube_softmax.hpp
+// (the batched tile recurrence), common/turboquant_codec_mx.h:289-359 (levels,
+// FP8 operand cast), cube/turboquant_query_basis.h:181-208 (output stages).
+//
+// Work split. One workgroup = (token, kv head, 16-head chunk, part); part
+// covers 4*nt consecutive 64-row tiles, wave w the w-th nt of them. Each wave
+// runs the reference's tile recurrence over its tiles; the four waves merge
+// in LDS and the workgroup leaves one partial record (m, l, acc) per q head;
+// kv4_reduce_kernel merges a row's records and runs the egress. Tiles are the
+// reference's tiles (64 aligned rows of the sequence), so the per-tile FP8
+// operands are the same; only the summation order of the merges differs.
+//
+// Operands on the f16 MFMA (16x16x32). Every FP8 e4m3 value and every level
+// n + 0.5 is exact in f16, and their products are exact in FP32, so the f16
+// MFMA computes the reference's FP8 products exactly:
+//   scores  S[token][head] = K[token][k] . Q8[k][head]: A = key row (lane =
+//           token, its 32-byte chunk of column group g), B = the query operand
+//           in the same k order (lane = head);
+//   context ctx^T[channel][head] = V^T[channel][k] . P8[k][head]: A = value
+//           (lane = channel, 8 rows paired by v_perm), B = the lane's own
+//           probabilities -- the k order is chosen as the score layout's row
+//           order, so P needs no transpose.
+// A level is fed as w = 1 + (n ^ 8)/64 (one v_bitop3 per pair, as the TQ4
+// decode does), i.e. n + 0.5 = 64 (w - 1.1171875): scores start from
+// -1.1171875 * sum(Q8) and are scaled by 64 with the key scale; the context's
+// offset is tracked per head (B below) and removed at the end.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "tq4_internal.hpp"
+
+namespace tq4 {
+namespace {
+
+typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+typedef float f4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kWaves = 4;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kTile = 64;
+constexpr int kD = 256;
+constexpr uint32_t kNib = 0x00F000F0u;       // a level at f16 mantissa bits [7:4], both halves
+constexpr uint32_t kCodeBase = 0x3C803C80u;  // f16 1.0 outside kNib; the nibble sign bit inside
+constexpr float kLevelOffset = 1.1171875f;   // w = 1.1171875 + (n + 0.5) / 64
+constexpr float kLevelUnit = 64.0f;
+constexpr float kOperandMax = 448.0f;        // OperandMax<KV4_FP8> (e4m3)
+constexpr float kEps = 1e-20f;               // TurboQuantCodec4::kEps
+constexpr float kNegInf = -3.4028235e38f;    // kVectorNegInf
+constexpr float kMaskGain = -5.0e36f;
+constexpr float kMaskMid = 0.5f;
+constexpr float kGateFloor = -80.0f;
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr uint32_t kRecFloats = 260;         // acc[256], m, l, pad, pad
+constexpr int kMergeFloats = kWaves * 16 * kD;
+constexpr int kScaleFloats = kWaves * 2 * kTile;
+
+// Eight levels of one dword as f16 pairs, halves in nibble order 0,4,1,5,2,6,3,7:
+// each pair is kNib ? (bits ^ kCodeBase) : kCodeBase (v_bitop3 0x6A).
+__device__ __forceinline__ u4_t codes8(uint32_t w)
+{
+    return u4_t{(uint32_t)__builtin_amdgcn_bitop3_b32(w << 4, kNib, kCodeBase, 0x6A),
+                (uint32_t)__builtin_amdgcn_bitop3_b32(w, kNib, kCodeBase, 0x6A),
+                (uint32_t)__builtin_amdgcn_bitop3_b32(w >> 4, kNib, kCodeBase, 0x6A),
+                (uint32_t)__builtin_amdgcn_bitop3_b32(w >> 8, kNib, kCodeBase, 0x6A)};
+}
+
+__device__ __forceinline__ f4_t mfma(u4_t a, h8_t b, f4_t c)
+{
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8_t, a), b, c, 0, 0, 0);
+}
+
+// Reductions over the four lanes l, l^16, l^32, l^48 (one head's lane column).
+__device__ __forceinline__ float col_max(float v)
+{
+    const uint32_t u = __float_as_uint(v);
+    const auto a = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const uint32_t w = __float_as_uint(v);
+    const auto b = __builtin_amdgcn_permlane16_swap(w, w, false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
+__device__ __forceinline__ float col_sum(float v)
+{
+    const uint32_t u = __float_as_uint(v);
+    const auto a = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const uint32_t w = __float_as_uint(v);
+    const auto b = __builtin_amdgcn_permlane16_swap(w, w, false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+__device__ __forceinline__ float fexp(float x) { return __builtin_amdgcn_exp2f(x * kLog2e); }
+
+// Two FP32 values on the FP8 e4m3 grid (v_cvt_pk_fp8_f32: OCP e4m3, round to
+// nearest even, subnormals kept), back to FP32 (v_cvt_pk_f32_fp8) and packed
+// as f16 (exact: every e4m3 value is an f16 value, so the truncating pack
+// does not round).
+__device__ __forceinline__ h2_t fp8_pair(float a, float b)
+{
+    const uint32_t w = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+    const auto f = __builtin_amdgcn_cvt_pk_f32_fp8(w, false);
+    return __builtin_bit_cast(h2_t, __builtin_amdgcn_cvt_pkrtz(f[0], f[1]));
+}
+
+__device__ __forceinline__ float elem_to_f32(uint16_t bits, uint32_t element)
+{
+    if (element) return __uint_as_float((uint32_t)bits << 16);
+    return (float)__builtin_bit_cast(_Float16, bits);
+}
+
+__device__ __forceinline__ uint16_t f32_to_elem(float x, uint32_t element)
+{
+    if (element) {
+        const uint32_t u = __float_as_uint(x);
+        if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x7fffffu)) return (uint16_t)((u >> 16) | 0x40u);
+        return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+    }
+    return __builtin_bit_cast(uint16_t, (_Float16)x);  // v_cvt_f16_f32: round to nearest even
+}
+
+// One stride of the Walsh-Hadamard butterfly across lanes (lane bit `m`):
+// the lower lane keeps a + b, the upper b' = a - b (a = lower, b = upper).
+__device__ __forceinline__ float wht_lanes(float v, int m, int lane)
+{
+    const float o = __shfl_xor(v, m, 64);
+    return (lane & m) ? o - v : v + o;
+}
+
+// ApplyPi over one 256-channel row held four consecutive channels per lane.
+__device__ __forceinline__ void apply_pi(float (&x)[4], const float (&s)[4], float inv_sqrt_len,
+                                         int lane)
+{
+#pragma unroll
+    for (int j = 0; j < 4; ++j) x[j] = x[j] * s[j];
+    {
+        const float a0 = x[0] + x[1], a1 = x[0] - x[1], a2 = x[2] + x[3], a3 = x[2] - x[3];
+        x[0] = a0 + a2;
+        x[1] = a1 + a3;
+        x[2] = a0 - a2;
+        x[3] = a1 - a3;
+    }
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) x[j] = wht_lanes(x[j], m, lane);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) x[j] = x[j] * inv_sqrt_len;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) x[j] = x[j] * s[j];
+}
+
+// One tile's operands in registers.
+struct Tile {
+    u4_t k[8];        // key: token block tb's 32-byte chunk of column group g (k[2tb], k[2tb+1])
+    uint2 v[16];      // value: rows 16tb + 4g + i (v[4tb + i]), packed columns 8m..8m+7
+    float ks, vs;     // scales of row `lane`
+    int ok;
+};
+
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void kv4_decode_kernel(Kv4Params p)
+{
+    extern __shared__ __align__(16) float lds[];
+    float* merge = lds;                                  // [4][16][256] (q rows first)
+    float* q_lds = lds;                                  // [16][256]
+    float* ml = lds + kMergeFloats;                      // [4][16][2]
+    float* sc_all = ml + kWaves * 32;                    // [4][2][64]
+    int32_t* win = (int32_t*)(sc_all + kScaleFloats);    // the part's block-table window
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int n16 = lane & 15, g = lane >> 4;
+    const uint32_t part = blockIdx.x;
+    const uint32_t kvh = blockIdx.y / p.chunks, chunk = blockIdx.y % p.chunks;
+    const uint32_t token = blockIdx.z;
+    const uint32_t S = 1u << p.block_shift;
+
+    int32_t ctx_raw = p.context_lens[token];
+    uint32_t ctx = ctx_raw > 0 ? (uint32_t)ctx_raw : 0u;
+    const uint64_t cap = (uint64_t)p.max_blocks << p.block_shift;
+    if (ctx > cap) ctx = (uint32_t)cap;
+    const uint32_t tiles = (ctx + kTile - 1) / kTile;
+    const uint32_t t0 = part * kWaves * p.nt;
+    const bool live = t0 < tiles;
+    // no live tile: no record (the reduce counts parts from ctx); part 0 of a
+    // raw-query launch still writes the rotated query back
+    if (!live && !(part == 0 && p.query_out != nullptr)) return;
+    const uint32_t t1 = live ? min(t0 + kWaves * p.nt, tiles) : t0;
+    const uint32_t head0 = chunk * 16;
+    const uint32_t gc = min(16u, p.G - head0);  // live heads of this chunk
+
+    // ---- phase 0: the block-table window and the chunk's query rows.
+    const uint32_t page0 = (t0 * kTile) >> p.block_shift;
+    const uint32_t npages = live ? (((t1 * kTile - 1) >> p.block_shift) - page0) + 1 : 0u;
+    for (uint32_t i = tid; i < npages; i += kThreads)
+        win[i] = p.block_table[(size_t)token * p.max_blocks + page0 + i];
+    for (uint32_t h = wave; h < 16; h += kWaves) {
+        float x[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        const size_t row = (size_t)token * p.Hq + p.G * kvh + head0 + h;
+        if (h < gc) {
+            if (p.raw_query) {
+                const uint2 w = *(const uint2*)(p.raw_query + row * kD + 4 * lane);
+                x[0] = elem_to_f32((uint16_t)w.x, p.element);
+                x[1] = elem_to_f32((uint16_t)(w.x >> 16), p.element);
+                x[2] = elem_to_f32((uint16_t)w.y, p.element);
+                x[3] = elem_to_f32((uint16_t)(w.y >> 16), p.element);
+                const float4 sg = *(const float4*)(p.pi_signs + 4 * lane);
+                const float s[4] = {sg.x, sg.y, sg.z, sg.w};
+                apply_pi(x, s, p.inv_sqrt_len, lane);
+                if (p.query_out && part == 0)
+                    *(float4*)(p.query_out + row * kD + 4 * lane) = make_float4(x[0], x[1], x[2], x[3]);
+            } else {
+                const float4 v = *(const float4*)(p.query + row * kD + 4 * lane);
+                x[0] = v.x;
+                x[1] = v.y;
+                x[2] = v.z;
+                x[3] = v.w;
+            }
+        }
+        *(float4*)(q_lds + h * kD + 4 * lane) = make_float4(x[0], x[1], x[2], x[3]);
+    }
+    __syncthreads();
+    if (!live) return;
+
+    // ---- the query operand of head n16 for k group g: k-step ks covers the
+    // dword d = 8g + ks of a key row, channels 4d + {0, 2, 128, 130, 1, 3, 129, 131}.
+    float qv[8][8];
+    float amax = 0.0f;
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) {
+        const int c0 = 4 * (8 * g + ks);
+        const float* qr = q_lds + n16 * kD;
+        const float4 lo = *(const float4*)(qr + c0);
+        const float4 hi = *(const float4*)(qr + 128 + c0);
+        qv[ks][0] = lo.x; qv[ks][1] = lo.z; qv[ks][2] = hi.x; qv[ks][3] = hi.z;
+        qv[ks][4] = lo.y; qv[ks][5] = lo.w; qv[ks][6] = hi.y; qv[ks][7] = hi.w;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(qv[ks][j]));
+    }
+    amax = col_max(amax);
+    amax = amax + kEps;
+    const float q_scale = kOperandMax / amax;
+    const float q_inv = 1.0f / q_scale;
+    h8_t qop[8];
+    float q1 = 0.0f;
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) {
+#pragma unroll
+        for (int j = 0; j < 8; j += 2) {
+            const h2_t h = fp8_pair(qv[ks][j] * q_scale, qv[ks][j + 1] * q_scale);
+            qop[ks][j] = h[0];
+            qop[ks][j + 1] = h[1];
+            q1 += (float)h[0] + (float)h[1];
+        }
+    }
+    q1 = col_sum(q1);
+    const float sbias = -kLevelOffset * q1;
+
+    // ---- this wave's tiles
+    const uint32_t w0 = min(t0 + wave * p.nt, t1), w1 = min(w0 + p.nt, t1);
+    float* sc = sc_all + wave * 2 * kTile;
+    const uint32_t H = p.H;
+    const uint32_t m8 = 8 * n16;  // this lane's packed value columns 8m..8m+7
+
+    auto fetch = [&](Tile& r, uint32_t t) {
+        const uint32_t row_abs = t * kTile;
+        const int32_t e = win[(row_abs >> p.block_shift) - page0];
+        r.ok = e >= 0 && (uint32_t)e < p.num_blocks;
+        if (!r.ok) return;
+        const uint32_t rip = row_abs & (S - 1);
+        const size_t base = ((size_t)(uint32_t)e * S + rip) * H * 128 + (size_t)kvh * (kTile * 128);
+        const int8_t* kb = (const int8_t*)p.key + base;
+        const int8_t* vb = (const int8_t*)p.value + base;
+#pragma unroll
+        for (int tb = 0; tb < 4; ++tb) {
+            const u4_t* src = (const u4_t*)(kb + (g * kTile + 16 * tb + n16) * 32);
+            r.k[2 * tb] = src[0];
+            r.k[2 * tb + 1] = src[1];
+        }
+        const int8_t* vcol = vb + ((m8 >> 5) * kTile) * 32 + (m8 & 31);
+#pragma unroll
+        for (int tb = 0; tb < 4; ++tb)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) r.v[4 * tb + i] = *(const uint2*)(vcol + (16 * tb + 4 * g + i) * 32);
+        const float* srow = p.scales + ((size_t)(uint32_t)e * S + rip + lane) * 8;
+        r.ks = srow[kvh];
+        r.vs = srow[H + kvh];
+    };
+
+    float run_max = kNegInf, run_sum = 0.0f, bsum = 0.0f, inv_prev = 1.0f;
+    f4_t acc[16];
+#pragma unroll
+    for (int b = 0; b < 16; ++b) acc[b] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+    auto process = [&](const Tile& r, uint32_t t) {
+        if (!r.ok) return;
+        const uint32_t valid = min((uint32_t)kTile, ctx - t * kTile);
+        // scales through the wave's LDS slot: row `lane` in, rows 16tb + 4g .. out
+        sc[lane] = (r.ks * p.score_scale) * kLevelUnit;
+        sc[kTile + lane] = r.vs * p.inv_gain;
+        // scores
+        f4_t s4[4];
+#pragma unroll
+        for (int tb = 0; tb < 4; ++tb) {
+            f4_t c = f4_t{sbias, sbias, sbias, sbias};
+#pragma unroll
+            for (int ks = 0; ks < 8; ++ks) {
+                const uint32_t w = ks < 4 ? r.k[2 * tb][ks] : r.k[2 * tb + 1][ks - 4];
+                c = mfma(codes8(w), qop[ks], c);
+            }
+            s4[tb] = c;
+        }
+        float s[16], vsc[16];
+#pragma unroll
+        for (int tb = 0; tb < 4; ++tb) {
+            const f4_t k4 = *(const f4_t*)(sc + 16 * tb + 4 * g);
+            const f4_t v4 = *(const f4_t*)(sc + kTile + 16 * tb + 4 * g);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                float x = s4[tb][i] * k4[i];
+                x = x * q_inv;
+                s[4 * tb + i] = x;
+                vsc[4 * tb + i] = v4[i];
+            }
+        }
+        if (valid < (uint32_t)kTile) {
+            const float mid = kMaskMid - (float)valid;
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                const uint32_t row = 16 * (j >> 2) + 4 * g + (j & 3);
+                float mask = (float)row + mid;
+                mask = mask * kMaskGain;
+                s[j] = row < valid ? fminf(s[j], mask) : mask;
+                vsc[j] = row < valid ? vsc[j] : 0.0f;
+            }
+        }
+        float tmax = s[0];
+#pragma unroll
+        for (int j = 1; j < 16; ++j) tmax = fmaxf(tmax, s[j]);
+        tmax = col_max(tmax);
+        const float new_max = fmaxf(run_max, tmax);
+        const float alpha = fexp(run_max - new_max);
+        float part_sum = 0.0f, pmax = 0.0f;
+        float pv[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const float e = fexp(s[j] - new_max);
+            part_sum += e;
+            pv[j] = e * vsc[j];
+            pmax = fmaxf(pmax, pv[j]);
+        }
+        part_sum = col_sum(part_sum);
+        run_sum = run_sum * alpha;
+        run_sum = run_sum + part_sum;
+        pmax = col_max(pmax);
+        pmax = pmax + kEps;
+        const float prob_scale = kOperandMax / pmax;
+        h8_t pop[2];
+        float p1 = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 16; j += 2) {
+            const h2_t h = fp8_pair(pv[j] * prob_scale, pv[j + 1] * prob_scale);
+            pop[j >> 3][j & 7] = h[0];
+            pop[j >> 3][(j & 7) + 1] = h[1];
+            p1 += (float)h[0] + (float)h[1];
+        }
+        p1 = col_sum(p1);
+        // acc holds acc_ref * prob_scale (this tile's units): rescale, then add P8 . V
+        const float rho = alpha * (prob_scale * inv_prev);
+        bsum = bsum * rho;
+        bsum = bsum + p1;
+#pragma unroll
+        for (int b = 0; b < 16; ++b) acc[b] = acc[b] * rho;
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            // row pairs (tb, i01), (tb, i23), (tb+1, i01), (tb+1, i23) of k-step ks
+            u4_t cv[4][4];
+#pragma unroll
+            for (int rp = 0; rp < 4; ++rp) {
+                const uint2 ra = r.v[4 * (2 * ks + (rp >> 1)) + 2 * (rp & 1)];
+                const uint2 rb = r.v[4 * (2 * ks + (rp >> 1)) + 2 * (rp & 1) + 1];
+                cv[rp][0] = codes8(__builtin_amdgcn_perm(rb.x, ra.x, 0x05040100u));
+                cv[rp][1] = codes8(__builtin_amdgcn_perm(rb.x, ra.x, 0x07060302u));
+                cv[rp][2] = codes8(__builtin_amdgcn_perm(rb.y, ra.y, 0x05040100u));
+                cv[rp][3] = codes8(__builtin_amdgcn_perm(rb.y, ra.y, 0x07060302u));
+            }
+            // block b: channel 8m + b (b < 8, low nibble of column b) or
+            // 128 + 8m + b - 8 (high nibble); codes8 of columns (2q, 2q+1)
+            // gives pairs for blocks 2q, 8 + 2q, 2q + 1, 9 + 2q.
+#pragma unroll
+            for (int b = 0; b < 16; ++b) {
+                const int col = b & 7, q = col >> 1;
+                const int e = (col & 1) * 2 + (b >> 3);
+                const u4_t a = u4_t{cv[0][q][e], cv[1][q][e], cv[2][q][e], cv[3][q][e]};
+                acc[b] = mfma(a, pop[ks], acc[b]);
+            }
+        }
+        inv_prev = 1.0f / prob_scale;
+        run_max = new_max;
+    };
+
+    Tile A, B;
+    for (uint32_t t = w0; t < w1; t += 2) {
+        if (t == w0) fetch(A, t);
+        if (t + 1 < w1) fetch(B, t + 1);
+        process(A, t);
+        if (t + 1 >= w1) break;
+        if (t + 2 < w1) fetch(A, t + 2);
+        process(B, t + 1);
+    }
+
+    // ---- this wave's (m, l, acc): acc = (64 acc' - 71.5 B) / prob_scale_last
+    const float off = bsum * (kLevelUnit * kLevelOffset);
+    __syncthreads();  // every wave is past its q_lds reads
+    float* mw = merge + wave * 16 * kD + n16 * kD;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int qd = 0; qd < 4; ++qd) {
+            float o[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float x = acc[4 * qd + j][i] * kLevelUnit;
+                o[j] = (x - off) * inv_prev;
+            }
+            const int c = (qd < 2 ? 0 : 128) + 32 * g + 8 * i + 4 * (qd & 1);
+            *(float4*)(mw + c) = make_float4(o[0], o[1], o[2], o[3]);
+        }
+    if (g == 0) {
+        ml[(wave * 16 + n16) * 2] = run_max;
+        ml[(wave * 16 + n16) * 2 + 1] = run_sum;
+    }
+    __syncthreads();
+
+    // ---- merge the four waves: thread -> head tid / 16, channels 16 (tid % 16) ..
+    const uint32_t h = tid >> 4, c0 = (tid & 15) * 16;
+    if (h < gc) {
+        float mwv[kWaves], M = kNegInf;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+            mwv[w] = ml[(w * 16 + h) * 2];
+            M = fmaxf(M, mwv[w]);
+        }
+        float f[kWaves], L = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+            f[w] = fexp(mwv[w] - M);
+            L += ml[(w * 16 + h) * 2 + 1] * f[w];
+        }
+        float* rec = p.records +
+                     (((size_t)token * p.Hq + p.G * kvh + head0 + h) * p.parts + part) * kRecFloats;
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {
+            float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+            for (int w = 0; w < kWaves; ++w) {
+                const float4 x = *(const float4*)(merge + (w * 16 + h) * kD + c0 + 4 * q4);
+                o.x += x.x * f[w];
+                o.y += x.y * f[w];
+                o.z += x.z * f[w];
+                o.w += x.w * f[w];
+            }
+            *(float4*)(rec + c0 + 4 * q4) = o;
+        }
+        if ((tid & 15) == 0) *(float2*)(rec + kD) = make_float2(M, L);
+    }
+}
+
+// One wave per (token, q head): merge the part records in order (the split
+// reduce's recurrence), normalise, output stage, cast.
+__global__ __launch_bounds__(kThreads) void kv4_reduce_kernel(Kv4Params p)
+{
+    const int lane = threadIdx.x & 63;
+    const uint32_t row = blockIdx.x * kWaves + (threadIdx.x >> 6);
+    if (row >= p.T * p.Hq) return;
+    const uint32_t token = row / p.Hq;
+    int32_t ctx_raw = p.context_lens[token];
+    uint32_t ctx = ctx_raw > 0 ? (uint32_t)ctx_raw : 0u;
+    const uint64_t cap = (uint64_t)p.max_blocks << p.block_shift;
+    if (ctx > cap) ctx = (uint32_t)cap;
+    const uint32_t tiles = (ctx + kTile - 1) / kTile;
+    const uint32_t live = (tiles + kWaves * p.nt - 1) / (kWaves * p.nt);
+    float run_max = kNegInf, run_sum = 0.0f;
+    float x[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    const float* rec = p.records + (size_t)row * p.parts * kRecFloats;
+    for (uint32_t k = 0; k < live; ++k, rec += kRecFloats) {
+        const float2 ml = *(const float2*)(rec + kD);
+        const float4 a = *(const float4*)(rec + 4 * lane);
+        const float new_max = fmaxf(run_max, ml.x);
+        const float alpha = fexp(run_max - new_max);
+        const float beta = fexp(ml.x - new_max);
+        run_sum = run_sum * alpha;
+        const float ps = ml.y * beta;
+        run_sum = run_sum + ps;
+        const float av[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float u = x[j] * alpha;
+            const float v = av[j] * beta;
+            x[j] = u + v;
+        }
+        run_max = new_max;
+    }
+    run_sum = run_sum + kEps;
+    const float inv = 1.0f / run_sum;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) x[j] = x[j] * inv;
+    if (p.stage >= 1) {
+        const float4 sg = *(const float4*)(p.pi_signs + 4 * lane);
+        const float s[4] = {sg.x, sg.y, sg.z, sg.w};
+        apply_pi(x, s, p.inv_sqrt_len, lane);
+        if (p.stage == 2) {
+            const uint2 gw = *(const uint2*)(p.gate + (size_t)row * kD + 4 * lane);
+            const uint16_t gb[4] = {(uint16_t)gw.x, (uint16_t)(gw.x >> 16), (uint16_t)gw.y,
+                                    (uint16_t)(gw.y >> 16)};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                float gv = elem_to_f32(gb[j], p.element);
+                gv = fmaxf(gv, kGateFloor);
+                float den = gv * -1.0f;
+                den = fexp(den);
+                den = den + 1.0f;
+                x[j] = x[j] / den;
+            }
+        }
+    }
+    uint2 o;
+    o.x = (uint32_t)f32_to_elem(x[0], p.element) | ((uint32_t)f32_to_elem(x[1], p.element) << 16);
+    o.y = (uint32_t)f32_to_elem(x[2], p.element) | ((uint32_t)f32_to_elem(x[3], p.element) << 16);
+    *(uint2*)(p.out + (size_t)row * kD + 4 * lane) = o;
+}
+
+// The FP8 e4m3 conversion pair the decode uses, exposed for the conversion test.
+__global__ void fp8_probe_kernel(const float* in, uint16_t* out, uint32_t n)
+{
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (2 * i + 1 >= n) return;
+    const h2_t h = fp8_pair(in[2 * i], in[2 * i + 1]);
+    *(uint32_t*)(out + 2 * i) = __builtin_bit_cast(uint32_t, h);
+}
+
+}  // namespace
+
+size_t kv4_lds_bytes(uint32_t npages)
+{
+    return (size_t)(kMergeFloats + kWaves * 32 + kScaleFloats) * sizeof(float) +
+           (size_t)npages * sizeof(int32_t);
+}
+
+hipError_t launch_kv4_decode(hipStream_t stream, const Kv4Params& p)
+{
+    const uint32_t npages = ((kWaves * p.nt * kTile - 1) >> p.block_shift) + 2;
+    const dim3 grid(p.parts, p.H * p.chunks, p.T);
+    hipLaunchKernelGGL(kv4_decode_kernel, grid, dim3(kThreads), kv4_lds_bytes(npages), stream, p);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const uint32_t rows = p.T * p.Hq;
+    hipLaunchKernelGGL(kv4_reduce_kernel, dim3((rows + kWaves - 1) / kWaves), dim3(kThreads), 0,
+                       stream, p);
+    return hipGetLastError();
+}
+
+hipError_t launch_fp8_probe(hipStream_t stream, const float* in, uint16_t* out, uint32_t n)
+{
+    const uint32_t pairs = n / 2;
+    if (pairs == 0) return hipSuccess;
+    hipLaunchKernelGGL(fp8_probe_kernel, dim3((pairs + 255) / 256), dim3(256), 0, stream, in, out, n);
+    return hipGetLastError();
+}
+
+}  // namespace tq4

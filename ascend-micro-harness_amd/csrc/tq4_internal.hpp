@@ -54,6 +54,27 @@ hipError_t launch_codebook_quantize(hipStream_t stream, uint32_t book, uint32_t 
 hipError_t launch_codebook_dequantize(hipStream_t stream, uint32_t bits, const uint8_t* codes,
                                       float* recon, uint64_t count);
 
+// KV4/FP8 NZ-tiled decode (kv4fp8_decode.hip); filled by the ABI layer.
+struct Kv4Params {
+    const float* query;          // rotated FP32 [T][Hq][256] (pre-rotated entry)
+    const uint16_t* raw_query;   // element bits [T][Hq][256] (raw-query entry) or null
+    float* query_out;            // raw-query entry: the rotated query written back (or null)
+    const uint8_t* key;
+    const uint8_t* value;
+    const float* scales;
+    const int32_t* block_table;
+    const int32_t* context_lens;
+    const float* pi_signs;
+    const uint16_t* gate;
+    float* records;              // [T][Hq][parts][260]
+    uint16_t* out;
+    uint32_t T, Hq, H, G, chunks, block_shift, max_blocks, num_blocks, parts, nt;
+    float score_scale, inv_gain, inv_sqrt_len;
+    uint32_t stage, element;
+};
+hipError_t launch_kv4_decode(hipStream_t stream, const Kv4Params& p);
+hipError_t launch_fp8_probe(hipStream_t stream, const float* in, uint16_t* out, uint32_t n);
+
 // Byte offset of the counter region inside a workspace of K splits.
 size_t decode_records_bytes(uint32_t B, uint32_t Hq, uint32_t D, uint32_t K);
 

@@ -16,6 +16,9 @@ Reference launchers mirrored (paths relative to the reference checkout):
   splitk_combine          tests/common/l2_atomic_oracle.hpp:156-176 (host merge in the reference)
   icdf_quantize           kernels/camodel/icdf_quantize.cpp:161-172
   lloydmax_quantize       kernels/camodel/lloydmax_quantize.cpp:96-99
+  kv4fp8_decode           include/turboquant_fused_decode_opt.hpp:186-188 (launch_fused_decode_opt)
+  kv4fp8_decode_raw_query include/turboquant_fused_decode_opt.hpp:192-194
+  fused_decode_opt_launch tests/common/fused_decode_opt_fixture.hpp (Fixture::launch, launch_raw)
 """
 from __future__ import annotations
 
@@ -83,6 +86,14 @@ def lib():
     L.tq4_icdf_quantize.argtypes = [_P, _I32, _P, _P, _U32]
     L.tq4_lloydmax_quantize.restype = _I32
     L.tq4_lloydmax_quantize.argtypes = [_P] * 5 + [_U32] * 4
+    L.tq4_kv4fp8_workspace_bytes.restype = C.c_uint64
+    L.tq4_kv4fp8_workspace_bytes.argtypes = [_P]
+    L.tq4_kv4fp8_decode.restype = _I32
+    L.tq4_kv4fp8_decode.argtypes = [_P, _P, _P]
+    L.tq4_kv4fp8_decode_raw_query.restype = _I32
+    L.tq4_kv4fp8_decode_raw_query.argtypes = [_P, _P, _P]
+    L.tq4_fp8_e4m3_round.restype = _I32
+    L.tq4_fp8_e4m3_round.argtypes = [_P, _P, _P, C.c_uint64]
     _lib = L
     return L
 
@@ -317,4 +328,137 @@ __all__ = [
     "reshape_scatter", "decode_workspace_bytes", "auto_splits", "decode_workspace",
     "paged_decode", "paged_decode_partials", "splitk_combine", "icdf_quantize",
     "lloydmax_quantize", "TQ4_DECODE_QUERY_ROTATED", "TQ4_MAX_SPLITS",
+    "Kv4Fp8Launch", "Kv4Fp8Buffers", "Kv4Fp8RawQueryBuffers", "fused_decode_opt_launch",
+    "kv4fp8_workspace_bytes", "kv4fp8_decode", "kv4fp8_decode_raw_query", "fp8_e4m3_round",
 ]
+
+
+# ------------------------------------------------- KV4/FP8 NZ-tiled decode
+class Kv4Fp8Launch(C.Structure):
+    """tq4_kv4fp8_launch (include/tq4_kv4fp8.h): the reference's Launch fields
+    (include/turboquant_fused_decode_opt.hpp:98-124) plus num_blocks and
+    workspace_bytes."""
+    _fields_ = [(n, _U32) for n in (
+        "grid", "tokens", "heads", "kv_heads", "head_size", "block_size", "max_blocks", "splits",
+        "heads_per_task", "tasks_per_block", "reduce_tasks_per_block", "fused_context_limit")] + \
+        [("scale", _F32), ("inv_sqrt_len", _F32)] + \
+        [(n, _U32) for n in ("prologue_vectors_per_block", "prologue_cube_chunk_vectors",
+                             "output_stage", "element_type", "probe_page", "probe_tile",
+                             "num_blocks")] + [("workspace_bytes", C.c_uint64)]
+
+
+class Kv4Fp8Buffers(C.Structure):
+    _fields_ = [(n, _P) for n in ("query", "key", "value", "scales", "block_table",
+                                  "context_lengths", "mode_tables", "workspace", "output",
+                                  "tiling")]
+
+
+class Kv4Fp8RawQueryBuffers(C.Structure):
+    _fields_ = [(n, _P) for n in ("raw_query", "pi_signs", "rot_tables", "h16", "gate")] + \
+        [("decode", Kv4Fp8Buffers)]
+
+
+def fused_decode_opt_launch(tokens, heads, kv_heads, block_size, max_blocks, splits=1,
+                            heads_per_task=16, fused_context_limit=4096, scale=0.0625,
+                            inv_sqrt_len=0.0625, output_stage=0, element_type=0,
+                            raw_query=False, num_blocks=0):
+    """The Launch the reference's fixture builds (Fixture::launch / launch_raw):
+    tasks spread over at most 32 blocks."""
+    group = heads // kv_heads if kv_heads else 0
+    chunk = min(heads_per_task, group) if group else 1
+    tasks = tokens * kv_heads * splits * ((group + chunk - 1) // chunk if chunk else 0)
+    tpb = max(1, (tasks + 31) // 32)
+    grid = max(1, (tasks + tpb - 1) // tpb)
+    L = Kv4Fp8Launch()
+    L.grid, L.tokens, L.heads, L.kv_heads = grid, tokens, heads, kv_heads
+    L.head_size, L.block_size, L.max_blocks, L.splits = 256, block_size, max_blocks, splits
+    L.heads_per_task, L.tasks_per_block = heads_per_task, tpb
+    L.reduce_tasks_per_block = max(1, (tokens * heads + grid - 1) // grid)
+    L.fused_context_limit, L.scale, L.inv_sqrt_len = fused_context_limit, scale, inv_sqrt_len
+    if raw_query:
+        L.prologue_vectors_per_block = (tokens * heads + grid - 1) // grid
+    L.output_stage, L.element_type = output_stage, element_type
+    L.probe_page, L.probe_tile = 0xFFFFFFFF, 0
+    L.num_blocks = num_blocks
+    return L
+
+
+def kv4fp8_workspace_bytes(launch):
+    return int(lib().tq4_kv4fp8_workspace_bytes(C.byref(launch)))
+
+
+def _kv4_prepare(launch, tensors, workspace, device, stream):
+    for name, t in tensors:
+        _dev(t, name)
+    need = kv4fp8_workspace_bytes(launch)
+    if need == 0:
+        raise ValueError("kv4fp8 decode: unsupported geometry")
+    if workspace is None:
+        workspace = torch.empty(need, dtype=torch.uint8, device=device)
+    launch.workspace_bytes = workspace.numel() * workspace.element_size()
+    return workspace
+
+
+def kv4fp8_decode(query, key_cache, value_cache, scales, block_table, context_lens, kv_heads,
+                  block_size, num_blocks, out=None, workspace=None, out_dtype=torch.float16,
+                  splits=1, heads_per_task=16, fused_context_limit=4096, scale=None,
+                  inv_sqrt_len=None, stream=None):
+    """The pre-rotated entry: query FP32 [T][Hq][256] -> out [T][Hq][256] (FP16/BF16)."""
+    T, Hq, d = query.shape
+    element = 1 if (out.dtype if out is not None else out_dtype) == torch.bfloat16 else 0
+    if out is None:
+        out = torch.empty((T, Hq, d), dtype=out_dtype, device=query.device)
+    L = fused_decode_opt_launch(T, Hq, kv_heads, block_size, block_table.shape[1], splits,
+                                heads_per_task, fused_context_limit,
+                                1.0 / math.sqrt(d) if scale is None else scale,
+                                1.0 / math.sqrt(d) if inv_sqrt_len is None else inv_sqrt_len,
+                                0, element, False, num_blocks)
+    workspace = _kv4_prepare(L, (("query", query), ("key_cache", key_cache),
+                                 ("value_cache", value_cache), ("scales", scales),
+                                 ("block_table", block_table), ("context_lens", context_lens),
+                                 ("out", out)), workspace, query.device, stream)
+    B = Kv4Fp8Buffers(_ptr(query), _ptr(key_cache), _ptr(value_cache), _ptr(scales),
+                      _ptr(block_table), _ptr(context_lens), None, _ptr(workspace), _ptr(out),
+                      None)
+    _check(lib().tq4_kv4fp8_decode(_stream(stream), C.byref(L), C.byref(B)), "kv4fp8_decode")
+    return out
+
+
+def kv4fp8_decode_raw_query(raw_query, pi_signs, key_cache, value_cache, scales, block_table,
+                            context_lens, kv_heads, block_size, num_blocks, gate=None,
+                            output_stage=1, query_out=None, out=None, workspace=None,
+                            splits=1, heads_per_task=16, fused_context_limit=4096, scale=None,
+                            inv_sqrt_len=None, stream=None):
+    """The raw-query entry: raw_query FP16/BF16 [T][Hq][256] in the original
+    basis -> out (same element type); query_out receives the rotated FP32 query."""
+    T, Hq, d = raw_query.shape
+    element = 1 if raw_query.dtype == torch.bfloat16 else 0
+    if out is None:
+        out = torch.empty_like(raw_query)
+    L = fused_decode_opt_launch(T, Hq, kv_heads, block_size, block_table.shape[1], splits,
+                                heads_per_task, fused_context_limit,
+                                1.0 / math.sqrt(d) if scale is None else scale,
+                                1.0 / math.sqrt(d) if inv_sqrt_len is None else inv_sqrt_len,
+                                output_stage, element, True, num_blocks)
+    workspace = _kv4_prepare(L, (("raw_query", raw_query), ("pi_signs", pi_signs),
+                                 ("key_cache", key_cache), ("value_cache", value_cache),
+                                 ("scales", scales), ("block_table", block_table),
+                                 ("context_lens", context_lens), ("gate", gate),
+                                 ("query_out", query_out), ("out", out)),
+                             workspace, raw_query.device, stream)
+    D = Kv4Fp8Buffers(_ptr(query_out), _ptr(key_cache), _ptr(value_cache), _ptr(scales),
+                      _ptr(block_table), _ptr(context_lens), None, _ptr(workspace), _ptr(out),
+                      None)
+    R = Kv4Fp8RawQueryBuffers(_ptr(raw_query), _ptr(pi_signs), None, None, _ptr(gate), D)
+    _check(lib().tq4_kv4fp8_decode_raw_query(_stream(stream), C.byref(L), C.byref(R)),
+           "kv4fp8_decode_raw_query")
+    return out
+
+
+def fp8_e4m3_round(x, stream=None):
+    """FP32 -> the FP8 e4m3 operand grid (RNE), as FP16 values."""
+    _dev(x, "x")
+    out = torch.empty(x.shape, dtype=torch.float16, device=x.device)
+    _check(lib().tq4_fp8_e4m3_round(_stream(stream), _ptr(x), _ptr(out), x.numel()),
+           "fp8_e4m3_round")
+    return out

@@ -1,4 +1,4 @@
-"""The C ABI without a GPU: libtq4.so loads, exports every symbol include/tq4.h
+"""The C ABI without a GPU: libtq4.so loads, exports every symbol include/*.h
 declares, and refuses bad geometry before touching the HIP runtime (no compute
 call is made here)."""
 import ctypes as C
@@ -8,14 +8,16 @@ import re
 import pytest
 
 REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADER = os.path.join(REPO, "include", "tq4.h")
+HEADERS = [os.path.join(REPO, "include", h) for h in ("tq4.h", "tq4_kv4fp8.h")]
 LIB = os.path.join(REPO, "ascend-micro-harness_amd", "libtq4.so")
 
 
 def declared_functions():
-    text = open(HEADER).read()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(tq4_[a-z0-9_]+)\s*\(", text)))
+    names = set()
+    for h in HEADERS:
+        text = re.sub(r"/\*.*?\*/", "", open(h).read(), flags=re.S)
+        names |= set(re.findall(r"\b(tq4_[a-z0-9_]+)\s*\(", text))
+    return sorted(names)
 
 
 @pytest.fixture(scope="module")
@@ -27,7 +29,7 @@ def test_library_exports_every_declared_symbol(lib):
     names = declared_functions()
     assert len(names) >= 10
     for n in names:
-        assert hasattr(lib, n), f"{n} declared in include/tq4.h but not exported"
+        assert hasattr(lib, n), f"{n} declared in include/ but not exported"
 
 
 def test_status_strings_and_version(lib):
@@ -107,3 +109,60 @@ def test_codebook_refusals(lib):
     assert g(None, 0, None, d, 1) == -1
     assert g(None, 1, d, d, 0) == 0
 
+
+
+def test_kv4fp8_refusals_and_workspace(tq4, lib):
+    """The KV4/FP8 entry points: valid_launch's refusals (before any HIP call)
+    and the workspace size."""
+    d = C.c_void_p(4096)
+    L = lambda **kw: tq4.fused_decode_opt_launch(**{**dict(  # noqa: E731
+        tokens=1, heads=16, kv_heads=1, block_size=64, max_blocks=17, splits=3,
+        num_blocks=36), **kw})
+    ok = L()
+    need = tq4.kv4fp8_workspace_bytes(ok)
+    assert need > 0 and need % 256 == 0
+    bufs = tq4.Kv4Fp8Buffers(d, d, d, d, d, d, None, d, d, None)
+    dec = lambda launch, b=bufs: lib.tq4_kv4fp8_decode(None, C.byref(launch), C.byref(b))  # noqa: E731
+    ok.workspace_bytes = need - 256
+    assert dec(ok) == -6                                   # workspace too small
+    bad = L()
+    bad.head_size = 128
+    assert dec(bad) == -2                                  # D = 256 only
+    for kw in (dict(kv_heads=5, heads=20), dict(heads=18, kv_heads=4), dict(block_size=96),
+               dict(block_size=192), dict(max_blocks=0), dict(num_blocks=0)):
+        x = L(**kw)
+        x.workspace_bytes = 1 << 30
+        assert dec(x) == -3, kw
+        assert tq4.kv4fp8_workspace_bytes(x) == 0
+    for k in (0, 9):
+        x = L(splits=k)
+        x.workspace_bytes = 1 << 30
+        assert dec(x) == -5
+    x = L()
+    x.workspace_bytes = 1 << 30
+    x.grid = 1
+    x.tasks_per_block = 1                                  # tasks not covered
+    assert dec(x) == -3
+    x = L()
+    x.workspace_bytes = 1 << 30
+    x.element_type = 2
+    assert dec(x) == -3
+    nb = tq4.Kv4Fp8Buffers(None, d, d, d, d, d, None, d, d, None)
+    x = L()
+    x.workspace_bytes = 1 << 30
+    assert dec(x, nb) == -1                                # no query
+    raw = lambda launch, g=d: lib.tq4_kv4fp8_decode_raw_query(  # noqa: E731
+        None, C.byref(launch), C.byref(tq4.Kv4Fp8RawQueryBuffers(d, d, None, None, g, bufs)))
+    x = tq4.fused_decode_opt_launch(1, 16, 1, 64, 17, 3, num_blocks=36, raw_query=True,
+                                    output_stage=3)
+    x.workspace_bytes = 1 << 30
+    assert raw(x) == -7                                    # stage
+    x.output_stage = 2
+    assert raw(x, None) == -7                              # gated without a gate
+    x.output_stage = 1
+    x.prologue_cube_chunk_vectors = 8
+    assert raw(x) == -3                                    # Cube chunk 0 or 16
+    x.prologue_cube_chunk_vectors = 16
+    x.prologue_vectors_per_block = 0
+    assert raw(x) == -3                                    # prologue share
+    assert lib.tq4_fp8_e4m3_round(None, d, d, 3) == -10   # odd count

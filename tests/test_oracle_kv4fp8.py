@@ -196,12 +196,14 @@ def _levels(b, hi, signed=True):
     return (np.where(n >= 8, n - 16, n) if signed else n) + 0.5
 
 
-def random_case(rng, T, H, G, S, P, ctx):
+def random_case(rng, T, H, G, S, P, ctx, key_scale=(0.02, 0.3)):
+    """Random NZ caches; key_scale sets the logit spread (the default gives
+    logits of standard deviation ~0.5, (0.5, 2.0) about 5: a peaked softmax)."""
     key = rng.integers(0, 256, P * S * H * 128, dtype=np.uint8)
     val = rng.integers(0, 256, P * S * H * 128, dtype=np.uint8)
     scales = np.full(P * S * 8, np.nan, np.float32)
     for h in range(H):
-        scales[h::8] = rng.uniform(0.02, 0.3, P * S).astype(np.float32) * GAIN
+        scales[h::8] = rng.uniform(*key_scale, P * S).astype(np.float32) * GAIN
         scales[H + h::8] = rng.uniform(0.5, 2.0, P * S).astype(np.float32) * GAIN
     maxb = max((c + S - 1) // S for c in ctx)
     table = np.full((T, maxb), -1, np.int32)
