@@ -272,11 +272,14 @@ void kv4_decode_kernel(Kv4Params p)
     const uint32_t H = p.H;
     const uint32_t m8 = 8 * n16;  // this lane's packed value columns 8m..8m+7
 
+    // Every fetch issues the same loads (an unmapped page reads page 0 and its
+    // tile is masked), so the count of loads in flight behind a tile is fixed
+    // and the compiler waits for exactly that tile's operands.
     auto fetch = [&](Tile& r, uint32_t t) {
         const uint32_t row_abs = t * kTile;
-        const int32_t e = win[(row_abs >> p.block_shift) - page0];
+        int32_t e = win[(row_abs >> p.block_shift) - page0];
         r.ok = e >= 0 && (uint32_t)e < p.num_blocks;
-        if (!r.ok) return;
+        e = r.ok ? e : 0;
         const uint32_t rip = row_abs & (S - 1);
         const size_t base = ((size_t)(uint32_t)e * S + rip) * H * 128 + (size_t)kvh * (kTile * 128);
         const int8_t* kb = (const int8_t*)p.key + base;
@@ -303,8 +306,8 @@ void kv4_decode_kernel(Kv4Params p)
     for (int b = 0; b < 16; ++b) acc[b] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
     auto process = [&](const Tile& r, uint32_t t) {
-        if (!r.ok) return;
-        const uint32_t valid = min((uint32_t)kTile, ctx - t * kTile);
+        // rows of the tile that count; 0 for an unmapped page (the tile adds nothing)
+        const uint32_t valid = r.ok ? min((uint32_t)kTile, ctx - t * kTile) : 0u;
         // scales through the wave's LDS slot: row `lane` in, rows 16tb + 4g .. out
         sc[lane] = (r.ks * p.score_scale) * kLevelUnit;
         sc[kTile + lane] = r.vs * p.inv_gain;
@@ -348,13 +351,15 @@ void kv4_decode_kernel(Kv4Params p)
 #pragma unroll
         for (int j = 1; j < 16; ++j) tmax = fmaxf(tmax, s[j]);
         tmax = col_max(tmax);
+        tmax = valid ? tmax : kNegInf;
         const float new_max = fmaxf(run_max, tmax);
         const float alpha = fexp(run_max - new_max);
         float part_sum = 0.0f, pmax = 0.0f;
         float pv[16];
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
-            const float e = fexp(s[j] - new_max);
+            const uint32_t row = 16 * (j >> 2) + 4 * g + (j & 3);
+            const float e = row < valid ? fexp(s[j] - new_max) : 0.0f;
             part_sum += e;
             pv[j] = e * vsc[j];
             pmax = fmaxf(pmax, pv[j]);
@@ -375,8 +380,9 @@ void kv4_decode_kernel(Kv4Params p)
             p1 += (float)h[0] + (float)h[1];
         }
         p1 = col_sum(p1);
-        // acc holds acc_ref * prob_scale (this tile's units): rescale, then add P8 . V
-        const float rho = alpha * (prob_scale * inv_prev);
+        // acc holds acc_ref * prob_scale (this tile's units): rescale, then add
+        // P8 . V. A tile that adds nothing keeps the previous units.
+        const float rho = valid ? alpha * (prob_scale * inv_prev) : 1.0f;
         bsum = bsum * rho;
         bsum = bsum + p1;
 #pragma unroll
@@ -405,18 +411,28 @@ void kv4_decode_kernel(Kv4Params p)
                 acc[b] = mfma(a, pop[ks], acc[b]);
             }
         }
-        inv_prev = 1.0f / prob_scale;
+        inv_prev = valid ? 1.0f / prob_scale : inv_prev;
         run_max = new_max;
     };
 
-    Tile A, B;
-    for (uint32_t t = w0; t < w1; t += 2) {
-        if (t == w0) fetch(A, t);
-        if (t + 1 < w1) fetch(B, t + 1);
-        process(A, t);
-        if (t + 1 >= w1) break;
-        if (t + 2 < w1) fetch(A, t + 2);
-        process(B, t + 1);
+    // A three-deep ring: tiles t+1 and t+2 are in flight while t is processed
+    // (the index is clamped, so the tail re-reads the last tile).
+    if (w0 < w1) {
+        Tile R0, R1, R2;
+        const uint32_t last = w1 - 1;
+        fetch(R0, w0);
+        fetch(R1, min(w0 + 1, last));
+        for (uint32_t t = w0;; t += 3) {
+            fetch(R2, min(t + 2, last));
+            process(R0, t);
+            if (t + 1 > last) break;
+            fetch(R0, min(t + 3, last));
+            process(R1, t + 1);
+            if (t + 2 > last) break;
+            fetch(R1, min(t + 4, last));
+            process(R2, t + 2);
+            if (t + 3 > last) break;
+        }
     }
 
     // ---- this wave's (m, l, acc): acc = (64 acc' - 71.5 B) / prob_scale_last
