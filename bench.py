@@ -271,7 +271,7 @@ def main():
 
     extra = {}
     if not args.no_extra:
-        extra = extra_workloads(tq4, torch, dev, w)
+        extra = extra_workloads(tq4, torch, dev, w, cpu=not args.no_cpu)
 
     cpu = None
     if not args.no_cpu:
@@ -309,7 +309,7 @@ def main():
     print(json.dumps(result), flush=True)
 
 
-def extra_workloads(tq4, torch, dev, w):
+def extra_workloads(tq4, torch, dev, w, cpu=True):
     """reshape_and_cache tokens/s and the batched step."""
     out = {}
     rng = np.random.default_rng(0x71340002)
@@ -406,7 +406,75 @@ def extra_workloads(tq4, torch, dev, w):
                           "algorithmic_bytes": ibytes}}
     log(f"codebook: Lloyd-Max {lbytes / (lms * 1e-3) / 1e9:.0f} GB/s, "
         f"ICDF {ibytes / (ims * 1e-3) / 1e9:.0f} GB/s")
+    out["kv4fp8_decode"] = kv4fp8_workloads(tq4, torch, dev, cpu)
     return out
+
+
+def kv4fp8_cache_bytes(tokens, ctx, kv_heads):
+    """Live KV4/FP8 cache bytes, as the reference's benchmark counts them
+    (Fixture::cache_bytes: 256 packed bytes per row and KV head for K and V,
+    plus the row's 32-byte scale slot)."""
+    return tokens * ctx * (kv_heads * 256 + 32)
+
+
+def kv4fp8_workloads(tq4, torch, dev, cpu=True):
+    """The KV4/FP8 NZ-tiled decode: the reference benchmark's shape
+    (bench_turboquant_decode_splitk --impl fused-opt: 1 request, 16 q heads over
+    one KV head, D=256, 128-row pages, FP32 pre-rotated query, FP16 output) at
+    ctx 4096, and a batched case beyond the 256 MiB Infinity Cache."""
+    res = {}
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0x4B5F8)
+    gain = 2.9832882881
+    for name, (T, H, G, S, ctx) in (("ref_shape_1x16q1kv_ctx4096", (1, 1, 16, 128, 4096)),
+                                     ("batched_32x64q4kv_ctx8192", (32, 4, 16, 128, 8192))):
+        pages = (ctx + S - 1) // S
+        P = T * pages
+        key = torch.randint(0, 256, (P * S * H * 128,), dtype=torch.uint8, device=dev,
+                            generator=gen)
+        val = torch.randint(0, 256, key.shape, dtype=torch.uint8, device=dev, generator=gen)
+        sc = (torch.rand(P * S * 8, device=dev, generator=gen) * 1.5 + 0.5) * gain
+        tb = torch.randperm(P, device=dev, generator=gen).to(torch.int32).view(T, pages)
+        ln = torch.full((T,), ctx, dtype=torch.int32, device=dev)
+        q = torch.randn((T, H * G, 256), device=dev, generator=gen)
+        o = torch.empty((T, H * G, 256), dtype=torch.float16, device=dev)
+        L = tq4.fused_decode_opt_launch(T, H * G, H, S, pages, num_blocks=P)
+        ws = torch.empty(tq4.kv4fp8_workspace_bytes(L), dtype=torch.uint8, device=dev)
+        run = lambda: tq4.kv4fp8_decode(q, key, val, sc, tb, ln, H, S, P, out=o,  # noqa: E731
+                                        workspace=ws)
+        run()
+        torch.cuda.synchronize()
+        assert torch.isfinite(o.float()).all(), "kv4fp8 decode produced non-finite values"
+        ms, _, _ = graph_time(torch, [run] * 16, 256 if T == 1 else 64, 32 if T == 1 else 8)
+        nbytes = kv4fp8_cache_bytes(T, ctx, H) + T * H * G * 256 * (4 + 2) + T * pages * 4
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        res[name] = {"us": round(ms * 1e3, 3), "GBps": round(gbs, 1),
+                     "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
+                     "tokens": T, "q_heads": H * G, "kv_heads": H, "head_dim": 256,
+                     "ctx": ctx, "page_size": S, "algorithmic_bytes": nbytes,
+                     "cache": "warm" if nbytes < (256 << 20) else "beyond the Infinity Cache"}
+        log(f"kv4fp8 {name}: {ms * 1e3:.2f} us -> {gbs:.0f} GB/s")
+        if cpu and T == 1:
+            # the C oracle (oracle/kv4fp8_oracle.c) on the same inputs, bounded at ~2 s
+            sys.path.insert(0, os.path.join(REPO, "tests"))
+            from oracle_bindings import Oracle
+            orc = Oracle()
+            threads = min(16, os.cpu_count() or 1)
+            h = [x.cpu().numpy() for x in (q, key, val, sc, tb, ln)]
+            iters, t0 = 0, time.perf_counter()
+            while time.perf_counter() - t0 < 2.0:
+                orc.kv4fp8_decode(*h, heads=H * G, kv_heads=H, block_size=S, max_blocks=pages,
+                                  num_blocks=P, threads=threads)
+                iters += 1
+            el = time.perf_counter() - t0
+            res[name]["cpu_baseline"] = {
+                "value": round(nbytes * iters / el / 1e9, 4), "unit": "GB/s",
+                "cores": min(threads, T * H),
+                "kind": "port", "us_per_decode": round(el / iters * 1e6, 1),
+                "sample": f"{iters} decodes of this shape by oracle/kv4fp8_oracle.c in "
+                          f"{el:.1f} s (FP64 products; one task per (token, kv head), so "
+                          f"{min(threads, T * H)} thread(s) busy)"}
+    return res
 
 
 def cpu_baseline(torch, w, dec_bytes, seconds):
