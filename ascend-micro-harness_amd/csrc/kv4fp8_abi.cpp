@@ -18,7 +18,7 @@ namespace {
 constexpr uint32_t kTile = 64;
 constexpr uint32_t kWaves = 4;
 constexpr uint32_t kRecFloats = 260;
-constexpr uint64_t kTargetWorkgroups = 256;  // one workgroup (four waves) per CU
+constexpr uint64_t kTargetWorkgroups = 512;  // two workgroups (eight waves) per CU
 constexpr uint32_t kMaxWindowPages = 8192;
 
 struct Plan {

@@ -13,7 +13,10 @@
 // covers 4*nt consecutive 64-row tiles, wave w the w-th nt of them. Each wave
 // runs the reference's tile recurrence over its tiles; the four waves merge
 // in LDS and the workgroup leaves one partial record (m, l, acc) per q head;
-// kv4_reduce_kernel merges a row's records and runs the egress. Tiles are the
+// kv4_reduce_kernel merges a row's records and runs the egress. (A variant
+// in which the last part of a (token, kv head, chunk) merges its group's
+// records in the same launch was slower: one workgroup then reads every
+// record of 16 rows, where the reduce spreads the rows over one wave each.) Tiles are the
 // reference's tiles (64 aligned rows of the sequence), so the per-tile FP8
 // operands are the same; only the summation order of the merges differs.
 //
@@ -55,13 +58,12 @@ constexpr float kLevelUnit = 64.0f;
 constexpr float kOperandMax = 448.0f;        // OperandMax<KV4_FP8> (e4m3)
 constexpr float kEps = 1e-20f;               // TurboQuantCodec4::kEps
 constexpr float kNegInf = -3.4028235e38f;    // kVectorNegInf
-constexpr float kMaskGain = -5.0e36f;
-constexpr float kMaskMid = 0.5f;
 constexpr float kGateFloor = -80.0f;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr uint32_t kRecFloats = 260;         // acc[256], m, l, pad, pad
 constexpr int kMergeFloats = kWaves * 16 * kD;
-constexpr int kScaleFloats = kWaves * 2 * kTile;
+constexpr int kScaleFloats = kWaves * 3 * kTile;
+constexpr int kQopFloats = 8 * 64 * 4;  // 8 k-steps x 64 lanes x 8 f16
 
 // Eight levels of one dword as f16 pairs, halves in nibble order 0,4,1,5,2,6,3,7:
 // each pair is kNib ? (bits ^ kCodeBase) : kCodeBase (v_bitop3 0x6A).
@@ -167,14 +169,85 @@ struct Tile {
     int ok;
 };
 
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
+// One wave, one (token, q head) row: merge the row's `live` part records in
+// order (the split reduce's recurrence, in batches of eight loads), normalise,
+// output stage, cast.
+__device__ __forceinline__ void combine_row(const Kv4Params& p, uint32_t row, uint32_t live,
+                                            int lane)
+{
+    float run_max = kNegInf, run_sum = 0.0f;
+    float x[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    const float* rec = p.records + (size_t)row * p.parts * kRecFloats;
+    // eight records' loads at a time (slots past `live` re-read the last
+    // record and are not merged), then the recurrence over them in order
+    for (uint32_t k0 = 0; k0 < live; k0 += 8) {
+        float2 mlv[8];
+        float4 av[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float* r = rec + (size_t)min(k0 + j, live - 1) * kRecFloats;
+            mlv[j] = *(const float2*)(r + kD);
+            av[j] = *(const float4*)(r + 4 * lane);
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            if (k0 + j >= live) break;
+            const float new_max = fmaxf(run_max, mlv[j].x);
+            const float alpha = fexp(run_max - new_max);
+            const float beta = fexp(mlv[j].x - new_max);
+            run_sum = run_sum * alpha;
+            const float ps = mlv[j].y * beta;
+            run_sum = run_sum + ps;
+            const float a4[4] = {av[j].x, av[j].y, av[j].z, av[j].w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float u = x[i] * alpha;
+                const float v = a4[i] * beta;
+                x[i] = u + v;
+            }
+            run_max = new_max;
+        }
+    }
+    run_sum = run_sum + kEps;
+    const float inv = 1.0f / run_sum;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) x[j] = x[j] * inv;
+    if (p.stage >= 1) {
+        const float4 sg = *(const float4*)(p.pi_signs + 4 * lane);
+        const float s[4] = {sg.x, sg.y, sg.z, sg.w};
+        apply_pi(x, s, p.inv_sqrt_len, lane);
+        if (p.stage == 2) {
+            const uint2 gw = *(const uint2*)(p.gate + (size_t)row * kD + 4 * lane);
+            const uint16_t gb[4] = {(uint16_t)gw.x, (uint16_t)(gw.x >> 16), (uint16_t)gw.y,
+                                    (uint16_t)(gw.y >> 16)};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                float gv = elem_to_f32(gb[j], p.element);
+                gv = fmaxf(gv, kGateFloor);
+                float den = gv * -1.0f;
+                den = fexp(den);
+                den = den + 1.0f;
+                x[j] = x[j] / den;
+            }
+        }
+    }
+    uint2 o;
+    o.x = (uint32_t)f32_to_elem(x[0], p.element) | ((uint32_t)f32_to_elem(x[1], p.element) << 16);
+    o.y = (uint32_t)f32_to_elem(x[2], p.element) | ((uint32_t)f32_to_elem(x[3], p.element) << 16);
+    *(uint2*)(p.out + (size_t)row * kD + 4 * lane) = o;
+}
+
+// Two waves per SIMD (248 registers): one wave's VALU and MFMA work overlaps
+// the other's; a three-deep ring at one wave per SIMD was 15 % slower.
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void kv4_decode_kernel(Kv4Params p)
 {
     extern __shared__ __align__(16) float lds[];
     float* merge = lds;                                  // [4][16][256] (q rows first)
     float* q_lds = lds;                                  // [16][256]
     float* ml = lds + kMergeFloats;                      // [4][16][2]
-    float* sc_all = ml + kWaves * 32;                    // [4][2][64]
+    h8_t* qop_lds = (h8_t*)(ml + kWaves * 32);           // [8 k-steps][64 lanes] query operand
+    float* sc_all = ml + kWaves * 32 + kQopFloats;       // [4][3][64]
     int32_t* win = (int32_t*)(sc_all + kScaleFloats);    // the part's block-table window
 
     const int tid = threadIdx.x, lane = tid & 63;
@@ -192,8 +265,8 @@ void kv4_decode_kernel(Kv4Params p)
     const uint32_t tiles = (ctx + kTile - 1) / kTile;
     const uint32_t t0 = part * kWaves * p.nt;
     const bool live = t0 < tiles;
-    // no live tile: no record (the reduce counts parts from ctx); part 0 of a
-    // raw-query launch still writes the rotated query back
+    // a part with no live tile leaves no record (the reduce counts parts from
+    // ctx); part 0 of a raw-query launch still writes the rotated query back
     if (!live && !(part == 0 && p.query_out != nullptr)) return;
     const uint32_t t1 = live ? min(t0 + kWaves * p.nt, tiles) : t0;
     const uint32_t head0 = chunk * 16;
@@ -232,6 +305,44 @@ void kv4_decode_kernel(Kv4Params p)
     __syncthreads();
     if (!live) return;
 
+    // ---- this wave's tiles
+    const uint32_t w0 = min(t0 + wave * p.nt, t1), w1 = min(w0 + p.nt, t1);
+    float* sc = sc_all + wave * 3 * kTile;
+    const uint32_t H = p.H;
+    const uint32_t m8 = 8 * n16;  // this lane's packed value columns 8m..8m+7
+
+    // Every fetch issues the same loads (an unmapped page reads page 0 and its
+    // tile is masked), so the count of loads in flight behind a tile is fixed
+    // and the compiler waits for exactly that tile's operands.
+    auto fetch = [&](Tile& r, uint32_t t) {
+        const uint32_t row_abs = t * kTile;
+        int32_t e = win[(row_abs >> p.block_shift) - page0];
+        r.ok = e >= 0 && (uint32_t)e < p.num_blocks;
+        e = r.ok ? e : 0;
+        const uint32_t rip = row_abs & (S - 1);
+        const size_t base = ((size_t)(uint32_t)e * S + rip) * H * 128 + (size_t)kvh * (kTile * 128);
+        const int8_t* kb = (const int8_t*)p.key + base;
+        const int8_t* vb = (const int8_t*)p.value + base;
+#pragma unroll
+        for (int tb = 0; tb < 4; ++tb) {
+            const u4_t* src = (const u4_t*)(kb + (g * kTile + 16 * tb + n16) * 32);
+            r.k[2 * tb] = src[0];
+            r.k[2 * tb + 1] = src[1];
+        }
+        const int8_t* vcol = vb + ((m8 >> 5) * kTile) * 32 + (m8 & 31);
+#pragma unroll
+        for (int tb = 0; tb < 4; ++tb)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) r.v[4 * tb + i] = *(const uint2*)(vcol + (16 * tb + 4 * g + i) * 32);
+        const float* srow = p.scales + ((size_t)(uint32_t)e * S + rip + lane) * 8;
+        r.ks = srow[kvh];
+        r.vs = srow[H + kvh];
+    };
+
+    // the first tile's loads go out before the query prologue
+    Tile R0, R1;
+    if (w0 < w1) fetch(R0, w0);
+
     // ---- the query operand of head n16 for k group g: k-step ks covers the
     // dword d = 8g + ks of a key row, channels 4d + {0, 2, 128, 130, 1, 3, 129, 131}.
     float qv[8][8];
@@ -265,52 +376,31 @@ void kv4_decode_kernel(Kv4Params p)
     }
     q1 = col_sum(q1);
     const float sbias = -kLevelOffset * q1;
-
-    // ---- this wave's tiles
-    const uint32_t w0 = min(t0 + wave * p.nt, t1), w1 = min(w0 + p.nt, t1);
-    float* sc = sc_all + wave * 2 * kTile;
-    const uint32_t H = p.H;
-    const uint32_t m8 = 8 * n16;  // this lane's packed value columns 8m..8m+7
-
-    // Every fetch issues the same loads (an unmapped page reads page 0 and its
-    // tile is masked), so the count of loads in flight behind a tile is fixed
-    // and the compiler waits for exactly that tile's operands.
-    auto fetch = [&](Tile& r, uint32_t t) {
-        const uint32_t row_abs = t * kTile;
-        int32_t e = win[(row_abs >> p.block_shift) - page0];
-        r.ok = e >= 0 && (uint32_t)e < p.num_blocks;
-        e = r.ok ? e : 0;
-        const uint32_t rip = row_abs & (S - 1);
-        const size_t base = ((size_t)(uint32_t)e * S + rip) * H * 128 + (size_t)kvh * (kTile * 128);
-        const int8_t* kb = (const int8_t*)p.key + base;
-        const int8_t* vb = (const int8_t*)p.value + base;
+    // one copy of the query operand for the four waves (identical in each)
+    if (wave == 0) {
 #pragma unroll
-        for (int tb = 0; tb < 4; ++tb) {
-            const u4_t* src = (const u4_t*)(kb + (g * kTile + 16 * tb + n16) * 32);
-            r.k[2 * tb] = src[0];
-            r.k[2 * tb + 1] = src[1];
-        }
-        const int8_t* vcol = vb + ((m8 >> 5) * kTile) * 32 + (m8 & 31);
-#pragma unroll
-        for (int tb = 0; tb < 4; ++tb)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) r.v[4 * tb + i] = *(const uint2*)(vcol + (16 * tb + 4 * g + i) * 32);
-        const float* srow = p.scales + ((size_t)(uint32_t)e * S + rip + lane) * 8;
-        r.ks = srow[kvh];
-        r.vs = srow[H + kvh];
-    };
+        for (int ks = 0; ks < 8; ++ks) qop_lds[ks * 64 + lane] = qop[ks];
+    }
+    __syncthreads();
 
     float run_max = kNegInf, run_sum = 0.0f, bsum = 0.0f, inv_prev = 1.0f;
     f4_t acc[16];
 #pragma unroll
     for (int b = 0; b < 16; ++b) acc[b] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
+    const u4_t ones = u4_t{0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u};  // f16 1.0
     auto process = [&](const Tile& r, uint32_t t) {
         // rows of the tile that count; 0 for an unmapped page (the tile adds nothing)
         const uint32_t valid = r.ok ? min((uint32_t)kTile, ctx - t * kTile) : 0u;
-        // scales through the wave's LDS slot: row `lane` in, rows 16tb + 4g .. out
-        sc[lane] = (r.ks * p.score_scale) * kLevelUnit;
-        sc[kTile + lane] = r.vs * p.inv_gain;
+        // per-row operands through the wave's LDS slot (row `lane` in, rows
+        // 16tb + 4g .. out): key and value scales, and the row mask as an
+        // additive bias -- 0 (x + 0 = x) or -inf, as the reference's Min with
+        // its -2.5e36 mask leaves an exp of 0 -- with the dead rows' scales
+        // zeroed so that no poisoned slot reaches the sums
+        const bool live_row = (uint32_t)lane < valid;
+        sc[lane] = live_row ? (r.ks * p.score_scale) * kLevelUnit : 0.0f;
+        sc[kTile + lane] = live_row ? r.vs * p.inv_gain : 0.0f;
+        sc[2 * kTile + lane] = live_row ? 0.0f : -INFINITY;
         // scores
         f4_t s4[4];
 #pragma unroll
@@ -319,7 +409,7 @@ void kv4_decode_kernel(Kv4Params p)
 #pragma unroll
             for (int ks = 0; ks < 8; ++ks) {
                 const uint32_t w = ks < 4 ? r.k[2 * tb][ks] : r.k[2 * tb + 1][ks - 4];
-                c = mfma(codes8(w), qop[ks], c);
+                c = mfma(codes8(w), qop_lds[ks * 64 + lane], c);
             }
             s4[tb] = c;
         }
@@ -328,38 +418,26 @@ void kv4_decode_kernel(Kv4Params p)
         for (int tb = 0; tb < 4; ++tb) {
             const f4_t k4 = *(const f4_t*)(sc + 16 * tb + 4 * g);
             const f4_t v4 = *(const f4_t*)(sc + kTile + 16 * tb + 4 * g);
+            const f4_t m4 = *(const f4_t*)(sc + 2 * kTile + 16 * tb + 4 * g);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 float x = s4[tb][i] * k4[i];
                 x = x * q_inv;
-                s[4 * tb + i] = x;
+                s[4 * tb + i] = x + m4[i];
                 vsc[4 * tb + i] = v4[i];
-            }
-        }
-        if (valid < (uint32_t)kTile) {
-            const float mid = kMaskMid - (float)valid;
-#pragma unroll
-            for (int j = 0; j < 16; ++j) {
-                const uint32_t row = 16 * (j >> 2) + 4 * g + (j & 3);
-                float mask = (float)row + mid;
-                mask = mask * kMaskGain;
-                s[j] = row < valid ? fminf(s[j], mask) : mask;
-                vsc[j] = row < valid ? vsc[j] : 0.0f;
             }
         }
         float tmax = s[0];
 #pragma unroll
         for (int j = 1; j < 16; ++j) tmax = fmaxf(tmax, s[j]);
-        tmax = col_max(tmax);
-        tmax = valid ? tmax : kNegInf;
+        tmax = col_max(tmax);  // -inf when no row counts: new_max stays run_max
         const float new_max = fmaxf(run_max, tmax);
         const float alpha = fexp(run_max - new_max);
         float part_sum = 0.0f, pmax = 0.0f;
         float pv[16];
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
-            const uint32_t row = 16 * (j >> 2) + 4 * g + (j & 3);
-            const float e = row < valid ? fexp(s[j] - new_max) : 0.0f;
+            const float e = fexp(s[j] - new_max);
             part_sum += e;
             pv[j] = e * vsc[j];
             pmax = fmaxf(pmax, pv[j]);
@@ -371,67 +449,61 @@ void kv4_decode_kernel(Kv4Params p)
         pmax = pmax + kEps;
         const float prob_scale = kOperandMax / pmax;
         h8_t pop[2];
-        float p1 = 0.0f;
 #pragma unroll
         for (int j = 0; j < 16; j += 2) {
             const h2_t h = fp8_pair(pv[j] * prob_scale, pv[j + 1] * prob_scale);
             pop[j >> 3][j & 7] = h[0];
             pop[j >> 3][(j & 7) + 1] = h[1];
-            p1 += (float)h[0] + (float)h[1];
         }
-        p1 = col_sum(p1);
         // acc holds acc_ref * prob_scale (this tile's units): rescale, then add
         // P8 . V. A tile that adds nothing keeps the previous units.
         const float rho = valid ? alpha * (prob_scale * inv_prev) : 1.0f;
-        bsum = bsum * rho;
-        bsum = bsum + p1;
 #pragma unroll
         for (int b = 0; b < 16; ++b) acc[b] = acc[b] * rho;
+        // sum(P8) per head on the matrix unit (an all-ones operand): the
+        // context's level offset
+        f4_t p1 = mfma(ones, pop[0], f4_t{0.0f, 0.0f, 0.0f, 0.0f});
+        p1 = mfma(ones, pop[1], p1);
+        bsum = bsum * rho;
+        bsum = bsum + p1[0];
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
-            // row pairs (tb, i01), (tb, i23), (tb+1, i01), (tb+1, i23) of k-step ks
-            u4_t cv[4][4];
+            // row pairs (tb, i01), (tb, i23), (tb+1, i01), (tb+1, i23) of k-step ks;
+            // columns (2q, 2q+1) of them feed blocks 2q, 2q + 1 (low nibbles:
+            // channel 8m + b) and 8 + 2q, 9 + 2q (high: 128 + 8m + b - 8)
 #pragma unroll
-            for (int rp = 0; rp < 4; ++rp) {
-                const uint2 ra = r.v[4 * (2 * ks + (rp >> 1)) + 2 * (rp & 1)];
-                const uint2 rb = r.v[4 * (2 * ks + (rp >> 1)) + 2 * (rp & 1) + 1];
-                cv[rp][0] = codes8(__builtin_amdgcn_perm(rb.x, ra.x, 0x05040100u));
-                cv[rp][1] = codes8(__builtin_amdgcn_perm(rb.x, ra.x, 0x07060302u));
-                cv[rp][2] = codes8(__builtin_amdgcn_perm(rb.y, ra.y, 0x05040100u));
-                cv[rp][3] = codes8(__builtin_amdgcn_perm(rb.y, ra.y, 0x07060302u));
-            }
-            // block b: channel 8m + b (b < 8, low nibble of column b) or
-            // 128 + 8m + b - 8 (high nibble); codes8 of columns (2q, 2q+1)
-            // gives pairs for blocks 2q, 8 + 2q, 2q + 1, 9 + 2q.
+            for (int q = 0; q < 4; ++q) {
+                u4_t cv[4];
 #pragma unroll
-            for (int b = 0; b < 16; ++b) {
-                const int col = b & 7, q = col >> 1;
-                const int e = (col & 1) * 2 + (b >> 3);
-                const u4_t a = u4_t{cv[0][q][e], cv[1][q][e], cv[2][q][e], cv[3][q][e]};
-                acc[b] = mfma(a, pop[ks], acc[b]);
+                for (int rp = 0; rp < 4; ++rp) {
+                    const uint2 ra = r.v[4 * (2 * ks + (rp >> 1)) + 2 * (rp & 1)];
+                    const uint2 rb = r.v[4 * (2 * ks + (rp >> 1)) + 2 * (rp & 1) + 1];
+                    const uint32_t x = q < 2 ? ra.x : ra.y, y = q < 2 ? rb.x : rb.y;
+                    cv[rp] = codes8(__builtin_amdgcn_perm(y, x, (q & 1) ? 0x07060302u : 0x05040100u));
+                }
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int b = (e & 1) * 8 + 2 * q + (e >> 1);
+                    const u4_t a = u4_t{cv[0][e], cv[1][e], cv[2][e], cv[3][e]};
+                    acc[b] = mfma(a, pop[ks], acc[b]);
+                }
             }
         }
         inv_prev = valid ? 1.0f / prob_scale : inv_prev;
         run_max = new_max;
     };
 
-    // A three-deep ring: tiles t+1 and t+2 are in flight while t is processed
-    // (the index is clamped, so the tail re-reads the last tile).
+    // The register ring: tile t+1 is in flight while t is processed (the
+    // index is clamped, so the tail re-reads the last tile).
     if (w0 < w1) {
-        Tile R0, R1, R2;
         const uint32_t last = w1 - 1;
-        fetch(R0, w0);
-        fetch(R1, min(w0 + 1, last));
-        for (uint32_t t = w0;; t += 3) {
-            fetch(R2, min(t + 2, last));
+        for (uint32_t t = w0;; t += 2) {
+            fetch(R1, min(t + 1, last));
             process(R0, t);
             if (t + 1 > last) break;
-            fetch(R0, min(t + 3, last));
+            fetch(R0, min(t + 2, last));
             process(R1, t + 1);
             if (t + 2 > last) break;
-            fetch(R1, min(t + 4, last));
-            process(R2, t + 2);
-            if (t + 3 > last) break;
         }
     }
 
@@ -492,68 +564,19 @@ void kv4_decode_kernel(Kv4Params p)
     }
 }
 
-// One wave per (token, q head): merge the part records in order (the split
-// reduce's recurrence), normalise, output stage, cast.
+// One wave per (token, q head) row: combine_row over the row's part records.
 __global__ __launch_bounds__(kThreads) void kv4_reduce_kernel(Kv4Params p)
 {
     const int lane = threadIdx.x & 63;
     const uint32_t row = blockIdx.x * kWaves + (threadIdx.x >> 6);
     if (row >= p.T * p.Hq) return;
     const uint32_t token = row / p.Hq;
-    int32_t ctx_raw = p.context_lens[token];
+    const int32_t ctx_raw = p.context_lens[token];
     uint32_t ctx = ctx_raw > 0 ? (uint32_t)ctx_raw : 0u;
     const uint64_t cap = (uint64_t)p.max_blocks << p.block_shift;
     if (ctx > cap) ctx = (uint32_t)cap;
     const uint32_t tiles = (ctx + kTile - 1) / kTile;
-    const uint32_t live = (tiles + kWaves * p.nt - 1) / (kWaves * p.nt);
-    float run_max = kNegInf, run_sum = 0.0f;
-    float x[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    const float* rec = p.records + (size_t)row * p.parts * kRecFloats;
-    for (uint32_t k = 0; k < live; ++k, rec += kRecFloats) {
-        const float2 ml = *(const float2*)(rec + kD);
-        const float4 a = *(const float4*)(rec + 4 * lane);
-        const float new_max = fmaxf(run_max, ml.x);
-        const float alpha = fexp(run_max - new_max);
-        const float beta = fexp(ml.x - new_max);
-        run_sum = run_sum * alpha;
-        const float ps = ml.y * beta;
-        run_sum = run_sum + ps;
-        const float av[4] = {a.x, a.y, a.z, a.w};
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const float u = x[j] * alpha;
-            const float v = av[j] * beta;
-            x[j] = u + v;
-        }
-        run_max = new_max;
-    }
-    run_sum = run_sum + kEps;
-    const float inv = 1.0f / run_sum;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) x[j] = x[j] * inv;
-    if (p.stage >= 1) {
-        const float4 sg = *(const float4*)(p.pi_signs + 4 * lane);
-        const float s[4] = {sg.x, sg.y, sg.z, sg.w};
-        apply_pi(x, s, p.inv_sqrt_len, lane);
-        if (p.stage == 2) {
-            const uint2 gw = *(const uint2*)(p.gate + (size_t)row * kD + 4 * lane);
-            const uint16_t gb[4] = {(uint16_t)gw.x, (uint16_t)(gw.x >> 16), (uint16_t)gw.y,
-                                    (uint16_t)(gw.y >> 16)};
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                float gv = elem_to_f32(gb[j], p.element);
-                gv = fmaxf(gv, kGateFloor);
-                float den = gv * -1.0f;
-                den = fexp(den);
-                den = den + 1.0f;
-                x[j] = x[j] / den;
-            }
-        }
-    }
-    uint2 o;
-    o.x = (uint32_t)f32_to_elem(x[0], p.element) | ((uint32_t)f32_to_elem(x[1], p.element) << 16);
-    o.y = (uint32_t)f32_to_elem(x[2], p.element) | ((uint32_t)f32_to_elem(x[3], p.element) << 16);
-    *(uint2*)(p.out + (size_t)row * kD + 4 * lane) = o;
+    combine_row(p, row, (tiles + kWaves * p.nt - 1) / (kWaves * p.nt), lane);
 }
 
 // The FP8 e4m3 conversion pair the decode uses, exposed for the conversion test.
@@ -569,7 +592,7 @@ __global__ void fp8_probe_kernel(const float* in, uint16_t* out, uint32_t n)
 
 size_t kv4_lds_bytes(uint32_t npages)
 {
-    return (size_t)(kMergeFloats + kWaves * 32 + kScaleFloats) * sizeof(float) +
+    return (size_t)(kMergeFloats + kWaves * 32 + kQopFloats + kScaleFloats) * sizeof(float) +
            (size_t)npages * sizeof(int32_t);
 }
 

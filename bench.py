@@ -439,7 +439,7 @@ def kv4fp8_workloads(tq4, torch, dev, cpu=True):
         q = torch.randn((T, H * G, 256), device=dev, generator=gen)
         o = torch.empty((T, H * G, 256), dtype=torch.float16, device=dev)
         L = tq4.fused_decode_opt_launch(T, H * G, H, S, pages, num_blocks=P)
-        ws = torch.empty(tq4.kv4fp8_workspace_bytes(L), dtype=torch.uint8, device=dev)
+        ws = torch.zeros(tq4.kv4fp8_workspace_bytes(L), dtype=torch.uint8, device=dev)
         run = lambda: tq4.kv4fp8_decode(q, key, val, sc, tb, ln, H, S, P, out=o,  # noqa: E731
                                         workspace=ws)
         run()

@@ -89,7 +89,9 @@ typedef struct tq4_kv4fp8_raw_query_buffers {
     tq4_kv4fp8_buffers decode;
 } tq4_kv4fp8_raw_query_buffers;
 
-/* Workspace this decode needs for `launch` (bytes, 256-aligned). */
+/* Workspace this decode needs for `launch` (bytes, 256-aligned): the partial
+ * records of every (token, q head, part). No initialisation is needed;
+ * calls that overlap in time need their own workspaces. */
 uint64_t tq4_kv4fp8_workspace_bytes(const tq4_kv4fp8_launch* launch);
 
 /* The pre-rotated entry (launch_fused_decode_opt): output_stage is not read. */

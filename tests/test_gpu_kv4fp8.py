@@ -223,3 +223,44 @@ def test_bench_size_properties(tq4):
     tb2 = perm[tb].astype(np.int32)
     c = bits(tq4.kv4fp8_decode(*args(key2, val2, sc2, tb2)))
     assert np.array_equal(a, c)
+
+
+def test_workspace_reuse_and_graph_replays(tq4):
+    """The part tickets return to zero after every call: one workspace serves
+    repeated eager calls and HIP graph replays (eager work and synchronisations
+    in between), every result bit-identical; a second geometry on the same
+    workspace too."""
+    rng = np.random.default_rng(21)
+    T, H, G, S = 3, 2, 16, 64
+    ctx = [900, 1, 2000]
+    P = sum((c + S - 1) // S for c in ctx) + 3
+    q, key, val, sc, tb, ln = random_case(rng, T, H, G, S, P, ctx, key_scale=(0.5, 2.0))
+    L = tq4.fused_decode_opt_launch(T, H * G, H, S, tb.shape[1], num_blocks=P)
+    ws = torch.zeros(tq4.kv4fp8_workspace_bytes(L) + 4096, dtype=torch.uint8, device=DEV)
+    args = (dev(q), dev(key), dev(val), dev(sc), dev(tb), dev(ln), H, S, P)
+    out = torch.empty((T, H * G, 256), dtype=torch.float16, device=DEV)
+    call = lambda: tq4.kv4fp8_decode(*args, out=out, workspace=ws)  # noqa: E731
+    first = bits(call()).copy()
+    for _ in range(3):
+        assert np.array_equal(bits(call()), first)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        call()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        call()
+    for i in range(4):
+        out.zero_()
+        g.replay()
+        assert np.array_equal(bits(out), first), f"replay {i}"
+        assert np.array_equal(bits(call()), first), f"eager {i}"
+    # another geometry on the same (still zero-ticketed) workspace
+    q2, k2, v2, s2, t2, l2 = random_case(rng, 1, 1, 16, 128, 40, [3000])
+    a = bits(tq4.kv4fp8_decode(dev(q2), dev(k2), dev(v2), dev(s2), dev(t2), dev(l2), 1, 128, 40,
+                               workspace=ws))
+    b = bits(tq4.kv4fp8_decode(dev(q2), dev(k2), dev(v2), dev(s2), dev(t2), dev(l2), 1, 128, 40))
+    assert np.array_equal(a, b)
+    assert np.array_equal(bits(call()), first)
