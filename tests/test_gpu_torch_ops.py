@@ -138,3 +138,30 @@ def test_paged_attention_op_in_hip_graph(tq4, oracle):
         torch.cuda.synchronize()
         assert torch.equal(static_out.view(torch.int16), eager.view(torch.int16)), f"replay {i}"
         assert torch.equal(call().view(torch.int16), eager.view(torch.int16)), f"eager {i}"
+
+
+def test_fused_decode_opt_ops_match_bindings(tq4):
+    """torch.ops.tq4.fused_decode_opt(_raw_query): the direct bindings' bits."""
+    from test_oracle_kv4fp8 import random_case
+    rng = np.random.default_rng(16)
+    T, H, G, S = 2, 2, 16, 64
+    ctx = [700, 1500]
+    P = sum((c + S - 1) // S for c in ctx) + 2
+    q, key, val, sc, tb, ln = random_case(rng, T, H, G, S, P, ctx, key_scale=(0.5, 2.0))
+    d = [dev(x) for x in (q, key, val, sc, tb, ln)]
+    ws = tq4.torch_ops.kv4fp8_workspace_for(d[0], H, d[4], S, P)
+    for bf16 in (False, True):
+        a = torch.ops.tq4.fused_decode_opt(d[0], d[1], d[2], d[3], d[4], d[5], ws, H, S, 3, 16,
+                                           4096, 0.0, 0.0, bf16)
+        b = tq4.kv4fp8_decode(*d, H, S, P, out_dtype=torch.bfloat16 if bf16 else torch.float16)
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+    signs = dev(np.where(rng.random(256) < 0.5, -1.0, 1.0).astype(np.float32))
+    raw = torch.from_numpy(q).to("cuda").to(torch.bfloat16)
+    gate = torch.from_numpy(rng.standard_normal(q.shape).astype(np.float32)).to("cuda").to(torch.bfloat16)
+    qr1, qr2 = torch.empty_like(d[0]), torch.empty_like(d[0])
+    a = torch.ops.tq4.fused_decode_opt_raw_query(raw, signs, gate, qr1, d[1], d[2], d[3], d[4],
+                                                 d[5], ws, H, S, 3, 16, 2, 4096, 0.0, 0.0)
+    b = tq4.kv4fp8_decode_raw_query(raw, signs, d[1], d[2], d[3], d[4], d[5], H, S, P, gate=gate,
+                                    output_stage=2, query_out=qr2)
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+    assert torch.equal(qr1.view(torch.int32), qr2.view(torch.int32))

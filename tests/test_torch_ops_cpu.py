@@ -50,3 +50,31 @@ def test_cpu_tensors_raise(ops):
         ops.paged_attention(q, kc, kc, torch.zeros(2, 4, 2, 16), torch.zeros(1, 4, dtype=torch.int32),
                             torch.ones(1, dtype=torch.int32), torch.ones(128),
                             torch.zeros(64, dtype=torch.uint8), None, 2, 16, 1, 0.0, 0.0, 1, False)
+
+
+def test_kv4fp8_schemas_and_fakes(ops):
+    s = str(ops.fused_decode_opt.default._schema)
+    assert "Tensor(a6!) workspace" in s and s.endswith("-> Tensor")
+    r = str(ops.fused_decode_opt_raw_query.default._schema)
+    assert "Tensor(a3!) query_rot" in r and "Tensor(a9!) workspace" in r
+    T, Hq, H, S = 2, 32, 2, 64
+    kc = meta(10 * S * H * 128, dtype=torch.uint8)
+    args = (kc, kc, meta(10 * S * 8), meta(T, 5, dtype=torch.int32), meta(T, dtype=torch.int32),
+            meta(4096, dtype=torch.uint8))
+    for bf16 in (False, True):
+        out = ops.fused_decode_opt(meta(T, Hq, 256), *args, H, S, 1, 16, 4096, 0.0, 0.0, bf16)
+        assert out.shape == (T, Hq, 256) and out.device.type == "meta"
+        assert out.dtype == (torch.bfloat16 if bf16 else torch.float16)
+    q = meta(T, Hq, 256, dtype=torch.bfloat16)
+    out = ops.fused_decode_opt_raw_query(q, meta(256), None, meta(T, Hq, 256), *args, H, S, 1,
+                                         16, 1, 4096, 0.0, 0.0)
+    assert out.shape == q.shape and out.dtype == torch.bfloat16
+
+
+def test_kv4fp8_cpu_tensors_raise(ops):
+    kc = torch.zeros(4 * 64 * 128, dtype=torch.uint8)
+    with pytest.raises(NotImplementedError):
+        ops.fused_decode_opt(torch.zeros(1, 16, 256), kc, kc, torch.ones(4 * 64 * 8),
+                             torch.zeros(1, 4, dtype=torch.int32), torch.ones(1, dtype=torch.int32),
+                             torch.zeros(4096, dtype=torch.uint8), 1, 64, 1, 16, 4096, 0.0, 0.0,
+                             False)
