@@ -234,8 +234,14 @@ __device__ __forceinline__ void rec_load(__amdgpu_buffer_rsrc_t r, uint32_t byte
 // (tests/common/l2_atomic_oracle.hpp:156-176; identity :100-108)
 // FUSED: the records are encoded; a chunk is reloaded until none of its words
 // is zero (bounded by kPollLimit), then zeroed for the next call.
-template <int D, bool FUSED, int NS = 8>
-__device__ void combine_records(const float* rr, uint32_t K, int lane, float (&v)[D / 32])
+// own_k < K: the calling split's own record is not in memory. Its encoded
+// words come from own(h, a), in this lane's combine layout, called once after
+// the first chunk's loads are issued (so it runs under their round trip);
+// they replace that slot's loaded words, and the combine is the same as if
+// the record had been stored and loaded.
+template <int D, bool FUSED, int NS = 8, class Own>
+__device__ void combine_records(const float* rr, uint32_t K, int lane, float (&v)[D / 32],
+                                uint32_t own_k, Own&& own)
 {
     constexpr int CC = D / 32;
     constexpr int LD = CC >= 4 ? 4 : CC;  // floats per load
@@ -244,8 +250,9 @@ __device__ void combine_records(const float* rr, uint32_t K, int lane, float (&v
     const int c = lane & 31, ks = lane >> 5;
     const uint32_t x = FUSED ? kRecMagic : 0u;
     float M = -INFINITY, L = 0.0f, a[CC];
+    uint32_t oh[2] = {0u, 0u}, oa[CC];
 #pragma unroll
-    for (int j = 0; j < CC; ++j) a[j] = 0.0f;
+    for (int j = 0; j < CC; ++j) a[j] = 0.0f, oa[j] = 0u;
     for (uint32_t k0 = 0; k0 < K; k0 += 2 * NS) {
         uint32_t roff[NS];
         bool vi[NS];
@@ -266,12 +273,29 @@ __device__ void combine_records(const float* rr, uint32_t K, int lane, float (&v
                     rec_load<LD, FUSED>(rsrc, roff[i] + 4u * (4 + c * CC + j), &aw[i][j]);
             }
             if constexpr (!FUSED) break;
+            if (k0 == 0 && it == 0) own(oh, oa);
+            // the own slot (wave-uniform: slot i_own of lane parity p_own)
+            if (own_k >= k0 && own_k < k0 + 2 * NS) {
+                const uint32_t i_own = (own_k - k0) >> 1;
+                const bool here = ks == (int)((own_k - k0) & 1);
+#pragma unroll
+                for (int i = 0; i < NS; ++i) {
+                    if (i == (int)i_own) {
+                        hw[i][0] = here ? oh[0] : hw[i][0];
+                        hw[i][1] = here ? oh[1] : hw[i][1];
+#pragma unroll
+                        for (int j = 0; j < CC; ++j) aw[i][j] = here ? oa[j] : aw[i][j];
+                    }
+                }
+            }
+            // slots past K are not waited for (they may alias the own slot)
             uint32_t mn = 0xffffffffu;
 #pragma unroll
             for (int i = 0; i < NS; ++i) {
-                mn = min(mn, min(hw[i][0], hw[i][1]));
+                uint32_t ms = min(hw[i][0], hw[i][1]);
 #pragma unroll
-                for (int j = 0; j < CC; ++j) mn = min(mn, aw[i][j]);
+                for (int j = 0; j < CC; ++j) ms = min(ms, aw[i][j]);
+                mn = vi[i] ? min(mn, ms) : mn;
             }
             if (!__any(mn == 0u) || it + 1 >= kPollLimit) break;
         }
@@ -388,7 +412,10 @@ __host__ __device__ constexpr size_t region_floats(uint32_t G, uint32_t D)
 
 // One (seq, kv head, split) work item: MODE 0 exports the partial record,
 // MODE 1 is the fused path (ticket, export or local finish, combine).
-template <int D, int MODE>
+// OWN (MODE 1): the combining split keeps its own record in registers instead
+// of storing and polling it (the one-launch kernel; the persistent kernel
+// stores it, which keeps that kernel's register budget).
+template <int D, int MODE, bool OWN = true>
 __device__ __forceinline__ void decode_item(const DecodeParams& p, const uint32_t seq,
                                             const uint32_t kvh, const uint32_t split)
 {
@@ -886,7 +913,7 @@ __device__ __forceinline__ void decode_item(const DecodeParams& p, const uint32_
         const bool local = p.K == 1 || k_live == 1;
         const bool combiner = local || *flag;
         float es[CC];
-        if (!local) {
+        if (!local && (!combiner || !OWN)) {
             // ---- export this split's encoded record.
             const __amdgpu_buffer_rsrc_t rsrc = records_rsrc(
                 p.records + (((size_t)seq * p.Hq + (size_t)kvh * G) * p.K + split) * RS);
@@ -904,18 +931,57 @@ __device__ __forceinline__ void decode_item(const DecodeParams& p, const uint32_
                 }
             }
             if (!combiner) return;
-            // ---- the combiner: poll and combine every record, its own
-            // included (the sign and gate loads ride with the first poll)
+        }
+        if (!local) {
+            // ---- the combiner: poll the records of its rows and combine
+            // them. With OWN its own record is never stored: its words are
+            // made from LDS (the export's arithmetic, in the combine layout)
+            // while the first poll is in flight. The sign and gate loads
+            // ride with that poll.
             if (p.output_stage >= 1) load_lane_floats<D>(p.pi_signs, lane, es);
             for (uint32_t g = wave; g < G; g += kWaves) {
                 const size_t qh = (size_t)seq * p.Hq + kvh * G + g;
                 float gt[CC];
                 if (p.output_stage == 2) load_lane_floats<D>(p.gate + qh * D, lane, gt);
+                auto own = [&](uint32_t (&h)[2], uint32_t (&a)[CC]) {
+                    float f[kWaves], M, L;
+                    row_weights(g, f, M, L);
+                    h[0] = __float_as_uint(M == -INFINITY ? kMasked : M * kLn2) ^ kRecMagic;
+                    h[1] = __float_as_uint(L) ^ kRecMagic;
+                    if constexpr (CC >= 4) {
+#pragma unroll
+                        for (int j = 0; j < CC; j += 4) {
+                            const float4 v = combined4((g * D + (lane & 31) * CC + j) / 4, f);
+                            a[j] = __float_as_uint(v.x) ^ kRecMagic;
+                            a[j + 1] = __float_as_uint(v.y) ^ kRecMagic;
+                            a[j + 2] = __float_as_uint(v.z) ^ kRecMagic;
+                            a[j + 3] = __float_as_uint(v.w) ^ kRecMagic;
+                        }
+                    } else {  // d = 64: the lane's two channels of a float4
+                        const uint32_t ch = (lane & 31) * CC;
+                        const float4 v = combined4((g * D + ch) / 4, f);
+                        const bool hi = (ch & 2) != 0;
+                        a[0] = __float_as_uint(hi ? v.z : v.x) ^ kRecMagic;
+                        a[1] = __float_as_uint(hi ? v.w : v.y) ^ kRecMagic;
+                    }
+                };
+                auto none = [](uint32_t(&)[2], uint32_t(&)[CC]) {};
                 float v[CC];
-                if (k_live > 16)
-                    combine_records<D, true, 16>(p.records + qh * p.K * RS, k_live, lane, v);
-                else
-                    combine_records<D, true, 8>(p.records + qh * p.K * RS, k_live, lane, v);
+                if constexpr (OWN) {
+                    if (k_live > 16)
+                        combine_records<D, true, 16>(p.records + qh * p.K * RS, k_live, lane, v,
+                                                     split, own);
+                    else
+                        combine_records<D, true, 8>(p.records + qh * p.K * RS, k_live, lane, v,
+                                                    split, own);
+                } else {
+                    if (k_live > 16)
+                        combine_records<D, true, 16>(p.records + qh * p.K * RS, k_live, lane, v,
+                                                     ~0u, none);
+                    else
+                        combine_records<D, true, 8>(p.records + qh * p.K * RS, k_live, lane, v,
+                                                    ~0u, none);
+                }
                 egress_row<D>(v, es, gt, p.out + qh * D, p.inv_sqrt_len, p.output_stage, lane);
             }
             return;
@@ -1045,7 +1111,7 @@ void decode_persistent_kernel(DecodeParams p)
             kvh = r % p.Hkv;
             split = splits[seq] - 1;
         }
-        decode_item<D, 1>(p, seq, kvh, split);
+        decode_item<D, 1, false>(p, seq, kvh, split);
         if (tid == 0) {
             if (fetched == n_items - 1)
                 __hip_atomic_store(p.queue, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1073,7 +1139,8 @@ __global__ __launch_bounds__(kThreads) void combine_kernel(DecodeParams p)
         if (row >= total) break;
         if (p.output_stage == 2) load_lane_floats<D>(p.gate + row * D, lane, gt);
         float v[CC];
-        combine_records<D, false>(p.records + row * p.K * (D + 4), p.K, lane, v);
+        combine_records<D, false>(p.records + row * p.K * (D + 4), p.K, lane, v, ~0u,
+                                  [](uint32_t(&)[2], uint32_t(&)[D / 32]) {});
         egress_row<D>(v, es, gt, p.out + row * D, p.inv_sqrt_len, p.output_stage, lane);
     }
 }
