@@ -147,15 +147,17 @@ size_t tq4_decode_workspace_bytes(uint32_t num_seqs, uint32_t num_heads, uint32_
 uint32_t tq4_decode_auto_splits(uint32_t num_seqs, uint32_t num_kv_heads,
                                 uint32_t max_blocks_per_seq, uint32_t block_size)
 {
-    // Splits of ~128 strips (64 MFMA pairs over four waves: the per-item
-    // prologue and combine stay a small share, and a large batch runs the
-    // persistent kernel over few, long items), but enough workgroups to fill
-    // every CU's two slots (256 CUs) when the batch is small, never fewer
-    // than 16 strips per split, and at most 64 splits (one to four record
-    // chunks per combine).
+    // Enough workgroups to fill every CU's two slots (256 CUs), and splits of
+    // at most ~512 strips; never fewer than 16 strips per split, and at most
+    // 64 splits (one to four record chunks per combine). Each extra item
+    // costs a table and a first-strip round trip, a merge and a record, and
+    // the persistent kernel orders the last splits longest first, so a batch
+    // that already fills the slots runs best with few, long items: on
+    // 64-sequence batches (8 KV heads) K = 1 beat K = 2 by 20 % at ctx 4096,
+    // and a spread of 1..32768 tokens wanted K = 4..8.
     const uint64_t strips = (uint64_t)max_blocks_per_seq * (block_size / kStrip);
     const uint64_t items = (uint64_t)num_seqs * num_kv_heads;
-    uint64_t k = (strips + 127) / 128;
+    uint64_t k = (strips + 511) / 512;
     const uint64_t fill = items == 0 ? 1 : (512 + items - 1) / items;
     if (k < fill) k = fill;
     const uint64_t by_len = strips / 16 > 0 ? strips / 16 : 1;

@@ -81,6 +81,7 @@ constexpr int kHdrFloats = 416;          // m_x, l_x [16][4], q_exp[16], flags, 
 constexpr uint32_t kRecMagic = 0x7FBADBADu;  // fused records hold bits ^ kRecMagic; 0 = not written
 constexpr uint32_t kPollLimit = 1u << 20;     // bound of the combiner's record polls
 constexpr uint32_t kPersistentMaxSeqs = 4096; // the persistent kernel stages two words per sequence
+constexpr uint32_t kLptMaxSeqs = 1024;        // and a third (the last-split order) up to this many
 constexpr int kStripSlots = TQ4_MAX_SPLIT_STRIPS + 4;  // staged window rows + padding
 
 // Eight codes of one dword as fp16 (1 + u/64), u = nibble ^ 8; halves in
@@ -1030,9 +1031,10 @@ __global__ TQ4_DECODE_ATTRS void decode_kernel(DecodeParams p)
 // Every split but a sequence's last covers exactly the partition width, so
 // the queue lists those equal items first -- (seq, kv head, split) order --
 // and the last, shorter splits after them (one per (seq, kv head), or the
-// zero-context item of an empty sequence), where their spread of sizes packs
-// the tail. Every workgroup derives the order from the context lengths (a
-// prefix over sequences, staged in LDS). A workgroup takes item blockIdx.x,
+// zero-context item of an empty sequence), longest first for batches of up to
+// kLptMaxSeqs sequences, so their spread of sizes packs the tail. Every
+// workgroup derives the order from the context lengths (a prefix over
+// sequences and a rank of the last splits, staged in LDS). A workgroup takes item blockIdx.x,
 // then one item at a time from an agent-scope queue counter, fetched as the
 // current item starts so the round trip hides under it. Each of the n_items
 // fetches returns a distinct value and the one that returns n_items - 1 is
@@ -1048,6 +1050,10 @@ void decode_persistent_kernel(DecodeParams p)
     extern __shared__ float smem[];
     uint32_t* full = (uint32_t*)(smem + kHdrFloats + kStripSlots + region_floats(p.G, D));
     uint32_t* splits = full + p.B;  // max(1, live splits) per sequence
+    // Up to kLptMaxSeqs sequences: the order of the last splits, longest
+    // first (ties in sequence order), so the short ones pack the tail.
+    uint32_t* order = splits + p.B;
+    const bool lpt = p.B <= kLptMaxSeqs;
     uint32_t* next_lds = (uint32_t*)(smem + 145);
     const int tid = threadIdx.x, lane = tid & 63;
     const uint32_t width = (p.max_blocks + p.K - 1) / p.K;
@@ -1061,8 +1067,30 @@ void decode_persistent_kernel(DecodeParams p)
         kl = kl > 0 ? kl : 1u;
         splits[s] = kl;
         full[s] = p.Hkv * (kl - 1);
+        if (lpt) order[s] = pages - (kl - 1) * width;  // the last split's pages (the sort key)
     }
     __syncthreads();
+    // Rank of each sequence's last split: longer ones, then equal ones of
+    // lower index, come before it (a stable descending sort; every
+    // workgroup derives the same order). Kept in registers until all keys
+    // are read.
+    constexpr int kRanks = kLptMaxSeqs / kThreads;
+    uint32_t rank[kRanks];
+    if (lpt) {
+#pragma unroll
+        for (int i = 0; i < kRanks; ++i) {
+            const uint32_t s = tid + i * kThreads;
+            if (s < p.B) {
+                const uint32_t key = order[s];
+                uint32_t r = 0;
+                for (uint32_t t = 0; t < p.B; ++t) {
+                    const uint32_t kt = order[t];
+                    r += (kt > key || (kt == key && t < s)) ? 1u : 0u;
+                }
+                rank[i] = r;
+            }
+        }
+    }
     if (tid < 64) {  // inclusive prefix of the full items, 64 sequences per step
         uint32_t carry = 0;
         for (uint32_t b = 0; b < p.B; b += 64) {
@@ -1078,7 +1106,15 @@ void decode_persistent_kernel(DecodeParams p)
             carry = __shfl(v, 63, 64);
         }
     }
-    __syncthreads();
+    __syncthreads();  // every key is read: the ranks can be placed
+    if (lpt) {
+#pragma unroll
+        for (int i = 0; i < kRanks; ++i) {
+            const uint32_t s = tid + i * kThreads;
+            if (s < p.B) order[rank[i]] = s;
+        }
+        __syncthreads();
+    }
     const uint32_t n_full = full[p.B - 1];
     const uint32_t n_items = n_full + p.B * p.Hkv;
     uint32_t item = blockIdx.x;
@@ -1107,7 +1143,7 @@ void decode_persistent_kernel(DecodeParams p)
         } else {
             // a last split
             const uint32_t r = item - n_full;
-            seq = r / p.Hkv;
+            seq = lpt ? order[r / p.Hkv] : r / p.Hkv;
             kvh = r % p.Hkv;
             split = splits[seq] - 1;
         }
@@ -1179,7 +1215,7 @@ hipError_t launch_decode_t(hipStream_t stream, const DecodeParams& p, int mode)
     }
     // Fused: persistent when the split grid outnumbers the resident slots.
     if (p.queue != nullptr && p.K > 1 && p.B <= kPersistentMaxSeqs) {
-        const size_t lds_p = lds + 2 * (size_t)p.B * sizeof(uint32_t);
+        const size_t lds_p = lds + (p.B <= kLptMaxSeqs ? 3 : 2) * (size_t)p.B * sizeof(uint32_t);
         const uint32_t slots = persistent_slots<D>(lds_p);
         if (slots > 0 && blocks > slots) {
             hipLaunchKernelGGL((decode_persistent_kernel<D>), dim3(slots), dim3(kThreads), lds_p,

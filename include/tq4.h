@@ -152,7 +152,8 @@ int tq4_reshape_scatter(void* stream, uint32_t block_dim, const uint16_t* key,
 size_t tq4_decode_workspace_bytes(uint32_t num_seqs, uint32_t num_heads, uint32_t num_kv_heads,
                                   uint32_t head_size, uint32_t num_splits);
 
-/* A split count that puts several workgroups per compute unit in flight. */
+/* A split count for this geometry: at least two workgroups per compute unit
+ * in flight, and splits of at most ~512 strips of 16 tokens. */
 uint32_t tq4_decode_auto_splits(uint32_t num_seqs, uint32_t num_kv_heads,
                                 uint32_t max_blocks_per_seq, uint32_t block_size);
 

@@ -209,6 +209,18 @@ def test_persistent_ragged_batch(tq4, oracle):
     check_out(got, want, "persistent ragged")
 
 
+@pytest.mark.parametrize("B", [1000, 1100])
+def test_persistent_large_batch(tq4, oracle, B):
+    """Up to 1024 sequences the persistent kernel ranks the last splits by
+    length (four ranks per thread at 1000, many ties); past that they run
+    in sequence order."""
+    rng = np.random.default_rng(0x5E14 + B)
+    ctx = [int(x) for x in rng.integers(0, 160, B)]
+    got, want, _ = run_decode(tq4, oracle, rng, ctx, 4, 1, 128, 16,
+                              sum((c + 15) // 16 for c in ctx) + 8, 2)
+    check_out(got, want, f"persistent B={B}")
+
+
 def test_persistent_fewer_live_items_than_slots(tq4, oracle):
     """A large split grid whose live items are fewer than the resident
     workgroups: the surplus workgroups leave at once, nobody fetches."""
