@@ -75,10 +75,19 @@ int geometry(const tq4_kv4fp8_launch* L)
     return TQ4_OK;
 }
 
+uint64_t round256(uint64_t b) { return (b + 255) & ~(uint64_t)255; }
+
+// Workspace: the part tickets of every (token, kv head, chunk), then the
+// partial records of every (token, q head, part); both all-zero between calls.
+uint64_t counters_bytes(const tq4_kv4fp8_launch* L, const Plan& p)
+{
+    return round256((uint64_t)L->tokens * L->kv_heads * p.chunks * sizeof(uint32_t));
+}
+
 uint64_t records_bytes(const tq4_kv4fp8_launch* L, const Plan& p)
 {
-    const uint64_t b = (uint64_t)L->tokens * L->heads * p.parts * kRecFloats * sizeof(float);
-    return (b + 255) & ~(uint64_t)255;
+    return counters_bytes(L, p) +
+           round256((uint64_t)L->tokens * L->heads * p.parts * kRecFloats * sizeof(float));
 }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
@@ -105,7 +114,8 @@ tq4::Kv4Params params_of(const tq4_kv4fp8_launch* L, const tq4_kv4fp8_buffers* b
     p.scales = (const float*)b->scales;
     p.block_table = (const int32_t*)b->block_table;
     p.context_lens = (const int32_t*)b->context_lengths;
-    p.records = (float*)b->workspace;
+    p.counters = (uint32_t*)b->workspace;
+    p.records = (float*)((char*)b->workspace + counters_bytes(L, plan));
     p.out = (uint16_t*)b->output;
     p.T = L->tokens;
     p.Hq = L->heads;
@@ -135,6 +145,15 @@ uint64_t tq4_kv4fp8_workspace_bytes(const tq4_kv4fp8_launch* launch)
 {
     if (geometry(launch) != TQ4_OK) return 0;
     return records_bytes(launch, plan_of(launch));
+}
+
+int tq4_kv4fp8_workspace_init(void* stream, void* workspace, uint64_t workspace_bytes)
+{
+    if (!workspace) return TQ4_ERR_NULL_POINTER;
+    if (!aligned16(workspace)) return TQ4_ERR_WORKSPACE;
+    return tq4::launch_fill_zero((hipStream_t)stream, workspace, workspace_bytes) == hipSuccess
+               ? TQ4_OK
+               : TQ4_ERR_LAUNCH;
 }
 
 int tq4_kv4fp8_decode(void* stream, const tq4_kv4fp8_launch* launch,

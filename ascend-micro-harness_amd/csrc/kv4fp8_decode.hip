@@ -12,13 +12,12 @@
 // Work split. One workgroup = (token, kv head, 16-head chunk, part); part
 // covers 4*nt consecutive 64-row tiles, wave w the w-th nt of them. Each wave
 // runs the reference's tile recurrence over its tiles; the four waves merge
-// in LDS and the workgroup leaves one partial record (m, l, acc) per q head;
-// kv4_reduce_kernel merges a row's records and runs the egress. (A variant
-// in which the last part of a (token, kv head, chunk) merges its group's
-// records in the same launch was slower: one workgroup then reads every
-// record of 16 rows, where the reduce spreads the rows over one wave each.) Tiles are the
-// reference's tiles (64 aligned rows of the sequence), so the per-tile FP8
-// operands are the same; only the summation order of the merges differs.
+// in LDS. The parts holding the last four tickets of their (token, kv head,
+// chunk) then merge the group's partial records (m, l, acc), a quarter of
+// the rows each, in the same launch, and run the egress; the other parts
+// only export records. Tiles are the reference's tiles (64 aligned rows of
+// the sequence), so the per-tile FP8 operands are the same; only the
+// summation order of the merges differs.
 //
 // Operands on the f16 MFMA (16x16x32). Every FP8 e4m3 value and every level
 // n + 0.5 is exact in f16, and their products are exact in FP32, so the f16
@@ -37,6 +36,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "tq4_device.hpp"
 #include "tq4_internal.hpp"
 
 namespace tq4 {
@@ -169,45 +169,31 @@ struct Tile {
     int ok;
 };
 
-// One wave, one (token, q head) row: merge the row's `live` part records in
-// order (the split reduce's recurrence, in batches of eight loads), normalise,
-// output stage, cast.
-__device__ __forceinline__ void combine_row(const Kv4Params& p, uint32_t row, uint32_t live,
-                                            int lane)
+// One part record (m, l, acc) into a row's running merge: the split reduce's
+// recurrence, records taken in part order.
+__device__ __forceinline__ void merge_record(float& run_max, float& run_sum, float (&x)[4],
+                                             float m, float l, const float (&a)[4])
 {
-    float run_max = kNegInf, run_sum = 0.0f;
-    float x[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    const float* rec = p.records + (size_t)row * p.parts * kRecFloats;
-    // eight records' loads at a time (slots past `live` re-read the last
-    // record and are not merged), then the recurrence over them in order
-    for (uint32_t k0 = 0; k0 < live; k0 += 8) {
-        float2 mlv[8];
-        float4 av[8];
+    const float new_max = fmaxf(run_max, m);
+    const float alpha = fexp(run_max - new_max);
+    const float beta = fexp(m - new_max);
+    run_sum = run_sum * alpha;
+    const float ps = l * beta;
+    run_sum = run_sum + ps;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const float* r = rec + (size_t)min(k0 + j, live - 1) * kRecFloats;
-            mlv[j] = *(const float2*)(r + kD);
-            av[j] = *(const float4*)(r + 4 * lane);
-        }
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            if (k0 + j >= live) break;
-            const float new_max = fmaxf(run_max, mlv[j].x);
-            const float alpha = fexp(run_max - new_max);
-            const float beta = fexp(mlv[j].x - new_max);
-            run_sum = run_sum * alpha;
-            const float ps = mlv[j].y * beta;
-            run_sum = run_sum + ps;
-            const float a4[4] = {av[j].x, av[j].y, av[j].z, av[j].w};
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float u = x[i] * alpha;
-                const float v = a4[i] * beta;
-                x[i] = u + v;
-            }
-            run_max = new_max;
-        }
+    for (int i = 0; i < 4; ++i) {
+        const float u = x[i] * alpha;
+        const float v = a[i] * beta;
+        x[i] = u + v;
     }
+    run_max = new_max;
+}
+
+// One wave, one (token, q head) row, lane = channels 4 lane .. 4 lane + 3:
+// normalise the merged row, output stage, cast, store.
+__device__ __forceinline__ void finish_row(const Kv4Params& p, uint32_t row, float (&x)[4],
+                                           float run_sum, int lane)
+{
     run_sum = run_sum + kEps;
     const float inv = 1.0f / run_sum;
 #pragma unroll
@@ -237,6 +223,85 @@ __device__ __forceinline__ void combine_row(const Kv4Params& p, uint32_t row, ui
     *(uint2*)(p.out + (size_t)row * kD + 4 * lane) = o;
 }
 
+
+constexpr uint32_t kRecBytes = kRecFloats * 4;
+constexpr int kPollBatch = 16;  // records polled together (one round trip)
+
+// The combiner's merge of one row: the records of parts 0 .. live-1 in part
+// order, its own part's (`own`) from LDS and the others' polled from the
+// workspace. A batch of records is reloaded until none of its words is zero
+// (bounded by kPollLimit), then zeroed for the next call.
+__device__ __forceinline__ void combine_polled(const Kv4Params& p, uint32_t row, uint32_t live,
+                                               uint32_t own, const float* own_acc,
+                                               const float* own_ml, int lane, float (&x)[4],
+                                               float& run_sum)
+{
+    const __amdgpu_buffer_rsrc_t rs =
+        records_rsrc(p.records + (size_t)row * p.parts * kRecFloats);
+    const float4 oa = *(const float4*)(own_acc + 4 * lane);
+    const float2 om = *(const float2*)own_ml;
+    float run_max = kNegInf;
+    run_sum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) x[i] = 0.0f;
+    for (uint32_t k0 = 0; k0 < live; k0 += kPollBatch) {
+        uint32_t aw[kPollBatch][4], hw[kPollBatch][2];
+        for (uint32_t it = 0;; ++it) {
+            asm volatile("" ::: "memory");  // every poll reloads
+#pragma unroll
+            for (int j = 0; j < kPollBatch; ++j) {
+                const uint32_t k = k0 + j;
+                if (k < live && k != own) {
+                    rec_load<4, true>(rs, k * kRecBytes + 16u * lane, aw[j]);
+                    rec_load<2, true>(rs, k * kRecBytes + 4u * kD, hw[j]);
+                }
+            }
+            uint32_t mn = 0xffffffffu;
+#pragma unroll
+            for (int j = 0; j < kPollBatch; ++j) {
+                const uint32_t k = k0 + j;
+                if (k < live && k != own)
+                    mn = min(min(mn, min(hw[j][0], hw[j][1])),
+                             min(min(aw[j][0], aw[j][1]), min(aw[j][2], aw[j][3])));
+            }
+            if (!__any(mn == 0u) || it + 1 >= kPollLimit) break;
+        }
+#pragma unroll
+        for (int j = 0; j < kPollBatch; ++j) {
+            const uint32_t k = k0 + j;
+            if (k < live && k != own) {
+                __builtin_amdgcn_raw_buffer_store_b128(rec_u4_t{0u, 0u, 0u, 0u}, rs,
+                                                       k * kRecBytes + 16u * lane, 0,
+                                                       kCachePolicySc1);
+                if (lane == 0)
+                    __builtin_amdgcn_raw_buffer_store_b64(rec_u2_t{0u, 0u}, rs,
+                                                          k * kRecBytes + 4u * kD, 0,
+                                                          kCachePolicySc1);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < kPollBatch; ++j) {
+            const uint32_t k = k0 + j;
+            if (k >= live) break;
+            float m, l, a[4];
+            if (k == own) {
+                m = om.x;
+                l = om.y;
+                a[0] = oa.x;
+                a[1] = oa.y;
+                a[2] = oa.z;
+                a[3] = oa.w;
+            } else {
+                m = __uint_as_float(hw[j][0] ^ kRecMagic);
+                l = __uint_as_float(hw[j][1] ^ kRecMagic);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) a[i] = __uint_as_float(aw[j][i] ^ kRecMagic);
+            }
+            merge_record(run_max, run_sum, x, m, l, a);
+        }
+    }
+}
+
 // Two waves per SIMD (248 registers): one wave's VALU and MFMA work overlaps
 // the other's; a three-deep ring at one wave per SIMD was 15 % slower.
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
@@ -246,8 +311,10 @@ void kv4_decode_kernel(Kv4Params p)
     float* merge = lds;                                  // [4][16][256] (q rows first)
     float* q_lds = lds;                                  // [16][256]
     float* ml = lds + kMergeFloats;                      // [4][16][2]
-    h8_t* qop_lds = (h8_t*)(ml + kWaves * 32);           // [8 k-steps][64 lanes] query operand
-    float* sc_all = ml + kWaves * 32 + kQopFloats;       // [4][3][64]
+    int* role_lds = (int*)(ml + kWaves * 32);            // [4] this part's combine role
+    float* mlo = ml + kWaves * 32 + 4;                   // [16][2] merged (m, l) per head
+    h8_t* qop_lds = (h8_t*)(mlo + 32);                   // [8 k-steps][64 lanes] query operand
+    float* sc_all = mlo + 32 + kQopFloats;               // [4][3][64]
     int32_t* win = (int32_t*)(sc_all + kScaleFloats);    // the part's block-table window
 
     const int tid = threadIdx.x, lane = tid & 63;
@@ -265,9 +332,11 @@ void kv4_decode_kernel(Kv4Params p)
     const uint32_t tiles = (ctx + kTile - 1) / kTile;
     const uint32_t t0 = part * kWaves * p.nt;
     const bool live = t0 < tiles;
-    // a part with no live tile leaves no record (the reduce counts parts from
-    // ctx); part 0 of a raw-query launch still writes the rotated query back
-    if (!live && !(part == 0 && p.query_out != nullptr)) return;
+    const uint32_t live_parts = (tiles + kWaves * p.nt - 1) / (kWaves * p.nt);
+    // a part with no live tile leaves no record (every part counts the live
+    // parts from ctx); part 0 still writes the rotated query back (raw-query
+    // launch) and, when no part is live, the rows' zero context
+    if (!live && part != 0) return;
     const uint32_t t1 = live ? min(t0 + kWaves * p.nt, tiles) : t0;
     const uint32_t head0 = chunk * 16;
     const uint32_t gc = min(16u, p.G - head0);  // live heads of this chunk
@@ -303,7 +372,16 @@ void kv4_decode_kernel(Kv4Params p)
         *(float4*)(q_lds + h * kD + 4 * lane) = make_float4(x[0], x[1], x[2], x[3]);
     }
     __syncthreads();
-    if (!live) return;
+    const size_t row0 = (size_t)token * p.Hq + p.G * kvh + head0;  // the chunk's first row
+    if (!live) {
+        if (live_parts == 0) {  // part 0: no live tile, so every row's context is zero
+            for (uint32_t h = wave; h < gc; h += kWaves) {
+                float x[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+                finish_row(p, row0 + h, x, 0.0f, lane);
+            }
+        }
+        return;
+    }
 
     // ---- this wave's tiles
     const uint32_t w0 = min(t0 + wave * p.nt, t1), w1 = min(w0 + p.nt, t1);
@@ -342,6 +420,13 @@ void kv4_decode_kernel(Kv4Params p)
     // the first tile's loads go out before the query prologue
     Tile R0, R1;
     if (w0 < w1) fetch(R0, w0);
+    // This part's ticket of its (token, kv head, chunk): the last R ticket
+    // holders combine. Its round trip overlaps the tile loads; the value is
+    // first needed at the merge.
+    uint32_t* counter = p.counters + ((size_t)token * p.H + kvh) * p.chunks + chunk;
+    uint32_t ticket = 0;
+    if (live_parts > 1 && tid == 0)
+        ticket = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
     // ---- the query operand of head n16 for k group g: k-step ks covers the
     // dword d = 8g + ks of a key row, channels 4d + {0, 2, 128, 130, 1, 3, 129, 131}.
@@ -528,9 +613,27 @@ void kv4_decode_kernel(Kv4Params p)
         ml[(wave * 16 + n16) * 2] = run_max;
         ml[(wave * 16 + n16) * 2 + 1] = run_sum;
     }
+    // R = min(p.combiners, live parts) combiners: the parts holding the last
+    // R tickets, role 0 .. R-1, combine the rows h = role (mod R). Every
+    // other live part of the group took its ticket earlier or takes one
+    // later: the host allows R > 1 only when the whole grid is resident,
+    // so a combiner waits only on running workgroups. The last ticket resets
+    // the counter for the next call.
+    const uint32_t R = live_parts > 1 ? min(p.combiners, live_parts) : 1u;
+    if (tid == 0) {
+        int role = live_parts > 1 ? -1 : 0;
+        if (live_parts > 1) {
+            if (ticket >= live_parts - R) role = (int)(ticket - (live_parts - R));
+            if (ticket == live_parts - 1)
+                __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        *role_lds = role;
+    }
     __syncthreads();
 
     // ---- merge the four waves: thread -> head tid / 16, channels 16 (tid % 16) ..
+    // The merged row replaces the wave-0 slice (each thread reads and writes
+    // only its own channels of it); (M, L) go to mlo.
     const uint32_t h = tid >> 4, c0 = (tid & 15) * 16;
     if (h < gc) {
         float mwv[kWaves], M = kNegInf;
@@ -545,8 +648,6 @@ void kv4_decode_kernel(Kv4Params p)
             f[w] = fexp(mwv[w] - M);
             L += ml[(w * 16 + h) * 2 + 1] * f[w];
         }
-        float* rec = p.records +
-                     (((size_t)token * p.Hq + p.G * kvh + head0 + h) * p.parts + part) * kRecFloats;
 #pragma unroll
         for (int q4 = 0; q4 < 4; ++q4) {
             float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
@@ -558,25 +659,45 @@ void kv4_decode_kernel(Kv4Params p)
                 o.z += x.z * f[w];
                 o.w += x.w * f[w];
             }
-            *(float4*)(rec + c0 + 4 * q4) = o;
+            *(float4*)(merge + h * kD + c0 + 4 * q4) = o;
         }
-        if ((tid & 15) == 0) *(float2*)(rec + kD) = make_float2(M, L);
+        if ((tid & 15) == 0) *(float2*)(mlo + 2 * h) = make_float2(M, L);
     }
-}
+    __syncthreads();
+    const int role = *role_lds;
 
-// One wave per (token, q head) row: combine_row over the row's part records.
-__global__ __launch_bounds__(kThreads) void kv4_reduce_kernel(Kv4Params p)
-{
-    const int lane = threadIdx.x & 63;
-    const uint32_t row = blockIdx.x * kWaves + (threadIdx.x >> 6);
-    if (row >= p.T * p.Hq) return;
-    const uint32_t token = row / p.Hq;
-    const int32_t ctx_raw = p.context_lens[token];
-    uint32_t ctx = ctx_raw > 0 ? (uint32_t)ctx_raw : 0u;
-    const uint64_t cap = (uint64_t)p.max_blocks << p.block_shift;
-    if (ctx > cap) ctx = (uint32_t)cap;
-    const uint32_t tiles = (ctx + kTile - 1) / kTile;
-    combine_row(p, row, (tiles + kWaves * p.nt - 1) / (kWaves * p.nt), lane);
+    // ---- one live part: its rows finish from LDS (the merge of one record)
+    if (live_parts == 1) {
+        for (uint32_t hh = wave; hh < gc; hh += kWaves) {
+            const float4 a4 = *(const float4*)(merge + hh * kD + 4 * lane);
+            const float2 m2 = *(const float2*)(mlo + 2 * hh);
+            const float a[4] = {a4.x, a4.y, a4.z, a4.w};
+            float x[4] = {0.0f, 0.0f, 0.0f, 0.0f}, run_max = kNegInf, run_sum = 0.0f;
+            merge_record(run_max, run_sum, x, m2.x, m2.y, a);
+            finish_row(p, row0 + hh, x, run_sum, lane);
+        }
+        return;
+    }
+
+    // ---- export the records of the rows other parts combine: encoded
+    // (bits ^ kRecMagic, never 0) with device-coherent stores
+    for (uint32_t hh = wave; hh < gc; hh += kWaves) {
+        if (role >= 0 && hh % R == (uint32_t)role) continue;
+        const __amdgpu_buffer_rsrc_t rs =
+            records_rsrc(p.records + (row0 + hh) * p.parts * kRecFloats);
+        rec_store<4, true>(rs, part * kRecBytes + 16u * lane, merge + hh * kD + 4 * lane);
+        if (lane == 0) rec_store<2, true>(rs, part * kRecBytes + 4u * kD, mlo + 2 * hh);
+    }
+    if (role < 0) return;
+
+    // ---- combiner `role`: rows role, role + R, ..., one wave each
+    for (uint32_t i = wave; role + R * i < gc; i += kWaves) {
+        const uint32_t hh = role + R * i;
+        float x[4], run_sum;
+        combine_polled(p, row0 + hh, live_parts, part, merge + hh * kD, mlo + 2 * hh, lane, x,
+                       run_sum);
+        finish_row(p, row0 + hh, x, run_sum, lane);
+    }
 }
 
 // The FP8 e4m3 conversion pair the decode uses, exposed for the conversion test.
@@ -592,7 +713,8 @@ __global__ void fp8_probe_kernel(const float* in, uint16_t* out, uint32_t n)
 
 size_t kv4_lds_bytes(uint32_t npages)
 {
-    return (size_t)(kMergeFloats + kWaves * 32 + kQopFloats + kScaleFloats) * sizeof(float) +
+    return (size_t)(kMergeFloats + kWaves * 32 + 4 + 32 + kQopFloats + kScaleFloats) *
+               sizeof(float) +
            (size_t)npages * sizeof(int32_t);
 }
 
@@ -600,12 +722,20 @@ hipError_t launch_kv4_decode(hipStream_t stream, const Kv4Params& p)
 {
     const uint32_t npages = ((kWaves * p.nt * kTile - 1) >> p.block_shift) + 2;
     const dim3 grid(p.parts, p.H * p.chunks, p.T);
-    hipLaunchKernelGGL(kv4_decode_kernel, grid, dim3(kThreads), kv4_lds_bytes(npages), stream, p);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    const uint32_t rows = p.T * p.Hq;
-    hipLaunchKernelGGL(kv4_reduce_kernel, dim3((rows + kWaves - 1) / kWaves), dim3(kThreads), 0,
-                       stream, p);
+    const size_t lds = kv4_lds_bytes(npages);
+    // Four combiners per group when every workgroup of the grid is resident
+    // at once (so a combiner never waits on one that has not started), else
+    // the last ticket alone.
+    Kv4Params q = p;
+    q.combiners = 1;
+    int dev = 0, cus = 0, per_cu = 0;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kv4_decode_kernel, kThreads, lds) ==
+            hipSuccess &&
+        (uint64_t)grid.x * grid.y * grid.z <= (uint64_t)(cus > 0 ? cus : 0) * (per_cu > 0 ? per_cu : 0))
+        q.combiners = 4;
+    hipLaunchKernelGGL(kv4_decode_kernel, grid, dim3(kThreads), lds, stream, q);
     return hipGetLastError();
 }
 

@@ -78,8 +78,6 @@ constexpr float kShiftLimit = 100.0f;    // bound of the value-scale normalisati
 constexpr uint32_t kBadStrip = 0xFFFFFFFFu;
 constexpr uint32_t kFlagRotated = 1u;
 constexpr int kHdrFloats = 416;          // m_x, l_x [16][4], q_exp[16], flags, 2^-sh[4], scale slots [4][64]
-constexpr uint32_t kRecMagic = 0x7FBADBADu;  // fused records hold bits ^ kRecMagic; 0 = not written
-constexpr uint32_t kPollLimit = 1u << 20;     // bound of the combiner's record polls
 constexpr uint32_t kPersistentMaxSeqs = 4096; // the persistent kernel stages two words per sequence
 constexpr uint32_t kLptMaxSeqs = 1024;        // and a third (the last-split order) up to this many
 constexpr int kStripSlots = TQ4_MAX_SPLIT_STRIPS + 4;  // staged window rows + padding
@@ -166,62 +164,6 @@ __device__ __forceinline__ void load_row_chunk(uint32_t (&k)[D / 32], const int8
     }
 }
 
-// Record traffic between workgroups of one launch: buffer stores and loads
-// with the device-coherence bit (sc1 -- what agent-scope relaxed atomic
-// stores and loads are on gfx950), plain accesses to the compiler, so they
-// vectorise and a whole chunk of loads is in flight at once. No whole-L2
-// write-back or invalidate is needed around the arrival counter.
-
-constexpr int kCachePolicySc1 = 16;  // cache-policy operand bit of sc1
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t records_rsrc(const float* base)
-{
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), (short)0, 0x7fffffff,
-                                             0x00020000);
-}
-
-typedef uint32_t u2_t __attribute__((ext_vector_type(2)));
-
-// Stores and loads of N = 1, 2 or 4 consecutive record floats. ENC: the fused
-// encoding (bits ^ kRecMagic) and the device-coherence bit.
-template <int N, bool ENC>
-__device__ __forceinline__ void rec_store(__amdgpu_buffer_rsrc_t r, uint32_t byte_off,
-                                          const float* v)
-{
-    const uint32_t x = ENC ? kRecMagic : 0u;
-    const int pol = ENC ? kCachePolicySc1 : 0;
-    if constexpr (N == 4) {
-        const u4_t u = u4_t{__float_as_uint(v[0]) ^ x, __float_as_uint(v[1]) ^ x,
-                            __float_as_uint(v[2]) ^ x, __float_as_uint(v[3]) ^ x};
-        __builtin_amdgcn_raw_buffer_store_b128(u, r, byte_off, 0, pol);
-    } else if constexpr (N == 2) {
-        const u2_t u = u2_t{__float_as_uint(v[0]) ^ x, __float_as_uint(v[1]) ^ x};
-        __builtin_amdgcn_raw_buffer_store_b64(u, r, byte_off, 0, pol);
-    } else {
-        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v[0]) ^ x, r, byte_off, 0, pol);
-    }
-}
-
-// Raw words (still encoded when ENC).
-template <int N, bool ENC>
-__device__ __forceinline__ void rec_load(__amdgpu_buffer_rsrc_t r, uint32_t byte_off,
-                                         uint32_t* w)
-{
-    const int pol = ENC ? kCachePolicySc1 : 0;
-    if constexpr (N == 4) {
-        const u4_t u = __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, pol);
-        w[0] = u[0];
-        w[1] = u[1];
-        w[2] = u[2];
-        w[3] = u[3];
-    } else if constexpr (N == 2) {
-        const u2_t u = __builtin_amdgcn_raw_buffer_load_b64(r, byte_off, 0, pol);
-        w[0] = u[0];
-        w[1] = u[1];
-    } else {
-        w[0] = __builtin_amdgcn_raw_buffer_load_b32(r, byte_off, 0, pol);
-    }
-}
 
 // Combine layout of one wave over one (seq, q head) row: lane c = lane & 31
 // owns channels c*CC .. c*CC+CC-1 (CC = d/32); ks = lane >> 5 takes the
@@ -306,16 +248,16 @@ __device__ void combine_records(const float* rr, uint32_t K, int lane, float (&v
             // the stores complete under the arithmetic below.
 #pragma unroll
             for (int i = 0; i < NS; ++i) {
-                __builtin_amdgcn_raw_buffer_store_b64(u2_t{0u, 0u}, rsrc, roff[i], 0,
+                __builtin_amdgcn_raw_buffer_store_b64(rec_u2_t{0u, 0u}, rsrc, roff[i], 0,
                                                       kCachePolicySc1);
 #pragma unroll
                 for (int j = 0; j < CC; j += LD) {
                     const uint32_t off = roff[i] + 4u * (4 + c * CC + j);
                     if constexpr (LD == 4)
-                        __builtin_amdgcn_raw_buffer_store_b128(u4_t{0u, 0u, 0u, 0u}, rsrc, off, 0,
+                        __builtin_amdgcn_raw_buffer_store_b128(rec_u4_t{0u, 0u, 0u, 0u}, rsrc, off, 0,
                                                                kCachePolicySc1);
                     else
-                        __builtin_amdgcn_raw_buffer_store_b64(u2_t{0u, 0u}, rsrc, off, 0,
+                        __builtin_amdgcn_raw_buffer_store_b64(rec_u2_t{0u, 0u}, rsrc, off, 0,
                                                               kCachePolicySc1);
                 }
             }

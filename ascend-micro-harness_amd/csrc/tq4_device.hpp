@@ -150,4 +150,64 @@ __device__ __forceinline__ void partition(uint32_t pages, uint32_t splits, uint3
     count = remaining < width ? remaining : width;
 }
 
+// Record traffic between workgroups of one launch: buffer stores and loads
+// with the device-coherence bit (sc1 -- what agent-scope relaxed atomic
+// stores and loads are on gfx950), plain accesses to the compiler, so they
+// vectorise and a whole chunk of loads is in flight at once. No whole-L2
+// write-back or invalidate is needed around the arrival counter.
+
+constexpr int kCachePolicySc1 = 16;          // cache-policy operand bit of sc1
+constexpr uint32_t kRecMagic = 0x7FBADBADu;  // fused records hold bits ^ kRecMagic; 0 = not written
+constexpr uint32_t kPollLimit = 1u << 20;    // bound of a combiner's record polls
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t records_rsrc(const float* base)
+{
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), (short)0, 0x7fffffff,
+                                             0x00020000);
+}
+
+typedef uint32_t rec_u2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t rec_u4_t __attribute__((ext_vector_type(4)));
+
+// Stores and loads of N = 1, 2 or 4 consecutive record floats. ENC: the fused
+// encoding (bits ^ kRecMagic) and the device-coherence bit.
+template <int N, bool ENC>
+__device__ __forceinline__ void rec_store(__amdgpu_buffer_rsrc_t r, uint32_t byte_off,
+                                          const float* v)
+{
+    const uint32_t x = ENC ? kRecMagic : 0u;
+    const int pol = ENC ? kCachePolicySc1 : 0;
+    if constexpr (N == 4) {
+        const rec_u4_t u = rec_u4_t{__float_as_uint(v[0]) ^ x, __float_as_uint(v[1]) ^ x,
+                                    __float_as_uint(v[2]) ^ x, __float_as_uint(v[3]) ^ x};
+        __builtin_amdgcn_raw_buffer_store_b128(u, r, byte_off, 0, pol);
+    } else if constexpr (N == 2) {
+        const rec_u2_t u = rec_u2_t{__float_as_uint(v[0]) ^ x, __float_as_uint(v[1]) ^ x};
+        __builtin_amdgcn_raw_buffer_store_b64(u, r, byte_off, 0, pol);
+    } else {
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v[0]) ^ x, r, byte_off, 0, pol);
+    }
+}
+
+// Raw words (still encoded when ENC).
+template <int N, bool ENC>
+__device__ __forceinline__ void rec_load(__amdgpu_buffer_rsrc_t r, uint32_t byte_off,
+                                         uint32_t* w)
+{
+    const int pol = ENC ? kCachePolicySc1 : 0;
+    if constexpr (N == 4) {
+        const rec_u4_t u = __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, pol);
+        w[0] = u[0];
+        w[1] = u[1];
+        w[2] = u[2];
+        w[3] = u[3];
+    } else if constexpr (N == 2) {
+        const rec_u2_t u = __builtin_amdgcn_raw_buffer_load_b64(r, byte_off, 0, pol);
+        w[0] = u[0];
+        w[1] = u[1];
+    } else {
+        w[0] = __builtin_amdgcn_raw_buffer_load_b32(r, byte_off, 0, pol);
+    }
+}
+
 }  // namespace tq4

@@ -66,11 +66,13 @@ struct Kv4Params {
     const int32_t* context_lens;
     const float* pi_signs;
     const uint16_t* gate;
-    float* records;              // [T][Hq][parts][260]
+    float* records;              // [T][Hq][parts][260], zero between calls
+    uint32_t* counters;          // [T][H][chunks] part tickets, zero between calls
     uint16_t* out;
     uint32_t T, Hq, H, G, chunks, block_shift, max_blocks, num_blocks, parts, nt;
     float score_scale, inv_gain, inv_sqrt_len;
     uint32_t stage, element;
+    uint32_t combiners;          // set by launch_kv4_decode
 };
 hipError_t launch_kv4_decode(hipStream_t stream, const Kv4Params& p);
 hipError_t launch_fp8_probe(hipStream_t stream, const float* in, uint16_t* out, uint32_t n);

@@ -209,14 +209,15 @@ def _(query, pi_signs, gate, query_rot, key_cache, value_cache, scale_cache, blo
 
 def kv4fp8_workspace_for(query: torch.Tensor, num_kv_heads: int, block_tables: torch.Tensor,
                          block_size: int, num_blocks: int = 1) -> torch.Tensor:
-    """A workspace for tq4::fused_decode_opt(_raw_query) at this geometry."""
+    """A zeroed workspace for tq4::fused_decode_opt(_raw_query) at this
+    geometry (every call leaves it zero again, so it can be reused)."""
     T, Hq, d = query.shape
     L = _tq4.fused_decode_opt_launch(T, Hq, num_kv_heads, block_size, block_tables.shape[1],
                                      num_blocks=max(1, num_blocks))
     n = _tq4.kv4fp8_workspace_bytes(L)
     if n == 0:
         raise ValueError("kv4fp8_workspace_for: unsupported geometry")
-    return torch.empty(n, dtype=torch.uint8, device=query.device)
+    return torch.zeros(n, dtype=torch.uint8, device=query.device)
 
 
 def workspace_for(query: torch.Tensor, num_kv_heads: int, block_tables: torch.Tensor,

@@ -92,6 +92,8 @@ def lib():
     L.tq4_kv4fp8_decode.argtypes = [_P, _P, _P]
     L.tq4_kv4fp8_decode_raw_query.restype = _I32
     L.tq4_kv4fp8_decode_raw_query.argtypes = [_P, _P, _P]
+    L.tq4_kv4fp8_workspace_init.restype = _I32
+    L.tq4_kv4fp8_workspace_init.argtypes = [_P, _P, C.c_uint64]
     L.tq4_fp8_e4m3_round.restype = _I32
     L.tq4_fp8_e4m3_round.argtypes = [_P, _P, _P, C.c_uint64]
     _lib = L
@@ -329,7 +331,8 @@ __all__ = [
     "paged_decode", "paged_decode_partials", "splitk_combine", "icdf_quantize",
     "lloydmax_quantize", "TQ4_DECODE_QUERY_ROTATED", "TQ4_MAX_SPLITS",
     "Kv4Fp8Launch", "Kv4Fp8Buffers", "Kv4Fp8RawQueryBuffers", "fused_decode_opt_launch",
-    "kv4fp8_workspace_bytes", "kv4fp8_decode", "kv4fp8_decode_raw_query", "fp8_e4m3_round",
+    "kv4fp8_workspace_bytes", "kv4fp8_workspace_init", "kv4fp8_decode", "kv4fp8_decode_raw_query",
+    "fp8_e4m3_round",
 ]
 
 
@@ -387,14 +390,24 @@ def kv4fp8_workspace_bytes(launch):
     return int(lib().tq4_kv4fp8_workspace_bytes(C.byref(launch)))
 
 
+def kv4fp8_workspace_init(workspace, stream=None):
+    """Zero a KV4/FP8 decode workspace (tq4_kv4fp8_workspace_init): needed
+    once before its first call; every call leaves it zero again."""
+    _dev(workspace, "workspace")
+    _check(lib().tq4_kv4fp8_workspace_init(_stream(stream), _ptr(workspace),
+                                           workspace.numel() * workspace.element_size()),
+           "kv4fp8_workspace_init")
+    return workspace
+
+
 def _kv4_prepare(launch, tensors, workspace, device, stream):
     for name, t in tensors:
         _dev(t, name)
     need = kv4fp8_workspace_bytes(launch)
     if need == 0:
         raise ValueError("kv4fp8 decode: unsupported geometry")
-    if workspace is None:
-        workspace = torch.empty(need, dtype=torch.uint8, device=device)
+    if workspace is None:  # a zeroed one for this call
+        workspace = torch.zeros(need, dtype=torch.uint8, device=device)
     launch.workspace_bytes = workspace.numel() * workspace.element_size()
     return workspace
 

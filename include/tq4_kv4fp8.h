@@ -89,10 +89,18 @@ typedef struct tq4_kv4fp8_raw_query_buffers {
     tq4_kv4fp8_buffers decode;
 } tq4_kv4fp8_raw_query_buffers;
 
-/* Workspace this decode needs for `launch` (bytes, 256-aligned): the partial
- * records of every (token, q head, part). No initialisation is needed;
- * calls that overlap in time need their own workspaces. */
+/* Workspace this decode needs for `launch` (bytes, 256-aligned): a part
+ * ticket per (token, kv head, 16-head chunk) and the partial records of every
+ * (token, q head, part). It must be zero before its first call
+ * (tq4_kv4fp8_workspace_init); every call leaves it zero again, so one
+ * workspace serves calls of any geometry it is large enough for. Calls that
+ * overlap in time need their own workspaces. */
 uint64_t tq4_kv4fp8_workspace_bytes(const tq4_kv4fp8_launch* launch);
+
+/* Zero a workspace on `stream` (a fill kernel, so it may be captured in a
+ * graph). workspace 16-byte aligned. No reference counterpart: the
+ * reference's host code allocates its workspace per call. */
+int tq4_kv4fp8_workspace_init(void* stream, void* workspace, uint64_t workspace_bytes);
 
 /* The pre-rotated entry (launch_fused_decode_opt): output_stage is not read. */
 int tq4_kv4fp8_decode(void* stream, const tq4_kv4fp8_launch* launch,

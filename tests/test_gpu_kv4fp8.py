@@ -174,6 +174,28 @@ def test_random_against_oracle(tq4, oracle, case, element):
     assert np.all(bits(out)[zero_rows] == 0)
 
 
+def test_grid_beyond_resident_workgroups(tq4, oracle):
+    """75 tokens x 4 KV heads x 2 parts = 600 workgroups, more than two per
+    CU: one combiner per group (the last ticket), which waits only on parts
+    that are already running. Two calls on one workspace agree bit for bit."""
+    rng = np.random.default_rng(31)
+    T, H, G, S = 75, 4, 16, 64
+    ctx = [int(c) for c in rng.integers(300, 1500, T)]
+    P = sum((c + S - 1) // S for c in ctx) + 4
+    q, key, val, sc, tb, ln = random_case(rng, T, H, G, S, P, ctx, key_scale=(0.5, 2.0))
+    kw = dict(heads=H * G, kv_heads=H, block_size=S, max_blocks=tb.shape[1], num_blocks=P)
+    _, want = oracle.kv4fp8_decode(q, key, val, sc, tb, ln, **kw)
+    L = tq4.fused_decode_opt_launch(T, H * G, H, S, tb.shape[1], num_blocks=P)
+    ws = tq4.kv4fp8_workspace_init(
+        torch.empty(tq4.kv4fp8_workspace_bytes(L), dtype=torch.uint8, device=DEV))
+    args = (dev(q), dev(key), dev(val), dev(sc), dev(tb), dev(ln), H, S, P)
+    first = bits(tq4.kv4fp8_decode(*args, workspace=ws)).copy()
+    mx, mr = compare(first, want, 0)
+    assert mx <= 2e-2 and mr <= 1e-3, (mx, mr)
+    assert np.array_equal(bits(tq4.kv4fp8_decode(*args, workspace=ws)), first)
+    assert not torch.any(ws)  # tickets and records are zero again
+
+
 def test_unmapped_pages_and_poisoned_tail_rows(tq4, oracle):
     rng = np.random.default_rng(9)
     T, H, G, S = 2, 2, 8, 64
@@ -226,10 +248,10 @@ def test_bench_size_properties(tq4):
 
 
 def test_workspace_reuse_and_graph_replays(tq4):
-    """The part tickets return to zero after every call: one workspace serves
-    repeated eager calls and HIP graph replays (eager work and synchronisations
-    in between), every result bit-identical; a second geometry on the same
-    workspace too."""
+    """The part tickets and records return to zero after every call: one
+    workspace serves repeated eager calls and HIP graph replays (eager work
+    and synchronisations in between), every result bit-identical; a second
+    geometry on the same workspace too."""
     rng = np.random.default_rng(21)
     T, H, G, S = 3, 2, 16, 64
     ctx = [900, 1, 2000]
@@ -264,3 +286,4 @@ def test_workspace_reuse_and_graph_replays(tq4):
     b = bits(tq4.kv4fp8_decode(dev(q2), dev(k2), dev(v2), dev(s2), dev(t2), dev(l2), 1, 128, 40))
     assert np.array_equal(a, b)
     assert np.array_equal(bits(call()), first)
+    assert not torch.any(ws)  # tickets and records are zero again
