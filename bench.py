@@ -366,7 +366,11 @@ def extra_workloads(tq4, torch, dev, w, cpu=True):
     kn = torch.randn((bsz, HKV, D), generator=gen, device=dev).to(torch.bfloat16)
     vn = torch.randn((bsz, HKV, D), generator=gen, device=dev).to(torch.bfloat16)
     out5 = torch.empty_like(q5)
-    k5 = tq4.auto_splits(bsz, HKV, maxb, S)
+    # configs[4] asks for a split-K decode. tq4_decode_auto_splits picks one
+    # split here (its rule knows the batch's longest context, not the spread);
+    # three splits, with the persistent kernel ordering the last splits
+    # longest first, measured best for this batch (K = 1..8 sweep).
+    k5 = 3
     ws5 = tq4.decode_workspace(bsz, HQ, HKV, D, k5)
 
     def step():
