@@ -244,6 +244,22 @@ __device__ __forceinline__ void combine_polled(const Kv4Params& p, uint32_t row,
     run_sum = 0.0f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) x[i] = 0.0f;
+    // zero a batch's records for the next call
+    auto zero_batch = [&](uint32_t k0) {
+#pragma unroll
+        for (int j = 0; j < kPollBatch; ++j) {
+            const uint32_t k = k0 + j;
+            if (k < live && k != own) {
+                __builtin_amdgcn_raw_buffer_store_b128(rec_u4_t{0u, 0u, 0u, 0u}, rs,
+                                                       k * kRecBytes + 16u * lane, 0,
+                                                       kCachePolicySc1);
+                if (lane == 0)
+                    __builtin_amdgcn_raw_buffer_store_b64(rec_u2_t{0u, 0u}, rs,
+                                                          k * kRecBytes + 4u * kD, 0,
+                                                          kCachePolicySc1);
+            }
+        }
+    };
     for (uint32_t k0 = 0; k0 < live; k0 += kPollBatch) {
         uint32_t aw[kPollBatch][4], hw[kPollBatch][2];
         for (uint32_t it = 0;; ++it) {
@@ -266,19 +282,9 @@ __device__ __forceinline__ void combine_polled(const Kv4Params& p, uint32_t row,
             }
             if (!__any(mn == 0u) || it + 1 >= kPollLimit) break;
         }
-#pragma unroll
-        for (int j = 0; j < kPollBatch; ++j) {
-            const uint32_t k = k0 + j;
-            if (k < live && k != own) {
-                __builtin_amdgcn_raw_buffer_store_b128(rec_u4_t{0u, 0u, 0u, 0u}, rs,
-                                                       k * kRecBytes + 16u * lane, 0,
-                                                       kCachePolicySc1);
-                if (lane == 0)
-                    __builtin_amdgcn_raw_buffer_store_b64(rec_u2_t{0u, 0u}, rs,
-                                                          k * kRecBytes + 4u * kD, 0,
-                                                          kCachePolicySc1);
-            }
-        }
+        // the last batch is zeroed at once, earlier ones after the loop (a
+        // later batch's poll would wait for their write acknowledgements)
+        if (k0 + kPollBatch >= live) zero_batch(k0);
 #pragma unroll
         for (int j = 0; j < kPollBatch; ++j) {
             const uint32_t k = k0 + j;
@@ -300,6 +306,7 @@ __device__ __forceinline__ void combine_polled(const Kv4Params& p, uint32_t row,
             merge_record(run_max, run_sum, x, m, l, a);
         }
     }
+    for (uint32_t k0 = 0; k0 + kPollBatch < live; k0 += kPollBatch) zero_batch(k0);
 }
 
 // Two waves per SIMD (248 registers): one wave's VALU and MFMA work overlaps

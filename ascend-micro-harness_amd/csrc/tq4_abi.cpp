@@ -147,22 +147,34 @@ size_t tq4_decode_workspace_bytes(uint32_t num_seqs, uint32_t num_heads, uint32_
 uint32_t tq4_decode_auto_splits(uint32_t num_seqs, uint32_t num_kv_heads,
                                 uint32_t max_blocks_per_seq, uint32_t block_size)
 {
-    // Enough workgroups to fill every CU's two slots (256 CUs), and splits of
-    // at most ~512 strips; never fewer than 16 strips per split, and at most
-    // 64 splits (one to four record chunks per combine). Each extra item
-    // costs a table and a first-strip round trip, a merge and a record, and
-    // the persistent kernel orders the last splits longest first, so a batch
-    // that already fills the slots runs best with few, long items: on
-    // 64-sequence batches (8 KV heads) K = 1 beat K = 2 by 20 % at ctx 4096,
-    // and a spread of 1..32768 tokens wanted K = 4..8.
+    // Workgroups for half the CUs (256), and for all their two slots when
+    // the splits would still be long (> 64 strips); splits of at most ~512
+    // strips; never fewer than 16 strips per split, and at most 32 splits.
+    // - Each extra item costs a table and a first-strip round trip, a merge
+    //   and a record, and the persistent kernel orders the last splits
+    //   longest first, so a batch that already fills the slots runs best
+    //   with few, long items: 64 sequences x 8 KV heads, K = 1 beat K = 2 by
+    //   20 % at ctx 4096; a spread of 1..32768 tokens wanted K = 4..8.
+    // - One sequence (8 KV heads): K = 16 was best from ctx 2048 to 16384,
+    //   K = 32 at 32768 and 65536.
+    // - More than 32 splits combine in two record chunks and measured 5-7 us
+    //   slower than 32 at d = 128.
     const uint64_t strips = (uint64_t)max_blocks_per_seq * (block_size / kStrip);
-    const uint64_t items = (uint64_t)num_seqs * num_kv_heads;
-    uint64_t k = (strips + 511) / 512;
-    const uint64_t fill = items == 0 ? 1 : (512 + items - 1) / items;
-    if (k < fill) k = fill;
+    const uint64_t items = (uint64_t)num_seqs * num_kv_heads > 0
+                               ? (uint64_t)num_seqs * num_kv_heads
+                               : 1;
+    uint64_t k = (128 + items - 1) / items;
+    if (strips > 64 * k) {
+        uint64_t more = (512 + items - 1) / items;
+        const uint64_t by_work = (strips + 63) / 64;
+        if (more > by_work) more = by_work;
+        if (k < more) k = more;
+    }
+    const uint64_t k_len = (strips + 511) / 512;
+    if (k < k_len) k = k_len;
     const uint64_t by_len = strips / 16 > 0 ? strips / 16 : 1;
     if (k > by_len) k = by_len;
-    if (k > 64) k = 64;
+    if (k > 32) k = 32;
     // one split stages at most TQ4_MAX_SPLIT_STRIPS strips of its window
     const uint64_t k_min = (strips + TQ4_MAX_SPLIT_STRIPS - 1) / TQ4_MAX_SPLIT_STRIPS;
     if (k < k_min) k = k_min;

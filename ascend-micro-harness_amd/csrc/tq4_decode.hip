@@ -196,6 +196,27 @@ __device__ void combine_records(const float* rr, uint32_t K, int lane, float (&v
     uint32_t oh[2] = {0u, 0u}, oa[CC];
 #pragma unroll
     for (int j = 0; j < CC; ++j) a[j] = 0.0f, oa[j] = 0u;
+    // Zero a chunk's records, so the next call starts from "not written"
+    // (slots past K zero split K-1 again).
+    auto zero_chunk = [&](uint32_t k0) {
+#pragma unroll
+        for (int i = 0; i < NS; ++i) {
+            const uint32_t k = k0 + ks + 2 * i;
+            const uint32_t off0 = (k < K ? k : K - 1) * RS * 4u;
+            __builtin_amdgcn_raw_buffer_store_b64(rec_u2_t{0u, 0u}, rsrc, off0, 0,
+                                                  kCachePolicySc1);
+#pragma unroll
+            for (int j = 0; j < CC; j += LD) {
+                const uint32_t off = off0 + 4u * (4 + c * CC + j);
+                if constexpr (LD == 4)
+                    __builtin_amdgcn_raw_buffer_store_b128(rec_u4_t{0u, 0u, 0u, 0u}, rsrc, off,
+                                                           0, kCachePolicySc1);
+                else
+                    __builtin_amdgcn_raw_buffer_store_b64(rec_u2_t{0u, 0u}, rsrc, off, 0,
+                                                          kCachePolicySc1);
+            }
+        }
+    };
     for (uint32_t k0 = 0; k0 < K; k0 += 2 * NS) {
         uint32_t roff[NS];
         bool vi[NS];
@@ -242,25 +263,12 @@ __device__ void combine_records(const float* rr, uint32_t K, int lane, float (&v
             }
             if (!__any(mn == 0u) || it + 1 >= kPollLimit) break;
         }
+        // The last chunk's records are zeroed at once (the stores complete
+        // under the arithmetic below); earlier chunks' after the loop, since
+        // the next chunk's poll would otherwise wait for their write
+        // acknowledgements (stores and loads share one counter).
         if constexpr (FUSED) {
-            // Zero what was consumed, so the next call starts from "not
-            // written" (slots past K zero split K-1 again). Issued at once:
-            // the stores complete under the arithmetic below.
-#pragma unroll
-            for (int i = 0; i < NS; ++i) {
-                __builtin_amdgcn_raw_buffer_store_b64(rec_u2_t{0u, 0u}, rsrc, roff[i], 0,
-                                                      kCachePolicySc1);
-#pragma unroll
-                for (int j = 0; j < CC; j += LD) {
-                    const uint32_t off = roff[i] + 4u * (4 + c * CC + j);
-                    if constexpr (LD == 4)
-                        __builtin_amdgcn_raw_buffer_store_b128(rec_u4_t{0u, 0u, 0u, 0u}, rsrc, off, 0,
-                                                               kCachePolicySc1);
-                    else
-                        __builtin_amdgcn_raw_buffer_store_b64(rec_u2_t{0u, 0u}, rsrc, off, 0,
-                                                              kCachePolicySc1);
-                }
-            }
+            if (k0 + 2 * NS >= K) zero_chunk(k0);
         }
         float mk[NS], Mc = -INFINITY;
 #pragma unroll
@@ -284,6 +292,9 @@ __device__ void combine_records(const float* rr, uint32_t K, int lane, float (&v
         }
         L = L * sc + (lw + xor_lanes(lw, 32));
         M = Mn;
+    }
+    if constexpr (FUSED) {
+        for (uint32_t k0 = 0; k0 + 2 * NS < K; k0 += 2 * NS) zero_chunk(k0);
     }
     // the two split parities
 #pragma unroll

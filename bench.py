@@ -17,9 +17,12 @@ launch stream bracket the replays, so ms_per_step is the average launch
 duration including the dispatch gap between consecutive kernels.
 
 Also reported: reshape_and_cache tokens/s on BASELINE configs[1] (1024 BF16
-tokens into a 4096-page pool, seeded page permutation), the batched decode
-step of configs[4] (64 sequences, ctx ~U[512, 8192]), and the CPU baseline:
-the C oracle's decode of the same sequence on the host cores (kind "port").
+tokens into a 4096-page pool, seeded page permutation; and the same tokens at
+token-granular slots through the scatter writer), the configs[0] A8 strip,
+the configs[3] split sweep (ctx 4096 / 16384 / 32768 x 2..16 splits, ragged
+4103), the batched decode step of configs[4] (64 sequences, ctx ~U[512,
+8192]), and the CPU baseline: the C oracle's decode of the same sequence on
+the host cores (kind "port"), on all of them and on one.
 
 Usage:
   python bench.py [--gpus 1] [--steps K] [--warmup W]
@@ -310,7 +313,9 @@ def main():
 
 
 def extra_workloads(tq4, torch, dev, w, cpu=True):
-    """reshape_and_cache tokens/s and the batched step."""
+    """reshape_and_cache tokens/s (configs[1], and its scatter variant), the A8
+    strip, the split sweep, the batched step
+    (configs[4]), the codebook leaves and the KV4/FP8 decode."""
     out = {}
     rng = np.random.default_rng(0x71340002)
     gen = torch.Generator(device=dev)
@@ -340,6 +345,54 @@ def extra_workloads(tq4, torch, dev, w, cpu=True):
                                 "GBps": round(wbytes / (wms * 1e-3) / 1e9, 2),
                                 "algorithmic_bytes": wbytes}
     log(f"reshape_and_cache: {wms * 1e3:.2f} us -> {wt / (wms * 1e-3) / 1e6:.1f} M tokens/s")
+
+    # --- configs[1], secondary: the same 1024 tokens at token-granular slots
+    # (the first 1024 of a permutation of the pool's 65536 slots) through the
+    # scatter writer, which merges each token into its value strip (RMW)
+    sins = []
+    for i in range(nin):
+        k, v, _ = ins[i]
+        sl = torch.from_numpy(rng.permutation(pool * S)[:wt].astype(np.int32)).to(dev)
+        sins.append((k, v, sl))
+
+    def scatter(i):
+        k, v, sl = sins[i]
+        tq4.reshape_scatter(k, v, wkc, wvc, wsc, sl, w.signs, num_blocks=pool, block_size=S,
+                            inv_sqrt_len=w.isl)
+
+    sms_, _, _ = graph_time(torch, [lambda i=i: scatter(i) for i in range(nin)], 512, 64)
+    sbytes_ = wbytes + wt * HKV * 2 * (D * S // 2)  # + the value-strip read and write-back
+    out["reshape_scatter"] = {"workload": "configs[1] secondary: 1024 BF16 tokens at permuted "
+                                          "slots (value-strip RMW)", "us": round(sms_ * 1e3, 3),
+                              "tokens_per_s": round(wt / (sms_ * 1e-3), 1),
+                              "GBps": round(sbytes_ / (sms_ * 1e-3) / 1e9, 2),
+                              "algorithmic_bytes": sbytes_}
+    log(f"reshape_scatter: {sms_ * 1e3:.2f} us -> {wt / (sms_ * 1e-3) / 1e6:.1f} M tokens/s")
+
+    # --- one 16-token A8 strip, uniform ints in [-127, 127], slot = identity
+    # into page 0 (latency-bound: one strip x 8 heads)
+    a8 = [(torch.randint(-127, 128, (S, HKV, D), dtype=torch.int8, device=dev, generator=gen),
+           torch.randint(-127, 128, (S, HKV, D), dtype=torch.int8, device=dev, generator=gen))
+          for _ in range(8)]
+    ident = torch.arange(S, dtype=torch.int32, device=dev)
+
+    def write_a8(i):
+        k, v = a8[i]
+        tq4.reshape_and_cache_a8(k, v, wkc, wvc, wsc, ident, pi_signs=w.signs, num_blocks=pool,
+                                 block_size=S, inv_sqrt_len=w.isl)
+
+    ams, _, _ = graph_time(torch, [lambda i=i: write_a8(i) for i in range(8)], 512, 64)
+    abytes = writer_algorithmic_bytes(S, HKV, D, 1)
+    out["reshape_and_cache_a8"] = {"workload": "configs[0] A8, one 16-token strip",
+                                   "us": round(ams * 1e3, 3),
+                                   "tokens_per_s": round(S / (ams * 1e-3), 1),
+                                   "algorithmic_bytes": abytes}
+    log(f"reshape_and_cache A8 strip: {ams * 1e3:.2f} us")
+
+    # --- split sweep. Sequences at ctx 4096 / 16384 / 32768 (and
+    # the ragged 4096 + 7) over random pages of the headline pool; each time
+    # rotates over enough sequences that >= 512 MB are read between re-reads.
+    out["split_sweep"] = split_sweep(tq4, torch, dev, w)
 
     # --- batched decode step, 64 sequences, ctx ~U[512, 8192]
     r = np.random.default_rng(0x71340005)
@@ -481,6 +534,57 @@ def kv4fp8_workloads(tq4, torch, dev, cpu=True):
     return res
 
 
+def split_sweep(tq4, torch, dev, w):
+    """the fused decode at ctx {4096, 16384, 32768} x K {2, 4, 8,
+    16, auto}, plus the ragged ctx 4103 at auto."""
+    rng = np.random.default_rng(0x71340004)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0x71340004)
+    rows = []
+    for ctx, ks in ((4096, (2, 4, 8, 16, 0)), (16384, (2, 4, 8, 16, 0)),
+                    (32768, (2, 4, 8, 16, 0)), (4103, (0,))):
+        pages = (ctx + S - 1) // S
+        nseq = max(4, (512 << 20) // (ctx * HKV * (D + 8)))
+        tabs = [torch.from_numpy(rng.permutation(w.pool)[:pages].astype(np.int32)[None, :]).to(dev)
+                for _ in range(nseq)]
+        qs = [torch.randn((1, HQ, D), generator=gen, device=dev).to(torch.bfloat16)
+              for _ in range(nseq)]
+        ctx_t = torch.tensor([ctx], dtype=torch.int32, device=dev)
+        out = torch.empty((1, HQ, D), dtype=torch.bfloat16, device=dev)
+        nbytes = decode_algorithmic_bytes([ctx], HQ, HKV, D, S)
+        for k in ks:
+            kk = k or tq4.auto_splits(1, HKV, pages, S)
+            ws = tq4.decode_workspace(1, HQ, HKV, D, kk)
+
+            def dec(i, kk=kk, ws=ws):
+                tq4.paged_decode(qs[i], w.kc, w.vc, w.sc, tabs[i], ctx_t, w.signs, HKV, S, w.pool,
+                                 out=out, workspace=ws, num_splits=kk, scale=w.scale,
+                                 inv_sqrt_len=w.isl)
+
+            ms, _, _ = graph_time(torch, [lambda i=i: dec(i) for i in range(nseq)],
+                                  max(256, nseq), max(32, nseq))
+            gbs = nbytes / (ms * 1e-3) / 1e9
+            rows.append({"ctx": ctx, "splits": kk, "auto": k == 0, "us": round(ms * 1e3, 2),
+                         "GBps": round(gbs, 1),
+                         "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
+                         "algorithmic_bytes": nbytes})
+            log(f"split sweep ctx {ctx} K {kk}{' (auto)' if k == 0 else ''}: "
+                f"{ms * 1e3:.2f} us -> {gbs:.0f} GB/s")
+    return {"workload": "configs[3] single-sequence decode, 32q:8kv, d128, page 16, cold "
+                        "(rotated sequences)", "rows": rows}
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
 def cpu_baseline(torch, w, dec_bytes, seconds):
     """The C oracle's decode of slice 0 on the host cores, bounded in time."""
     sys.path.insert(0, os.path.join(REPO, "tests"))
@@ -490,20 +594,33 @@ def cpu_baseline(torch, w, dec_bytes, seconds):
     h_q = w.q[0].view(torch.int16).cpu().numpy().view(np.uint16)
     h_kc, h_vc, h_sc = w.kc.cpu().numpy(), w.vc.cpu().numpy(), w.sc.cpu().numpy()
     h_tab, h_ctx = w.tables[0].cpu().numpy(), w.ctx.cpu().numpy()
-    iters, t0 = 0, time.perf_counter()
-    while True:
-        o.paged_decode(h_q, h_kc, h_vc, h_sc, h_tab, h_ctx, w.signs_np, None, HQ, HKV, D, S,
-                       w.pool, w.splits, np.float32(w.scale), np.float32(w.isl), 1,
-                       threads=threads)
-        iters += 1
-        el = time.perf_counter() - t0
-        if el >= seconds:
-            break
+
+    def timed(nthreads, budget):
+        iters, t0 = 0, time.perf_counter()
+        while True:
+            o.paged_decode(h_q, h_kc, h_vc, h_sc, h_tab, h_ctx, w.signs_np, None, HQ, HKV, D, S,
+                           w.pool, w.splits, np.float32(w.scale), np.float32(w.isl), 1,
+                           threads=nthreads)
+            iters += 1
+            el = time.perf_counter() - t0
+            if el >= budget:
+                return iters, el
+
+    iters1, el1 = timed(1, seconds / 2)
+    iters, el = timed(threads, seconds)
+    try:
+        nproc = len(os.sched_getaffinity(0))
+    except AttributeError:
+        nproc = os.cpu_count()
     return {"value": round(dec_bytes * iters / el / 1e9, 4), "unit": "GB/s", "cores": threads,
             "kind": "port",
             "sample": f"{iters} configs[2] decodes (B=1, 32q:8kv, d128, ctx4096, {w.splits} "
                       f"splits) by oracle/tq4_oracle.c in {el:.1f} s on {threads} threads",
-            "us_per_decode": round(el / iters * 1e6, 1)}
+            "us_per_decode": round(el / iters * 1e6, 1),
+            "single_thread": {"value": round(dec_bytes * iters1 / el1 / 1e9, 4), "unit": "GB/s",
+                              "us_per_decode": round(el1 / iters1 * 1e6, 1),
+                              "sample": f"{iters1} decodes in {el1:.1f} s on 1 thread"},
+            "nproc": nproc, "cpu_model": cpu_model()}
 
 
 if __name__ == "__main__":
