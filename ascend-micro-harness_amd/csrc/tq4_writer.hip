@@ -353,6 +353,91 @@ __global__ __launch_bounds__(kWriterThreads) void scatter_writer(
     }
 }
 
+// One-token requests (cu_seqlens NULL: the decode step's writer). A 16-lane
+// row group takes one (token, kv head) item, sixteen items per workgroup;
+// each lane rotates and quantises its channels of both planes. The value
+// strip's column is merged in registers: a lane reads the 2 CPL consecutive
+// strip words of its channels (channel c's 16 tokens are words 2c and
+// 2c + 1), replaces its nibble in each and writes the words back. A strip
+// has one owner per launch (the writer's contract), so writing back the
+// words read is safe. The rows' loads go out with the slot's; the strip's
+// load follows the slot.
+template <int D>
+__global__ __launch_bounds__(kWriterThreads) void scatter_token_writer(
+    const uint16_t* __restrict__ key, const uint16_t* __restrict__ value,
+    int8_t* __restrict__ key_cache, int8_t* __restrict__ value_cache,
+    float* __restrict__ scale_cache, const int32_t* __restrict__ slots,
+    const float* __restrict__ pi_signs, int32_t* __restrict__ probe, uint32_t probe_grid,
+    uint32_t num_requests, uint32_t H, uint32_t S, uint32_t P, uint32_t item_begin,
+    uint32_t item_count, float inv_sqrt_len)
+{
+    constexpr int CPL = D / 16;
+    constexpr int NW = 2 * CPL;  // strip words of a lane's channels
+    const int tid = threadIdx.x;
+    const int grp = tid >> 4;
+    const int lane_in_row = tid & 15;
+
+    if (probe != nullptr && blockIdx.x == 0 && tid < 32) {
+        const int32_t fields[4] = {0, (int32_t)probe_grid, 1, (int32_t)item_count};
+        probe[tid] = fields[tid >> 3];
+    }
+
+    float sign[CPL];
+    load_signs<CPL>(pi_signs, nullptr, 0, lane_in_row * CPL, sign);
+    const uint64_t item_end = (uint64_t)item_begin + item_count;
+    for (uint64_t item = (uint64_t)item_begin + (uint64_t)blockIdx.x * 16u + (uint32_t)grp;
+         item < item_end; item += (uint64_t)gridDim.x * 16u) {
+        const uint32_t request = (uint32_t)(item / H);
+        const uint32_t head = (uint32_t)(item % H);
+        if (request >= num_requests) continue;
+        // The rows do not depend on the slot: their loads go out with its
+        // load. A pad or out-of-pool slot reads page 0's strip and stores
+        // nothing (so no load waits behind a branch).
+        const size_t src_off = ((size_t)request * H + head) * D + lane_in_row * CPL;
+        const int32_t slot = slots[request];
+        float kx[CPL], vx[CPL];
+        load_row<CPL>(key + src_off, kx);
+        load_row<CPL>(value + src_off, vx);
+        const bool ok = slot >= 0 && (uint32_t)slot / S < P;
+        const uint32_t page = ok ? (uint32_t)slot / S : 0u;
+        const uint32_t tip = ok ? (uint32_t)slot % S : 0u;
+        const uint32_t col = tip % kStrip;
+        const size_t head_base = ((size_t)page * H + head) * S;
+        uint4* strip = (uint4*)(value_cache + (head_base + (tip - col)) * (D / 2)) +
+                       lane_in_row * (NW / 4);
+        uint32_t w[NW];
+#pragma unroll
+        for (int i = 0; i < NW / 4; ++i) {
+            const uint4 u = strip[i];
+            w[4 * i] = u.x;
+            w[4 * i + 1] = u.y;
+            w[4 * i + 2] = u.z;
+            w[4 * i + 3] = u.w;
+        }
+        int qk[CPL], qv[CPL];
+        const float sk = rotate_quantise<D, CPL>(kx, sign, lane_in_row, inv_sqrt_len,
+                                                 kPolicyExact, qk);
+        const float sv = rotate_quantise<D, CPL>(vx, sign, lane_in_row, inv_sqrt_len,
+                                                 kPolicyExact, qv);
+        if (!ok) continue;
+        if (lane_in_row == 0) {
+            scale_cache[((size_t)page * H + head) * S + tip] = sk;
+            scale_cache[(((size_t)P + page) * H + head) * S + tip] = sv;
+        }
+        store_key_codes<CPL>(key_cache + (head_base + tip) * (D / 2) + lane_in_row * (CPL / 2),
+                             qk);
+        const uint32_t sh = 4u * (col & 7u), half = col >> 3;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+            uint32_t& x = w[2 * j + half];
+            x = (x & ~(0xfu << sh)) | (((uint32_t)qv[j] & 0xfu) << sh);
+        }
+#pragma unroll
+        for (int i = 0; i < NW / 4; ++i)
+            strip[i] = make_uint4(w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]);
+    }
+}
+
 }  // namespace
 
 // ------------------------------------------------------------- launchers
@@ -404,12 +489,23 @@ hipError_t launch_scatter_writer(hipStream_t stream, uint32_t grid, const uint16
                                  uint32_t H, uint32_t D, uint32_t S, uint32_t P,
                                  uint32_t item_begin, uint32_t item_count, float inv_sqrt_len)
 {
+    // one-token requests: sixteen items per workgroup, a grid covering them
+    // (at most 4096 workgroups, striding beyond); `grid` is still what the
+    // launch probe reports
+    const uint64_t groups = ((uint64_t)item_count + 15) / 16;
+    const uint32_t tgrid = (uint32_t)(groups < 4096 ? groups : 4096);
 #define TQ4_SCATTER_CASE(DD)                                                                      \
     if (D == DD) {                                                                                \
-        hipLaunchKernelGGL((scatter_writer<DD>), dim3(grid), dim3(kWriterThreads), 0, stream,    \
-                           key, value, key_cache, value_cache, scale_cache, slots, pi_signs,      \
-                           cu_seqlens, probe, num_requests, H, S, P, item_begin, item_count,      \
-                           inv_sqrt_len);                                                         \
+        if (cu_seqlens == nullptr)                                                                \
+            hipLaunchKernelGGL((scatter_token_writer<DD>), dim3(tgrid), dim3(kWriterThreads), 0, \
+                               stream, key, value, key_cache, value_cache, scale_cache, slots,    \
+                               pi_signs, probe, grid, num_requests, H, S, P, item_begin,          \
+                               item_count, inv_sqrt_len);                                         \
+        else                                                                                      \
+            hipLaunchKernelGGL((scatter_writer<DD>), dim3(grid), dim3(kWriterThreads), 0, stream, \
+                               key, value, key_cache, value_cache, scale_cache, slots, pi_signs,  \
+                               cu_seqlens, probe, num_requests, H, S, P, item_begin, item_count,  \
+                               inv_sqrt_len);                                                     \
         return hipGetLastError();                                                                 \
     }
     TQ4_SCATTER_CASE(64)
