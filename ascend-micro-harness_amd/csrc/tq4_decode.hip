@@ -1005,10 +1005,11 @@ void decode_persistent_kernel(DecodeParams p)
     const uint32_t width = (p.max_blocks + p.K - 1) / p.K;
     const uint64_t capacity = (uint64_t)p.max_blocks * p.S;
     for (uint32_t s = tid; s < p.B; s += kThreads) {
+        // 32-bit arithmetic: a context length is below 2^31
         const int32_t c = p.context_lens[s];
-        uint64_t ctx = c < 0 ? 0u : (uint64_t)c;
-        if (ctx > capacity) ctx = capacity;
-        const uint32_t pages = (uint32_t)((ctx + p.S - 1) / p.S);
+        uint32_t ctx = c < 0 ? 0u : (uint32_t)c;
+        if (ctx > capacity) ctx = (uint32_t)capacity;
+        const uint32_t pages = (ctx + p.S - 1) / p.S;
         uint32_t kl = (pages + width - 1) / width;
         kl = kl > 0 ? kl : 1u;
         splits[s] = kl;
@@ -1020,15 +1021,32 @@ void decode_persistent_kernel(DecodeParams p)
     // lower index, come before it (a stable descending sort; every
     // workgroup derives the same order). Kept in registers until all keys
     // are read.
+    // Up to 64 sequences, the four waves each count over a quarter of the
+    // keys (partial ranks in the free q staging region, summed at placing).
     constexpr int kRanks = kLptMaxSeqs / kThreads;
     uint32_t rank[kRanks];
-    if (lpt) {
+    uint32_t* part_rank = (uint32_t*)(smem + kHdrFloats + kStripSlots);  // [4][64]
+    if (lpt && p.B <= 64) {
+        const uint32_t s = tid & 63, part = tid >> 6;
+        uint32_t r = 0;
+        if (s < p.B) {
+            const uint32_t key = order[s];
+            const uint32_t t1 = min(part * 16 + 16, p.B);
+#pragma unroll 4
+            for (uint32_t t = part * 16; t < t1; ++t) {
+                const uint32_t kt = order[t];
+                r += (kt > key || (kt == key && t < s)) ? 1u : 0u;
+            }
+        }
+        part_rank[part * 64 + s] = r;
+    } else if (lpt) {
 #pragma unroll
         for (int i = 0; i < kRanks; ++i) {
             const uint32_t s = tid + i * kThreads;
             if (s < p.B) {
                 const uint32_t key = order[s];
                 uint32_t r = 0;
+#pragma unroll 4
                 for (uint32_t t = 0; t < p.B; ++t) {
                     const uint32_t kt = order[t];
                     r += (kt > key || (kt == key && t < s)) ? 1u : 0u;
@@ -1053,7 +1071,12 @@ void decode_persistent_kernel(DecodeParams p)
         }
     }
     __syncthreads();  // every key is read: the ranks can be placed
-    if (lpt) {
+    if (lpt && p.B <= 64) {
+        if ((uint32_t)tid < p.B)
+            order[part_rank[tid] + part_rank[64 + tid] + part_rank[128 + tid] +
+                  part_rank[192 + tid]] = tid;
+        __syncthreads();
+    } else if (lpt) {
 #pragma unroll
         for (int i = 0; i < kRanks; ++i) {
             const uint32_t s = tid + i * kThreads;
