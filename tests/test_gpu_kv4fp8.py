@@ -174,6 +174,46 @@ def test_random_against_oracle(tq4, oracle, case, element):
     assert np.all(bits(out)[zero_rows] == 0)
 
 
+@pytest.mark.parametrize("element", [0, 1])
+def test_raw_query_zero_context_and_gate(tq4, oracle, element):
+    """Raw-query entry, output stage 2, with tokens of zero context between
+    live ones: part 0 writes the rotated query and the rows' gated zero
+    output; the live tokens match the oracle on the same rotated query."""
+    rng = np.random.default_rng(41 + element)
+    T, H, G, S = 4, 2, 16, 64
+    ctx = [0, 700, 0, 65]
+    P = sum((c + S - 1) // S for c in ctx) + 3
+    _, key, val, sc, tb, ln = random_case(rng, T, H, G, S, P, ctx, key_scale=(0.5, 2.0))
+    from oracle_bindings import f32_to_bf16
+    raw_f = rng.standard_normal((T, H * G, 256)).astype(np.float32)
+    gate_f = rng.standard_normal((T, H * G, 256)).astype(np.float32) * 3
+    if element:
+        raw_b, gate_b = f32_to_bf16(raw_f), f32_to_bf16(gate_f)
+    else:
+        raw_b, gate_b = raw_f.astype(np.float16).view(np.uint16), gate_f.astype(np.float16).view(np.uint16)
+    signs = np.where(rng.random(256) < 0.5, -1.0, 1.0).astype(np.float32)
+    isl = np.float32(1 / 16)
+    q_rot = oracle.kv4fp8_rotate_query(raw_b, signs, isl, element)
+    want, want_f32 = oracle.kv4fp8_decode(q_rot, key, val, sc, tb, ln, heads=H * G,
+                                          kv_heads=H, block_size=S, max_blocks=tb.shape[1],
+                                          num_blocks=P, element_type=element, output_stage=2,
+                                          pi_signs=signs, gate=gate_b)
+    shape = (T, H * G, 256)
+    raw = dev(raw_b.view(np.int16)).view(elem_dtype(element))
+    gate = dev(gate_b.view(np.int16)).view(elem_dtype(element))
+    qout = torch.full(shape, float("nan"), device=DEV)
+    out = tq4.kv4fp8_decode_raw_query(raw, dev(signs), dev(key), dev(val), dev(sc), dev(tb),
+                                      dev(ln), H, S, P, gate=gate, output_stage=2,
+                                      query_out=qout)
+    assert np.array_equal(qout.cpu().numpy().view(np.uint32), q_rot.view(np.uint32))
+    got = bits(out)
+    assert np.all(elem_to_f32(got[[0, 2]], element) == 0)  # +-0: the zero rows' signs follow Pi
+    assert np.array_equal(got[[0, 2]], want[[0, 2]])
+    # live rows: the decode's tolerance (the parts merge in another FP32 order)
+    mx, mr = compare(got[[1, 3]], want_f32[[1, 3]], element)
+    assert mx <= 2e-2 and mr <= 1e-3, (mx, mr)
+
+
 def test_grid_beyond_resident_workgroups(tq4, oracle):
     """75 tokens x 4 KV heads x 2 parts = 600 workgroups, more than two per
     CU: one combiner per group (the last ticket), which waits only on parts
