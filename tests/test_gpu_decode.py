@@ -104,6 +104,30 @@ def test_config4_split_sweep(tq4, oracle, ctx, K):
     check_out(got, want, f"ctx {ctx} K {K}")
 
 
+@pytest.mark.parametrize("K", [24, 40, 64])
+def test_multi_chunk_combine_one_launch(tq4, oracle, K):
+    """More than 16 live splits in the one-launch kernel: the combiner polls
+    16 records per round trip, its own record (kept in registers) may sit in
+    any chunk, and earlier chunks are zeroed after the last poll. Three calls
+    on one workspace with different queries must each match the oracle (a
+    record left unzeroed would be taken by the next call's poll)."""
+    import torch
+    rng = np.random.default_rng(0x5E20 + K)
+    ctx = [4096 + 7]
+    P = (ctx[0] + 15) // 16 + 8
+    kc, vc, sc, tables, signs, isl = build_cache(oracle, rng, ctx, 8, 128, 16, P)
+    scale = np.float32(1 / math.sqrt(128))
+    ws = tq4.decode_workspace(1, 32, 8, 128, K)
+    args = [dev(kc), dev(vc), dev(sc), dev(tables), dev(np.array(ctx, np.int32)), dev(signs)]
+    for call in range(3):
+        q = f32_to_bf16(rng.standard_normal((1, 32, 128)).astype(np.float32))
+        _, want = oracle.paged_decode(q, kc, vc, sc, tables, np.array(ctx, np.int32), signs,
+                                      None, 32, 8, 128, 16, P, K, scale, isl, 1, threads=8)
+        out = tq4.paged_decode(dev(q), *args, 8, 16, P, workspace=ws, num_splits=K,
+                               scale=float(scale), inv_sqrt_len=float(isl))
+        check_out(host(out), want, f"K {K} call {call}")
+
+
 def test_config4_ctx32768(tq4, oracle):
     rng = np.random.default_rng(0x71340004)
     got, want, _ = run_decode(tq4, oracle, rng, [32768], 32, 8, 128, 16, 2048 + 8, 16)
