@@ -46,8 +46,6 @@ constexpr float kCdf4C[16] = {-1.8627318674f, -1.3180108973f, -1.0099901692f, -0
                               0.7764217611f,  1.0099901692f,  1.3180108973f,  1.8627318674f};
 constexpr float kCdf2C[4] = {-1.1503493804f, -0.318639364f, 0.318639364f, 1.1503493804f};
 
-__device__ __forceinline__ float sel(bool c, float a, float b) { return c ? a : b; }
-
 // code (0..15) and centroid of one value, Lloyd-Max 4-bit
 __device__ __forceinline__ uint32_t lm4(float x, float& recon)
 {
