@@ -233,6 +233,17 @@ def test_persistent_ragged_batch(tq4, oracle):
     check_out(got, want, "persistent ragged")
 
 
+@pytest.mark.parametrize("d", [64, 256])
+def test_persistent_head_sizes_and_pages(tq4, oracle, d):
+    """The persistent form at d = 64 and d = 256 (its other instantiations),
+    32-token pages, GQA 3, ragged lengths with an empty sequence."""
+    rng = np.random.default_rng(0x5E30 + d)
+    ctx = [0, 5, 31, 32, 33] + [int(x) for x in rng.integers(1, 700, 75)]
+    got, want, _ = run_decode(tq4, oracle, rng, ctx, 12, 4, d, 32,
+                              sum((c + 31) // 32 for c in ctx) + 8, 8)
+    check_out(got, want, f"persistent d {d}")
+
+
 @pytest.mark.parametrize("B", [1000, 1100])
 def test_persistent_large_batch(tq4, oracle, B):
     """Up to 1024 sequences the persistent kernel ranks the last splits by
