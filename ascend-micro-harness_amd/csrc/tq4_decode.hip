@@ -422,6 +422,10 @@ __device__ __forceinline__ void decode_item(const DecodeParams& p, const uint32_
     partition(p.max_blocks, p.K, split, pb, pc);
     const uint32_t spp = S / kStrip;
     const int32_t* tbl = p.block_tables + (size_t)seq * p.max_blocks + pb;
+    // The window's first kThreads entries load beside the context length
+    // (the window depends on the partition alone); which of them are live is
+    // known once it returns.
+    const int32_t phys_first = (uint32_t)tid < pc ? tbl[tid] : 0;
     uint32_t ctx = ctx_raw < 0 ? 0u : (uint32_t)ctx_raw;
     const uint64_t capacity = (uint64_t)p.max_blocks * S;
     if (ctx > capacity) ctx = (uint32_t)capacity;
@@ -462,8 +466,7 @@ __device__ __forceinline__ void decode_item(const DecodeParams& p, const uint32_
     }
     const uint32_t live_pages = (ltok + S - 1) / S;
     int bad = 0;
-    for (uint32_t t = tid; t < pc; t += kThreads) {
-        const uint32_t phys = (uint32_t)tbl[t];
+    auto stage = [&](uint32_t t, uint32_t phys) {
         const bool ok = phys < p.P;
         if (!ok && t < live_pages) bad = 1;
         const uint32_t row = (phys * p.Hkv + kvh) * S;
@@ -471,7 +474,9 @@ __device__ __forceinline__ void decode_item(const DecodeParams& p, const uint32_
         // one padding row past the window: the second strip of a partial
         // last pair reads it (its tokens are masked)
         if (t == pc - 1) strip_lds[pc * spp] = ok ? row : 0u;
-    }
+    };
+    if ((uint32_t)tid < pc) stage(tid, (uint32_t)phys_first);
+    for (uint32_t t = tid + kThreads; t < pc; t += kThreads) stage(t, (uint32_t)tbl[t]);
     bad = __syncthreads_or(bad);
     // Every phase-0 load is complete here; saying so (vmcnt(0), expcnt and
     // lgkmcnt left at their maxima) keeps the compiler's wait analysis from
