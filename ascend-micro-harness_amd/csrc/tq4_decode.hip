@@ -439,14 +439,17 @@ __device__ __forceinline__ void decode_item(const DecodeParams& p, const uint32_
     // nothing -- the arrival count is the number of non-empty splits,
     // ceil(ceil(ctx / S) / width), which every workgroup of the sequence
     // derives from ctx alone -- and leave at once.
+    // split >= that count exactly when the window starts at or past ctx
+    // (the window starts at page split * width), a test without divisions.
     uint32_t k_live = p.K;
     if constexpr (MODE == 1) {
         if (p.K > 1) {
-            const uint32_t width = (p.max_blocks + p.K - 1) / p.K;
-            const uint32_t ctx_pages = (uint32_t)(((uint64_t)ctx + S - 1) / S);
-            k_live = (ctx_pages + width - 1) / width;
-            if (split >= k_live) {
-                if (k_live == 0 && split == 0) {
+            // 32-bit: its division runs while the table window is in flight
+            const uint32_t width = p.max_blocks / p.K + (p.max_blocks % p.K != 0u);
+            const uint32_t ctx_pages = ctx / S + (ctx % S != 0u);
+            k_live = ctx_pages / width + (ctx_pages % width != 0u);
+            if (tok0 >= ctx) {
+                if (ctx == 0 && split == 0) {
                     // empty context: the normalised context is 0 (l = 0)
                     float es[D / 32], gt[D / 32];
                     if (p.output_stage >= 1) load_lane_floats<D>(p.pi_signs, lane, es);
@@ -464,11 +467,10 @@ __device__ __forceinline__ void decode_item(const DecodeParams& p, const uint32_
             }
         }
     }
-    const uint32_t live_pages = (ltok + S - 1) / S;
     int bad = 0;
     auto stage = [&](uint32_t t, uint32_t phys) {
         const bool ok = phys < p.P;
-        if (!ok && t < live_pages) bad = 1;
+        if (!ok && t * S < ltok) bad = 1;  // page t holds a live token
         const uint32_t row = (phys * p.Hkv + kvh) * S;
         for (uint32_t s = 0; s < spp; ++s) strip_lds[t * spp + s] = ok ? row + kStrip * s : kBadStrip;
         // one padding row past the window: the second strip of a partial
