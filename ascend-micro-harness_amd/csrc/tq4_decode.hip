@@ -386,6 +386,7 @@ __device__ __forceinline__ void decode_item(const DecodeParams& p, const uint32_
     int* q_exp = (int*)(smem + 128);         // [16]
     int* flag = (int*)(smem + 144);
     float* u_x = smem + 148;                 // [4] per-wave 2^-sh
+    int* bad_w = (int*)(smem + 152);         // [4] per-wave invalid-page flags
     float* sc_wave = smem + 160 + 64 * (threadIdx.x >> 6);  // [4][64] per-wave scale slot
     uint32_t* strip_lds = (uint32_t*)(smem + kHdrFloats);  // [TQ4 max split strips + padding]
     float* region = smem + kHdrFloats + kStripSlots;
@@ -479,7 +480,14 @@ __device__ __forceinline__ void decode_item(const DecodeParams& p, const uint32_
     };
     if ((uint32_t)tid < pc) stage(tid, (uint32_t)phys_first);
     for (uint32_t t = tid + kThreads; t < pc; t += kThreads) stage(t, (uint32_t)tbl[t]);
-    bad = __syncthreads_or(bad);
+    // One barrier: every wave writes its own flag, so nothing needs clearing.
+    {
+        const int wb = __any(bad);
+        if (lane == 0) bad_w[wave] = wb;
+        lds_barrier();
+        const int4 bw = *(const int4*)bad_w;
+        bad = bw.x | bw.y | bw.z | bw.w;
+    }
     // Every phase-0 load is complete here; saying so (vmcnt(0), expcnt and
     // lgkmcnt left at their maxima) keeps the compiler's wait analysis from
     // later waiting on them -- and so on the strip loads queued after them.
