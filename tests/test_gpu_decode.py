@@ -159,6 +159,49 @@ def test_single_split_and_empty_splits(tq4, oracle):
         check_out(got, want, f"K {K}")
 
 
+@pytest.mark.parametrize("case", ["k1", "k4", "persistent"])
+def test_invalid_live_pages_are_skipped(tq4, oracle, case):
+    """Table entries of live pages that name no page (negative or >= the
+    pool) send their window through the masked path, which drops those
+    pages' tokens. Softmax attention does not depend on token order, so the
+    result must equal the oracle's over the same table with those pages
+    removed and the context shortened by theirs. Invalid entries past the
+    context change nothing. K = 1 puts an invalid page past the first 256
+    entries of a window; "persistent" runs the work-queue form."""
+    rng = np.random.default_rng({"k1": 0xBAD1, "k4": 0xBAD4, "persistent": 0xBAD8}[case])
+    S, H, Hq, d = 16, 8, 32, 128
+    if case == "persistent":
+        ctx_lens, K = [int(x) for x in rng.integers(40, 1500, 80)], 8
+    else:
+        ctx_lens, K = [1000, 4200, 300], (1 if case == "k1" else 4)
+    pages = [(c + S - 1) // S for c in ctx_lens]
+    P = sum(pages) + 8
+    kc, vc, sc, tables, signs, isl = build_cache(oracle, rng, ctx_lens, H, d, S, P)
+    bad = tables.copy()
+    comp = np.zeros_like(tables)
+    comp_ctx = []
+    for b, c in enumerate(ctx_lens):
+        full = c // S  # whole live pages (the partial last page stays)
+        drop = set(int(i) for i in rng.choice(full, size=min(2, full // 2), replace=False))
+        if case != "persistent" and b == 1:
+            drop.add(260)  # past the first 256 entries of the K = 1 window
+        for j, i in enumerate(sorted(drop)):
+            bad[b, i] = -1 if j % 2 == 0 else P + 3
+        keep = [tables[b, i] for i in range(pages[b]) if i not in drop]
+        comp[b, :len(keep)] = keep
+        comp_ctx.append(c - S * len(drop))
+        if b == 2:
+            bad[b, pages[b]:] = -1  # dead entries: no effect
+    q = f32_to_bf16(rng.standard_normal((len(ctx_lens), Hq, d)).astype(np.float32))
+    scale = np.float32(1.0 / math.sqrt(d))
+    _, want = oracle.paged_decode(q, kc, vc, sc, comp, np.array(comp_ctx, np.int32), signs, None,
+                                  Hq, H, d, S, P, K, scale, isl, 1, threads=8)
+    got = tq4.paged_decode(dev(q), dev(kc), dev(vc), dev(sc), dev(bad),
+                           dev(np.array(ctx_lens, np.int32)), dev(signs), H, S, P, num_splits=K,
+                           scale=float(scale), inv_sqrt_len=float(isl), output_stage=1)
+    check_out(host(got), want, f"invalid pages {case}")
+
+
 def test_partials_match_oracle(tq4, oracle):
     """Partial records (m, l, acc) per split, incl. exact neutral records."""
     rng = np.random.default_rng(123)
