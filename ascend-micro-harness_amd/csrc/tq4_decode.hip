@@ -77,7 +77,7 @@ constexpr float kTau = 8.0f;             // lazy-maximum headroom, log2 units
 constexpr float kShiftLimit = 100.0f;    // bound of the value-scale normalisation shift
 constexpr uint32_t kBadStrip = 0xFFFFFFFFu;
 constexpr uint32_t kFlagRotated = 1u;
-constexpr int kHdrFloats = 416;          // m_x, l_x [16][4], q_exp[16], flags, 2^-sh[4], scale slots [4][64]
+constexpr int kHdrFloats = 416;          // m_x, l_x [16][4], q_exp[16], flags, 2^-sh[4], wave flags[4], scale slots [4][64]
 constexpr uint32_t kPersistentMaxSeqs = 4096; // the persistent kernel stages two words per sequence
 constexpr uint32_t kLptMaxSeqs = 1024;        // and a third (the last-split order) up to this many
 constexpr int kStripSlots = TQ4_MAX_SPLIT_STRIPS + 4;  // staged window rows + padding
