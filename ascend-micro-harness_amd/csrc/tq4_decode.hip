@@ -129,13 +129,6 @@ __device__ __forceinline__ float wave_max(float v)
     return v;
 }
 
-// Workgroup barrier for LDS traffic only: it does not wait for outstanding
-// global loads (vmcnt), so prefetched pairs stay in flight across it.
-__device__ __forceinline__ void lds_barrier()
-{
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-}
-
 // One pair's operands for one lane (n = lane & 15, g = lane >> 4).
 template <int D>
 struct PairRegs {

@@ -150,6 +150,15 @@ __device__ __forceinline__ void partition(uint32_t pages, uint32_t splits, uint3
     count = remaining < width ? remaining : width;
 }
 
+// Workgroup barrier for LDS traffic only: it does not wait for outstanding
+// global loads or for store acknowledgements (vmcnt), which __syncthreads()
+// does, so prefetched loads stay in flight and earlier stores are not
+// waited for.
+__device__ __forceinline__ void lds_barrier()
+{
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 // Record traffic between workgroups of one launch: buffer stores and loads
 // with the device-coherence bit (sc1 -- what agent-scope relaxed atomic
 // stores and loads are on gfx950), plain accesses to the compiler, so they

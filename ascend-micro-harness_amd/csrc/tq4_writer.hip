@@ -160,6 +160,7 @@ __global__ __launch_bounds__(kWriterThreads) void strip_writer(
     // codes; 20-word rows put the 64 lanes of a wave (16 lanes x 4 tokens)
     // on distinct banks
     __shared__ __align__(16) uint32_t lds_t[NH][D / 8][TS];
+    __shared__ __align__(16) int ok_w[kWriterThreads / 64];  // per-wave slot checks
 
     const uint32_t groups = H / NH;
     const uint32_t head0 = (blockIdx.x % groups) * NH;
@@ -185,7 +186,15 @@ __global__ __launch_bounds__(kWriterThreads) void strip_writer(
     const int32_t mine = slots[(size_t)strip * kStrip + row];
     const bool ok = slot0 >= 0 && (slot0 % kStrip) == 0 && mine == slot0 + row &&
                     (uint32_t)slot0 / S < P;
-    if (!__syncthreads_and(ok)) return;
+    // One barrier: every wave writes its own vote, so nothing needs clearing.
+    static_assert(kWriterThreads == 256, "four wave votes");
+    {
+        const int wv = __all(ok);
+        if ((tid & 63) == 0) ok_w[tid >> 6] = wv;
+        __syncthreads();
+        const int4 w4 = *(const int4*)ok_w;
+        if (!(w4.x & w4.y & w4.z & w4.w)) return;
+    }
     const uint32_t page = (uint32_t)slot0 / S;
     const uint32_t tip = (uint32_t)slot0 % S + (uint32_t)row;
     int q[NJ][CPL];
