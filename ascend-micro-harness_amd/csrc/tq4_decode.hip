@@ -1130,9 +1130,11 @@ void decode_persistent_kernel(DecodeParams p)
                 __hip_atomic_store(p.queue, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             *next_lds = gridDim.x + fetched;
         }
-        __syncthreads();
+        // LDS-only barriers: the item's record stores are not waited for
+        // here; the next item's phase-0 loads go out first.
+        lds_barrier();
         item = __builtin_amdgcn_readfirstlane(*next_lds);
-        __syncthreads();
+        lds_barrier();
     }
 }
 
