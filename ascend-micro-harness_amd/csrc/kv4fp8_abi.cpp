@@ -11,6 +11,7 @@
 
 #include "../../include/tq4.h"
 #include "../../include/tq4_kv4fp8.h"
+#include "tq4_device.hpp"
 #include "tq4_internal.hpp"
 
 namespace {
@@ -90,6 +91,13 @@ uint64_t records_bytes(const tq4_kv4fp8_launch* L, const Plan& p)
            round256((uint64_t)L->tokens * L->heads * p.parts * kRecFloats * sizeof(float));
 }
 
+// ... then one 256-byte status block: word 0 the sticky poll-timeout count.
+constexpr uint64_t kStatusBytes = 256;
+uint64_t workspace_need(const tq4_kv4fp8_launch* L, const Plan& p)
+{
+    return records_bytes(L, p) + kStatusBytes;
+}
+
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 int common_checks(const tq4_kv4fp8_launch* L, const tq4_kv4fp8_buffers* b, const Plan& plan)
@@ -99,8 +107,12 @@ int common_checks(const tq4_kv4fp8_launch* L, const tq4_kv4fp8_buffers* b, const
         return TQ4_ERR_NULL_POINTER;
     if (!aligned16(b->key) || !aligned16(b->value) || !aligned16(b->scales))
         return TQ4_ERR_GEOMETRY;
-    if (!aligned16(b->workspace) || L->workspace_bytes < records_bytes(L, plan))
+    if (!aligned16(b->workspace) || L->workspace_bytes < workspace_need(L, plan))
         return TQ4_ERR_WORKSPACE;
+    if (L->test_flags & ~(uint32_t)(TQ4_KV4FP8_TEST_POLL_BOUND | TQ4_KV4FP8_TEST_WITHHOLD))
+        return TQ4_ERR_FLAGS;
+    if ((L->test_flags & TQ4_KV4FP8_TEST_WITHHOLD) && !(L->test_flags & TQ4_KV4FP8_TEST_POLL_BOUND))
+        return TQ4_ERR_FLAGS;
     return TQ4_OK;
 }
 
@@ -116,6 +128,10 @@ tq4::Kv4Params params_of(const tq4_kv4fp8_launch* L, const tq4_kv4fp8_buffers* b
     p.context_lens = (const int32_t*)b->context_lengths;
     p.counters = (uint32_t*)b->workspace;
     p.records = (float*)((char*)b->workspace + counters_bytes(L, plan));
+    p.timeouts = (uint32_t*)((char*)b->workspace + records_bytes(L, plan));
+    p.poll_limit = (L->test_flags & TQ4_KV4FP8_TEST_POLL_BOUND) ? tq4::kPollLimitTest
+                                                                 : tq4::kPollLimit;
+    p.withhold = (L->test_flags & TQ4_KV4FP8_TEST_WITHHOLD) ? 1u : 0u;
     p.out = (uint16_t*)b->output;
     p.T = L->tokens;
     p.Hq = L->heads;
@@ -144,7 +160,23 @@ extern "C" {
 uint64_t tq4_kv4fp8_workspace_bytes(const tq4_kv4fp8_launch* launch)
 {
     if (geometry(launch) != TQ4_OK) return 0;
-    return records_bytes(launch, plan_of(launch));
+    return workspace_need(launch, plan_of(launch));
+}
+
+int tq4_kv4fp8_poll_timeouts(void* stream, const tq4_kv4fp8_launch* launch,
+                             const void* workspace, uint32_t* count)
+{
+    const int st = geometry(launch);
+    if (st != TQ4_OK) return st;
+    if (!workspace || !count) return TQ4_ERR_NULL_POINTER;
+    const Plan plan = plan_of(launch);
+    if (!aligned16(workspace) || launch->workspace_bytes < workspace_need(launch, plan))
+        return TQ4_ERR_WORKSPACE;
+    const char* word = (const char*)workspace + records_bytes(launch, plan);
+    return hipMemcpyAsync(count, word, sizeof(uint32_t), hipMemcpyDefault,
+                          (hipStream_t)stream) == hipSuccess
+               ? TQ4_OK
+               : TQ4_ERR_LAUNCH;
 }
 
 int tq4_kv4fp8_workspace_init(void* stream, void* workspace, uint64_t workspace_bytes)

@@ -230,7 +230,8 @@ constexpr int kPollBatch = 16;  // records polled together (one round trip)
 // The combiner's merge of one row: the records of parts 0 .. live-1 in part
 // order, its own part's (`own`) from LDS and the others' polled from the
 // workspace. A batch of records is reloaded until none of its words is zero
-// (bounded by kPollLimit), then zeroed for the next call.
+// (at most p.poll_limit times; a batch still incomplete then adds one to
+// *p.timeouts), then zeroed for the next call.
 __device__ __forceinline__ void combine_polled(const Kv4Params& p, uint32_t row, uint32_t live,
                                                uint32_t own, const float* own_acc,
                                                const float* own_ml, int lane, float (&x)[4],
@@ -280,7 +281,11 @@ __device__ __forceinline__ void combine_polled(const Kv4Params& p, uint32_t row,
                     mn = min(min(mn, min(hw[j][0], hw[j][1])),
                              min(min(aw[j][0], aw[j][1]), min(aw[j][2], aw[j][3])));
             }
-            if (!__any(mn == 0u) || it + 1 >= kPollLimit) break;
+            if (!__any(mn == 0u)) break;
+            if (it + 1 >= p.poll_limit) {  // gave up: merged from what arrived
+                if (lane == 0) count_timeout(p.timeouts);
+                break;
+            }
         }
         // the last batch is zeroed at once, earlier ones after the loop (a
         // later batch's poll would wait for their write acknowledgements)
@@ -634,7 +639,10 @@ void kv4_decode_kernel(Kv4Params p)
             if (ticket == live_parts - 1)
                 __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
-        *role_lds = role;
+        role_lds[0] = role;
+        // test hook: the first ticket's part withholds the records the other
+        // combiners wait for
+        role_lds[1] = p.withhold && live_parts > 1 && ticket == 0;
     }
     __syncthreads();
 
@@ -688,7 +696,8 @@ void kv4_decode_kernel(Kv4Params p)
 
     // ---- export the records of the rows other parts combine: encoded
     // (bits ^ kRecMagic, never 0) with device-coherent stores
-    for (uint32_t hh = wave; hh < gc; hh += kWaves) {
+    const bool withheld = role_lds[1] != 0;
+    for (uint32_t hh = wave; hh < gc && !withheld; hh += kWaves) {
         if (role >= 0 && hh % R == (uint32_t)role) continue;
         const __amdgpu_buffer_rsrc_t rs =
             records_rsrc(p.records + (row0 + hh) * p.parts * kRecFloats);

@@ -8,6 +8,7 @@
 #include <hip/hip_runtime.h>
 
 #include "../../include/tq4.h"
+#include "tq4_device.hpp"
 #include "tq4_internal.hpp"
 
 namespace {
@@ -18,9 +19,12 @@ bool head_size_ok(uint32_t d) { return d == 64 || d == 128 || d == 256; }
 
 int launched(hipError_t e) { return e == hipSuccess ? TQ4_OK : TQ4_ERR_LAUNCH; }
 
-// Fused-decode workspace tail: the work-queue counter of the persistent
-// kernel (one 256-byte block), then one split-ticket word per (seq, kv head).
+// Fused-decode workspace tail: one 256-byte block holding the work-queue
+// counter of the persistent kernel (word 0) and the sticky poll-timeout count
+// (word 1), then one split-ticket word per (seq, kv head).
 constexpr size_t kQueueBytes = 256;
+constexpr uint32_t kFlagsKnown = TQ4_DECODE_QUERY_ROTATED | TQ4_DECODE_TEST_POLL_BOUND |
+                                 TQ4_DECODE_TEST_WITHHOLD;
 size_t ticket_bytes(uint32_t num_seqs, uint32_t num_kv_heads)
 {
     return ((size_t)num_seqs * num_kv_heads * sizeof(uint32_t) + 255) & ~(size_t)255;
@@ -68,6 +72,7 @@ const char* tq4_status_string(int status)
         case TQ4_ERR_LAUNCH: return "the HIP runtime refused the launch";
         case TQ4_ERR_RANGE: return "a size exceeds the kernels' index range";
         case TQ4_ERR_CODEBOOK: return "codebook leaf: bits must be 2 or 4, mode 0..5, elements a multiple of 8";
+        case TQ4_ERR_FLAGS: return "unknown flag bits, or a test hook without its poll bound";
         default: return "unknown status";
     }
 }
@@ -189,6 +194,19 @@ int tq4_decode_workspace_init(void* stream, void* workspace, size_t workspace_by
     return launched(tq4::launch_fill_zero((hipStream_t)stream, workspace, workspace_bytes));
 }
 
+int tq4_decode_poll_timeouts(void* stream, const void* workspace, size_t workspace_bytes,
+                             uint32_t num_seqs, uint32_t num_kv_heads, uint32_t* count)
+{
+    if (!workspace || !count) return TQ4_ERR_NULL_POINTER;
+    const size_t tail = ticket_bytes(num_seqs, num_kv_heads) + kQueueBytes;
+    if (num_seqs == 0 || num_kv_heads == 0 || workspace_bytes < tail ||
+        ((uintptr_t)workspace & 15u))
+        return TQ4_ERR_WORKSPACE;
+    const char* word = (const char*)workspace + workspace_bytes - tail + sizeof(uint32_t);
+    return launched(hipMemcpyAsync(count, word, sizeof(uint32_t), hipMemcpyDefault,
+                                   (hipStream_t)stream));
+}
+
 namespace {
 
 int decode_checks(const uint16_t* q, const int8_t* kc, const int8_t* vc, const float* sc,
@@ -203,6 +221,9 @@ int decode_checks(const uint16_t* q, const int8_t* kc, const int8_t* vc, const f
         num_blocks == 0 || max_blocks_per_seq == 0)
         return TQ4_ERR_GEOMETRY;
     if (!q || !kc || !vc || !sc || !tables || !ctx) return TQ4_ERR_NULL_POINTER;
+    if (flags & ~kFlagsKnown) return TQ4_ERR_FLAGS;
+    if ((flags & TQ4_DECODE_TEST_WITHHOLD) && !(flags & TQ4_DECODE_TEST_POLL_BOUND))
+        return TQ4_ERR_FLAGS;
     if (!(flags & TQ4_DECODE_QUERY_ROTATED) && !pi_signs) return TQ4_ERR_ROTATION;
     // cache rows are indexed in 32 bits on the device
     if ((uint64_t)num_blocks * num_kv_heads * block_size > 0xffffffffull) return TQ4_ERR_RANGE;
@@ -244,7 +265,9 @@ tq4::DecodeParams make_params(const uint16_t* q, const int8_t* kc, const int8_t*
     p.scale = scale;
     p.inv_sqrt_len = inv_sqrt_len;
     p.output_stage = output_stage;
-    p.flags = flags;
+    p.flags = flags & TQ4_DECODE_QUERY_ROTATED;
+    p.poll_limit = (flags & TQ4_DECODE_TEST_POLL_BOUND) ? tq4::kPollLimitTest : tq4::kPollLimit;
+    p.withhold = (flags & TQ4_DECODE_TEST_WITHHOLD) ? 1u : 0u;
     return p;
 }
 
@@ -290,6 +313,7 @@ int tq4_paged_decode(void* stream, const uint16_t* q, const int8_t* key_cache,
         char* end = (char*)workspace + workspace_bytes;
         p.counters = (uint32_t*)(end - ticket_bytes(num_seqs, num_kv_heads));
         p.queue = (uint32_t*)(end - ticket_bytes(num_seqs, num_kv_heads) - kQueueBytes);
+        p.timeouts = p.queue + 1;
     }
     return launched(tq4::launch_decode((hipStream_t)stream, p, 1));
 }
@@ -307,6 +331,7 @@ int tq4_paged_decode_partials(void* stream, const uint16_t* q, const int8_t* key
                            pi_signs, num_seqs, num_heads, num_kv_heads, head_size, block_size,
                            num_blocks, max_blocks_per_seq, flags);
     if (rc != TQ4_OK) return rc;
+    if (flags & ~TQ4_DECODE_QUERY_ROTATED) return TQ4_ERR_FLAGS;  // no poll, no test hook
     if (num_splits == 0 || num_splits > TQ4_MAX_SPLITS ||
         !split_pages_ok(max_blocks_per_seq, block_size, num_splits))
         return TQ4_ERR_SPLITS;

@@ -74,10 +74,12 @@ constexpr uint32_t kCodeBase = 0x3C803C80u;  // fp16 1.0 outside kNib; the nibbl
 constexpr float kCodeOffset = 1.125f;    // fp16 code value is 1 + u/64 = 1.125 + n/64
 constexpr float kCodeUnit = 64.0f;
 constexpr float kTau = 8.0f;             // lazy-maximum headroom, log2 units
-constexpr float kShiftLimit = 100.0f;    // bound of the value-scale normalisation shift
+constexpr float kShiftLimit = 100.0f;    // bound of a row's product normalisation shift
+constexpr float kXLimit = 32768.0f;      // a normalised product at or above this rescales (fp16 max 65504)
+constexpr int kMassLimit = 100;          // log2 bound of a row's normalised mass after a rescale
 constexpr uint32_t kBadStrip = 0xFFFFFFFFu;
 constexpr uint32_t kFlagRotated = 1u;
-constexpr int kHdrFloats = 416;          // m_x, l_x [16][4], q_exp[16], flags, 2^-sh[4], wave flags[4], scale slots [4][64]
+constexpr int kHdrFloats = 480;          // m_x, l_x [16][4], q_exp[16], flags, wave flags[4], scale slots [4][64], 2^-sh [16][4]
 constexpr uint32_t kPersistentMaxSeqs = 4096; // the persistent kernel stages two words per sequence
 constexpr uint32_t kLptMaxSeqs = 1024;        // and a third (the last-split order) up to this many
 constexpr int kStripSlots = TQ4_MAX_SPLIT_STRIPS + 4;  // staged window rows + padding
@@ -169,7 +171,8 @@ __device__ __forceinline__ void load_row_chunk(uint32_t (&k)[D / 32], const int8
 // in split order, leaving acc / L in v (0 when L == 0).
 // (tests/common/l2_atomic_oracle.hpp:156-176; identity :100-108)
 // FUSED: the records are encoded; a chunk is reloaded until none of its words
-// is zero (bounded by kPollLimit), then zeroed for the next call.
+// is zero (at most poll_limit times; a chunk still incomplete then adds one
+// to *timeouts), then zeroed for the next call.
 // own_k < K: the calling split's own record is not in memory. Its encoded
 // words come from own(h, a), in this lane's combine layout, called once after
 // the first chunk's loads are issued (so it runs under their round trip);
@@ -177,7 +180,8 @@ __device__ __forceinline__ void load_row_chunk(uint32_t (&k)[D / 32], const int8
 // the record had been stored and loaded.
 template <int D, bool FUSED, int NS = 8, class Own>
 __device__ void combine_records(const float* rr, uint32_t K, int lane, float (&v)[D / 32],
-                                uint32_t own_k, Own&& own)
+                                uint32_t own_k, Own&& own, uint32_t poll_limit = 1,
+                                uint32_t* timeouts = nullptr)
 {
     constexpr int CC = D / 32;
     constexpr int LD = CC >= 4 ? 4 : CC;  // floats per load
@@ -254,7 +258,11 @@ __device__ void combine_records(const float* rr, uint32_t K, int lane, float (&v
                 for (int j = 0; j < CC; ++j) ms = min(ms, aw[i][j]);
                 mn = vi[i] ? min(mn, ms) : mn;
             }
-            if (!__any(mn == 0u) || it + 1 >= kPollLimit) break;
+            if (!__any(mn == 0u)) break;
+            if (it + 1 >= poll_limit) {  // gave up: the row is combined from what arrived
+                if (lane == 0) count_timeout(timeouts);
+                break;
+            }
         }
         // The last chunk's records are zeroed at once (the stores complete
         // under the arithmetic below); earlier chunks' after the loop, since
@@ -378,7 +386,7 @@ __device__ __forceinline__ void decode_item(const DecodeParams& p, const uint32_
     float* l_x = smem + 64;                  // [16][4]
     int* q_exp = (int*)(smem + 128);         // [16]
     int* flag = (int*)(smem + 144);
-    float* u_x = smem + 148;                 // [4] per-wave 2^-sh
+    float* u_x = smem + 416;                 // [16][4] (row, wave) 2^-sh
     int* bad_w = (int*)(smem + 152);         // [4] per-wave invalid-page flags
     float* sc_wave = smem + 160 + 64 * (threadIdx.x >> 6);  // [4][64] per-wave scale slot
     uint32_t* strip_lds = (uint32_t*)(smem + kHdrFloats);  // [TQ4 max split strips + padding]
@@ -607,21 +615,22 @@ __device__ __forceinline__ void decode_item(const DecodeParams& p, const uint32_
     // q_st is next overwritten after the first merge barrier, which every
     // wave reaches only after building its operands.
 
-    // ---- streaming state. Scores t = s - mo with s = score * log2(e)
-    // (log2 units), mo = m_used - sh; P' = exp2(t) = P * 2^sh, where
-    // sh = 127 - E normalises P * vscale into fp16 (E: exponent field bound
-    // of the value scales seen so far, wave-uniform).
+    // ---- streaming state, per q row. Scores t = s - mo with s = score *
+    // log2(e) (log2 units), mo = m_used - sh: P' = exp2(t) = P * 2^sh, and
+    // the MFMA operand is the product P' * vscale in fp16. The row's shift
+    // sh is set at each rescale so that the largest product of that pair
+    // lands in [1, 2): every product that matters for the row's sum then
+    // fits fp16 (one below 2^-24 of the largest is below 2^-24 of the sum),
+    // whatever the spread of the value scales; the accumulators are FP32.
     f4_t acc[NB];
 #pragma unroll
     for (int b = 0; b < NB; ++b) acc[b] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
     f4_t cr = f4_t{0.0f, 0.0f, 0.0f, 0.0f};  // offset column: 1.125 * sum P'vs per row
     float m_used = row_live ? -INFINITY : INFINITY;  // padded rows stay silent
+    float sh = 0.0f;
     float mo = m_used;
     float lpart = 0.0f;
-    int E = 0;
-    float sh = kShiftLimit;
     float thr = kTau + sh;
-    float vb = ldexpf(1.0f, -126);
 
     auto process = [&](const PairRegs<D>& r, uint32_t gp, bool masked) {
         f4_t c1 = bias4, c2 = bias4;
@@ -637,17 +646,7 @@ __device__ __forceinline__ void decode_item(const DecodeParams& p, const uint32_
         const f4_t ks2 = *(const f4_t*)(sc_wave + 32 * sp + 8 * half + 4);
         const f4_t vs1 = *(const f4_t*)(sc_wave + 32 * sp + 16 + 8 * half);
         const f4_t vs2 = *(const f4_t*)(sc_wave + 32 * sp + 16 + 8 * half + 4);
-        float c[8], cfk[8], vs[8];
         bool live[8];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            c[i] = c1[i];
-            c[4 + i] = c2[i];
-            cfk[i] = cf * ks1[i];
-            cfk[4 + i] = cf * ks2[i];
-            vs[i] = vs1[i];
-            vs[4 + i] = vs2[i];
-        }
         if (masked) {
             // window token of value i: pair base + strip sp + 8*half + (i&3) + 4*(i>>2)
             const uint32_t tb = 32 * gp + 16 * sp + 8 * half;
@@ -659,24 +658,55 @@ __device__ __forceinline__ void decode_item(const DecodeParams& p, const uint32_
 #pragma unroll
             for (int i = 0; i < 8; ++i) live[i] = true;
         }
-        float t[8];
+        // scores (log2 units) and value scales; a dead token is overwritten
+        // -- score -inf, value scale 0 -- never multiplied (its payload may
+        // be NaN)
+        float sc8[8], vs[8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            sc8[i] = live[i] ? c1[i] * (cf * ks1[i]) : -INFINITY;
+            sc8[4 + i] = live[4 + i] ? c2[i] * (cf * ks2[i]) : -INFINITY;
+            vs[i] = live[i] ? vs1[i] : 0.0f;
+            vs[4 + i] = live[4 + i] ? vs2[i] : 0.0f;
+        }
+        // Rescale when a score passes the lazy maximum by kTau, or when a
+        // product could reach kXLimit: exp2(tmax) * vmax bounds every
+        // product (one exp per lane; the products themselves are formed
+        // after the branch, so nothing of them stays live across it).
         float tmax = -INFINITY, vmax = 0.0f;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            t[i] = live[i] ? __builtin_fmaf(c[i], cfk[i], -mo) : -INFINITY;
-            tmax = fmaxf(tmax, t[i]);
-            vmax = fmaxf(vmax, live[i] ? vs[i] : 0.0f);
+            tmax = fmaxf(tmax, sc8[i] - mo);
+            vmax = fmaxf(vmax, vs[i]);
         }
-        if (__builtin_expect(__any(tmax > thr || vmax >= vb), 0)) {
-            // Move the row maximum / the value-scale bound, rescale.
+        if (__builtin_expect(
+                __any(tmax > thr || __builtin_amdgcn_exp2f(tmax) * vmax >= kXLimit), 0)) {
+            // Move the row maximum and re-normalise the row's products.
             float smax = -INFINITY;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) smax = fmaxf(smax, live[i] ? c[i] * cfk[i] : -INFINITY);
+            for (int i = 0; i < 8; ++i) smax = fmaxf(smax, sc8[i]);
             smax = col_max(smax);
-            const float vm = wave_max(vmax);
-            const int En = max(E, (int)((__float_as_uint(vm) >> 23) & 0xffu));
-            const float shn = fminf(fmaxf(127.0f - (float)En, -kShiftLimit), kShiftLimit);
             const float mn = row_live ? fmaxf(m_used, smax) : m_used;
+            // the pair's largest product under the new maximum, unnormalised
+            float ymax = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) ymax = fmaxf(ymax, __builtin_amdgcn_exp2f(sc8[i] - mn) * vs[i]);
+            ymax = col_max(ymax);
+            // the row's mass so far (its offset-column sum, P.V layout row n)
+            const int src = 16 * (n >> 2);
+            const float r0 = __shfl(cr[0], src, 64), r1 = __shfl(cr[1], src, 64);
+            const float r2 = __shfl(cr[2], src, 64), r3 = __shfl(cr[3], src, 64);
+            const int k3 = n & 3;
+            const float crow = k3 == 0 ? r0 : k3 == 1 ? r1 : k3 == 2 ? r2 : r3;
+            float shn = sh;
+            if (row_live && ymax > 0.0f) {
+                shn = fminf(fmaxf(-(float)exponent_of(ymax), -kShiftLimit), kShiftLimit);
+                // keep the old mass, moved to the new units, inside FP32
+                if (m_used != -INFINITY && crow > 0.0f) {
+                    const float lm = (float)exponent_of(crow) + (shn - sh) + (m_used - mn);
+                    if (lm > (float)kMassLimit) shn -= ceilf(lm - (float)kMassLimit);
+                }
+            }
             const float mon = mn - shn;
             float f = 1.0f;
             if (row_live) f = mo == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mo - mon);
@@ -692,21 +722,18 @@ __device__ __forceinline__ void decode_item(const DecodeParams& p, const uint32_
             }
             m_used = mn;
             mo = mon;
-            E = En;
             sh = shn;
             thr = kTau + shn;
-            vb = ldexpf(1.0f, En - 126);
-#pragma unroll
-            for (int i = 0; i < 8; ++i)
-                t[i] = live[i] ? __builtin_fmaf(c[i], cfk[i], -mo) : -INFINITY;
         }
         _Float16 x[8];
         float psum = 0.0f;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            const float pr = __builtin_amdgcn_exp2f(t[i]);
+            // a dead token is 0 even while the row has no maximum yet
+            // (-inf - -inf would be NaN)
+            const float pr = sc8[i] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(sc8[i] - mo);
             psum += pr;
-            x[i] = (_Float16)(live[i] ? pr * vs[i] : 0.0f);
+            x[i] = (_Float16)(pr * vs[i]);
         }
         lpart += psum;
         // A operand in the codes8 token order: (T1[0], T2[0], T1[1], T2[1], ...)
@@ -793,16 +820,18 @@ __device__ __forceinline__ void decode_item(const DecodeParams& p, const uint32_
         m_x[n * kWaves + wave] = row_live ? m_used : -INFINITY;
         l_x[n * kWaves + wave] = lsum;
     }
-    if (lane == 0) u_x[wave] = ldexpf(1.0f, -(int)sh);
+    if (g4 == 0) u_x[n * kWaves + wave] = ldexpf(1.0f, -(int)sh);
     if constexpr (MODE == 1) {
         if (p.K > 1 && tid == 0) {
             // The last ticket combines; every live split of this (seq, kv
             // head) took its ticket before it, so all of them are running.
+            // Bit 1: the test hook's withheld record (the first ticket's,
+            // never the combiner's when more than one split is live).
             const int last = ticket == k_live - 1;
             if (last)
                 __hip_atomic_store(p.counters + (size_t)seq * p.Hkv + kvh, 0u, __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_AGENT);
-            *flag = last;
+            *flag = last | (p.withhold && ticket == 0 && !last ? 2 : 0);
         }
     }
     float* part = region;  // [kWaves][G][D]
@@ -821,7 +850,7 @@ __device__ __forceinline__ void decode_item(const DecodeParams& p, const uint32_
     auto row_weights = [&](uint32_t r, float (&f)[kWaves], float& M, float& L) {
         const float4 m4 = *(const float4*)(m_x + r * kWaves);
         const float4 l4 = *(const float4*)(l_x + r * kWaves);
-        const float4 u4 = *(const float4*)u_x;
+        const float4 u4 = *(const float4*)(u_x + r * kWaves);
         const float mw[kWaves] = {m4.x, m4.y, m4.z, m4.w};
         const float lw[kWaves] = {l4.x, l4.y, l4.z, l4.w};
         const float uw[kWaves] = {u4.x, u4.y, u4.z, u4.w};
@@ -873,8 +902,10 @@ __device__ __forceinline__ void decode_item(const DecodeParams& p, const uint32_
         // window) finalises from LDS; otherwise every split exports and the
         // last ticket combines.
         const bool local = p.K == 1 || k_live == 1;
-        const bool combiner = local || *flag;
+        const int fl = *flag;
+        const bool combiner = local || (fl & 1);
         float es[CC];
+        if (!local && (fl & 2)) return;  // test hook: this record is never written
         if (!local && (!combiner || !OWN)) {
             // ---- export this split's encoded record.
             const __amdgpu_buffer_rsrc_t rsrc = records_rsrc(
@@ -933,10 +964,10 @@ __device__ __forceinline__ void decode_item(const DecodeParams& p, const uint32_
                 // measured slower at every split count from 17 to 64
                 if constexpr (OWN)
                     combine_records<D, true, 8>(p.records + qh * p.K * RS, k_live, lane, v,
-                                                split, own);
+                                                split, own, p.poll_limit, p.timeouts);
                 else
                     combine_records<D, true, 8>(p.records + qh * p.K * RS, k_live, lane, v, ~0u,
-                                                none);
+                                                none, p.poll_limit, p.timeouts);
                 egress_row<D>(v, es, gt, p.out + qh * D, p.inv_sqrt_len, p.output_stage, lane);
             }
             return;

@@ -168,6 +168,16 @@ __device__ __forceinline__ void lds_barrier()
 constexpr int kCachePolicySc1 = 16;          // cache-policy operand bit of sc1
 constexpr uint32_t kRecMagic = 0x7FBADBADu;  // fused records hold bits ^ kRecMagic; 0 = not written
 constexpr uint32_t kPollLimit = 1u << 20;    // bound of a combiner's record polls
+constexpr uint32_t kPollLimitTest = 16;      // the bound under the test hook (a few microseconds)
+
+// A combiner whose bounded poll gave up adds one to a sticky count in the
+// workspace (per combined row), which the host reads back; the row's output
+// is then computed from incomplete records and must not be used.
+__device__ __forceinline__ void count_timeout(uint32_t* timeouts)
+{
+    if (timeouts != nullptr)
+        __hip_atomic_fetch_add(timeouts, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t records_rsrc(const float* base)
 {

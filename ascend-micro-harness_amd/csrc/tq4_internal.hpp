@@ -34,10 +34,13 @@ struct DecodeParams {
     float* records;       // [B][Hq][K][D+4] partial records (may be null when K == 1 fused)
     uint32_t* counters;   // [B][Hkv] split tickets (fused only)
     uint32_t* queue;      // work-queue counter of the persistent fused kernel (or null)
+    uint32_t* timeouts;   // fused: combined rows whose poll gave up (sticky count, or null)
     uint16_t* out;        // [B][Hq][D] bf16 (fused / combine)
     uint32_t B, Hq, Hkv, G, D, S, P, max_blocks, K;
     float scale, inv_sqrt_len;
     uint32_t output_stage, flags;
+    uint32_t poll_limit;  // bound of a combiner's record polls
+    uint32_t withhold;    // test hook: the first-ticket split of a group withholds its record
 };
 
 // mode 0: partials only; mode 1: fused (partials + last-workgroup combine).
@@ -68,6 +71,9 @@ struct Kv4Params {
     const uint16_t* gate;
     float* records;              // [T][Hq][parts][260], zero between calls
     uint32_t* counters;          // [T][H][chunks] part tickets, zero between calls
+    uint32_t* timeouts;          // combined rows whose poll gave up (sticky count)
+    uint32_t poll_limit;         // bound of a combiner's record polls
+    uint32_t withhold;           // test hook: the first-ticket part withholds its records
     uint16_t* out;
     uint32_t T, Hq, H, G, chunks, block_shift, max_blocks, num_blocks, parts, nt;
     float score_scale, inv_gain, inv_sqrt_len;

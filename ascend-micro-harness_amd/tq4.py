@@ -32,6 +32,10 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libtq4.so")
 
 TQ4_DECODE_QUERY_ROTATED = 1
+TQ4_DECODE_TEST_POLL_BOUND = 1 << 30  # test hooks of the bounded wait (include/tq4.h)
+TQ4_DECODE_TEST_WITHHOLD = 1 << 31
+TQ4_KV4FP8_TEST_POLL_BOUND = 1
+TQ4_KV4FP8_TEST_WITHHOLD = 2
 TQ4_MAX_SPLITS = 256
 
 _P = C.c_void_p
@@ -76,6 +80,10 @@ def lib():
     L.tq4_decode_auto_splits.argtypes = [_U32] * 4
     L.tq4_decode_workspace_init.restype = _I32
     L.tq4_decode_workspace_init.argtypes = [_P, _P, _SZ]
+    L.tq4_decode_poll_timeouts.restype = _I32
+    L.tq4_decode_poll_timeouts.argtypes = [_P, _P, _SZ, _U32, _U32, _P]
+    L.tq4_kv4fp8_poll_timeouts.restype = _I32
+    L.tq4_kv4fp8_poll_timeouts.argtypes = [_P, _P, _P, _P]
     L.tq4_paged_decode.restype = _I32
     L.tq4_paged_decode.argtypes = [_P] * 10 + [_SZ, _P] + [_U32] * 8 + [_F32, _F32, _U32, _U32]
     L.tq4_paged_decode_partials.restype = _I32
@@ -127,6 +135,37 @@ def _dev(t, name):
         raise ValueError(f"{name} must be a device tensor")
 
 
+_CACHE_BYTES = (torch.int8, torch.uint8)
+
+
+def _need(what, name, t, dtypes, numel=None, min_numel=None, ndim=None, optional=False):
+    """Refuse (ValueError) a tensor whose dtype or size the kernels would
+    misread: they take raw pointers, so a wrong element type or a short
+    buffer is otherwise an out-of-bounds or garbage read."""
+    if t is None:
+        if optional:
+            return
+        raise ValueError(f"{what}: {name} is required")
+    if t.dtype not in dtypes:
+        names = " or ".join(str(d).replace("torch.", "") for d in dtypes)
+        raise ValueError(f"{what}: {name} must be {names}, got {str(t.dtype).replace('torch.', '')}")
+    if ndim is not None and t.dim() != ndim:
+        raise ValueError(f"{what}: {name} must have {ndim} dimensions, got shape {tuple(t.shape)}")
+    if numel is not None and t.numel() != numel:
+        raise ValueError(f"{what}: {name} must hold {numel} elements, got {t.numel()}")
+    if min_numel is not None and t.numel() < min_numel:
+        raise ValueError(f"{what}: {name} must hold at least {min_numel} elements, "
+                         f"got {t.numel()}")
+
+
+def _check_cache(what, key_cache, value_cache, scale_cache, num_blocks, num_kv_heads,
+                 block_size, head_size):
+    rows = num_blocks * num_kv_heads * block_size
+    _need(what, "key_cache", key_cache, _CACHE_BYTES, min_numel=rows * head_size // 2)
+    _need(what, "value_cache", value_cache, _CACHE_BYTES, min_numel=rows * head_size // 2)
+    _need(what, "scale_cache", scale_cache, (torch.float32,), min_numel=2 * rows)
+
+
 # --------------------------------------------------------------- writers
 def reshape_and_cache_a8(key, value, key_cache, value_cache, scale_cache, slot_mapping,
                          pi_signs=None, tables=None, num_blocks=None, block_size=16,
@@ -155,13 +194,23 @@ def _reshape_and_cache(fn, what, dtype, key, value, key_cache, value_cache, scal
                        inv_sqrt_len, reuse_mode4_flags, stream):
     if key.dtype != dtype or value.dtype != dtype:
         raise ValueError(f"{what}: key/value must be {dtype}")
+    _need(what, "key", key, (dtype,), ndim=3)
+    _need(what, "value", value, (dtype,), numel=key.numel())
+    num_tokens, num_kv_heads, head_size = key.shape
+    if num_blocks is None:
+        num_blocks = key_cache.numel() * 2 // (num_kv_heads * block_size * head_size)
+    _check_cache(what, key_cache, value_cache, scale_cache, num_blocks, num_kv_heads,
+                 block_size, head_size)
+    _need(what, "slot_mapping", slot_mapping, (torch.int32,), min_numel=num_tokens)
+    _need(what, "pi_signs", pi_signs, (torch.float32,), min_numel=head_size, optional=True)
+    # the rotation tables' first column: entry c*32 for channel c, INT8 for
+    # the A8 writer, BF16 (+-1 bit patterns) for the BF16 writer
+    tdt = (torch.int8, torch.uint8) if dtype == torch.int8 else (torch.bfloat16, torch.int16)
+    _need(what, "tables", tables, tdt, min_numel=32 * head_size, optional=True)
     for name, t in (("key", key), ("value", value), ("key_cache", key_cache),
                     ("value_cache", value_cache), ("scale_cache", scale_cache),
                     ("slot_mapping", slot_mapping), ("pi_signs", pi_signs), ("tables", tables)):
         _dev(t, name)
-    num_tokens, num_kv_heads, head_size = key.shape
-    if num_blocks is None:
-        num_blocks = key_cache.numel() * 2 // (num_kv_heads * block_size * head_size)
     if inv_sqrt_len is None:
         inv_sqrt_len = 1.0 / math.sqrt(head_size)
     st = fn(_stream(stream), _ptr(key), _ptr(value), _ptr(key_cache), _ptr(value_cache),
@@ -176,16 +225,29 @@ def reshape_scatter(key, value, key_cache, value_cache, scale_cache, slot_mappin
                     block_size=16, item_begin=0, item_count=None, block_dim=0,
                     inv_sqrt_len=None, stream=None):
     """BF16 tokens at arbitrary slots; items are (request, kv_head)."""
-    for name, t in (("key", key), ("value", value), ("key_cache", key_cache),
-                    ("value_cache", value_cache), ("scale_cache", scale_cache),
-                    ("slot_mapping", slot_mapping), ("pi_signs", pi_signs),
-                    ("cu_seqlens", cu_seqlens), ("launch_probe", launch_probe)):
-        _dev(t, name)
+    what = "reshape_scatter"
+    _need(what, "key", key, (torch.bfloat16,), ndim=3)
+    _need(what, "value", value, (torch.bfloat16,), numel=key.numel())
     num_tokens, num_kv_heads, head_size = key.shape
     if num_requests is None:
         num_requests = (cu_seqlens.numel() - 1) if cu_seqlens is not None else num_tokens
     if num_blocks is None:
         num_blocks = key_cache.numel() * 2 // (num_kv_heads * block_size * head_size)
+    _check_cache(what, key_cache, value_cache, scale_cache, num_blocks, num_kv_heads,
+                 block_size, head_size)
+    _need(what, "slot_mapping", slot_mapping, (torch.int32,), min_numel=num_tokens)
+    _need(what, "pi_signs", pi_signs, (torch.float32,), min_numel=head_size)
+    _need(what, "cu_seqlens", cu_seqlens, (torch.int32,), min_numel=num_requests + 1,
+          optional=True)
+    if cu_seqlens is None and num_requests > num_tokens:
+        raise ValueError(f"{what}: {num_requests} requests of one token each need "
+                         f"{num_requests} tokens, got {num_tokens}")
+    _need(what, "launch_probe", launch_probe, (torch.int32,), min_numel=32, optional=True)
+    for name, t in (("key", key), ("value", value), ("key_cache", key_cache),
+                    ("value_cache", value_cache), ("scale_cache", scale_cache),
+                    ("slot_mapping", slot_mapping), ("pi_signs", pi_signs),
+                    ("cu_seqlens", cu_seqlens), ("launch_probe", launch_probe)):
+        _dev(t, name)
     if item_count is None:
         item_count = num_requests * num_kv_heads
     if inv_sqrt_len is None:
@@ -209,6 +271,16 @@ def auto_splits(num_seqs, num_kv_heads, max_blocks_per_seq, block_size):
                                             block_size))
 
 
+def decode_workspace_init(workspace, stream=None):
+    """Zero a fused-decode workspace in stream order (tq4_decode_workspace_init):
+    before its first use, and again after a reported poll timeout."""
+    _dev(workspace, "workspace")
+    _check(lib().tq4_decode_workspace_init(_stream(stream), _ptr(workspace),
+                                           workspace.numel() * workspace.element_size()),
+           "decode_workspace_init")
+    return workspace
+
+
 def decode_workspace(num_seqs, num_heads, num_kv_heads, head_size, num_splits=0, device="cuda",
                      stream=None):
     """A zero-initialised workspace (counters at zero) for tq4_paged_decode."""
@@ -219,11 +291,56 @@ def decode_workspace(num_seqs, num_heads, num_kv_heads, head_size, num_splits=0,
     return ws
 
 
+def _check_decode_inputs(what, q, key_cache, value_cache, scale_cache, block_tables,
+                         context_lens, pi_signs, num_kv_heads, block_size, num_blocks,
+                         pi_needed=True):
+    """The decode's operand contract (include/tq4.h): q BF16 [B][Hq][d];
+    block_tables int32 [B][max_blocks]; context_lens int32 [B]; the caches as
+    the writer leaves them; pi_signs FP32 [d]."""
+    _need(what, "q", q, (torch.bfloat16,), ndim=3)
+    B, Hq, d = q.shape
+    _check_cache(what, key_cache, value_cache, scale_cache, num_blocks, num_kv_heads,
+                 block_size, d)
+    _need(what, "block_tables", block_tables, (torch.int32,), ndim=2)
+    if block_tables.shape[0] != B:
+        raise ValueError(f"{what}: block_tables must have {B} rows (one per sequence), "
+                         f"got shape {tuple(block_tables.shape)}")
+    _need(what, "context_lens", context_lens, (torch.int32,), numel=B)
+    _need(what, "pi_signs", pi_signs, (torch.float32,), min_numel=d, optional=not pi_needed)
+
+
+def _read_count(fn, what, stream):
+    """Copy a 32-bit device count to pinned host memory in stream order, wait
+    for the stream, return it."""
+    host = torch.zeros(1, dtype=torch.int32, pin_memory=True)
+    _check(fn(_P(host.data_ptr())), what)
+    s = torch.cuda.current_stream() if stream is None else stream
+    s.synchronize()
+    return int(host[0]) & 0xFFFFFFFF
+
+
+def decode_poll_timeouts(workspace, num_seqs, num_kv_heads, stream=None):
+    """Rows whose fused-decode combiner gave up its bounded poll since the
+    workspace was last zeroed (tq4_decode_poll_timeouts). Nonzero: those
+    outputs are invalid and the workspace must be zeroed again. Synchronises
+    the stream."""
+    _dev(workspace, "workspace")
+    nbytes = workspace.numel() * workspace.element_size()
+    return _read_count(lambda dst: lib().tq4_decode_poll_timeouts(
+        _stream(stream), _ptr(workspace), nbytes, num_seqs, num_kv_heads, dst),
+        "decode_poll_timeouts", stream)
+
+
 def paged_decode(q, key_cache, value_cache, scale_cache, block_tables, context_lens, pi_signs,
                  num_kv_heads, block_size, num_blocks, out=None, workspace=None, gate=None,
                  num_splits=0, scale=None, inv_sqrt_len=None, output_stage=1, flags=0,
                  stream=None):
     """Fused split-K decode: q [B][Hq][d] bf16 -> out [B][Hq][d] bf16."""
+    _check_decode_inputs("paged_decode", q, key_cache, value_cache, scale_cache, block_tables,
+                         context_lens, pi_signs, num_kv_heads, block_size, num_blocks,
+                         pi_needed=output_stage >= 1 or not (flags & TQ4_DECODE_QUERY_ROTATED))
+    _need("paged_decode", "gate", gate, (torch.float32,), numel=q.numel(), optional=True)
+    _need("paged_decode", "out", out, (torch.bfloat16,), numel=q.numel(), optional=True)
     for name, t in (("q", q), ("key_cache", key_cache), ("value_cache", value_cache),
                     ("scale_cache", scale_cache), ("block_tables", block_tables),
                     ("context_lens", context_lens), ("pi_signs", pi_signs), ("gate", gate),
@@ -255,7 +372,17 @@ def paged_decode_partials(q, key_cache, value_cache, scale_cache, block_tables, 
                           pi_signs, num_kv_heads, block_size, num_blocks, num_splits,
                           workspace=None, scale=None, inv_sqrt_len=None, flags=0, stream=None):
     """Partial records [B][Hq][K][d+4] = (m, l, 0, 0, acc[d]) per split."""
+    _check_decode_inputs("paged_decode_partials", q, key_cache, value_cache, scale_cache,
+                         block_tables, context_lens, pi_signs, num_kv_heads, block_size,
+                         num_blocks, pi_needed=not (flags & TQ4_DECODE_QUERY_ROTATED))
     B, Hq, d = q.shape
+    _need("paged_decode_partials", "workspace", workspace, (torch.float32,),
+          min_numel=B * Hq * num_splits * (d + 4), optional=True)
+    for name, t in (("q", q), ("key_cache", key_cache), ("value_cache", value_cache),
+                    ("scale_cache", scale_cache), ("block_tables", block_tables),
+                    ("context_lens", context_lens), ("pi_signs", pi_signs),
+                    ("workspace", workspace)):
+        _dev(t, name)
     if scale is None:
         scale = 1.0 / math.sqrt(d)
     if inv_sqrt_len is None:
@@ -275,6 +402,17 @@ def paged_decode_partials(q, key_cache, value_cache, scale_cache, block_tables, 
 def splitk_combine(workspace, pi_signs, num_seqs, num_heads, head_size, num_splits, out=None,
                    gate=None, inv_sqrt_len=None, output_stage=1, stream=None):
     """LSE combine + egress of partial records into BF16 [B][Hq][d]."""
+    what = "splitk_combine"
+    rows = num_seqs * num_heads
+    _need(what, "workspace", workspace, (torch.float32,),
+          min_numel=rows * num_splits * (head_size + 4))
+    _need(what, "pi_signs", pi_signs, (torch.float32,), min_numel=head_size,
+          optional=output_stage == 0)
+    _need(what, "gate", gate, (torch.float32,), numel=rows * head_size, optional=True)
+    _need(what, "out", out, (torch.bfloat16,), numel=rows * head_size, optional=True)
+    for name, t in (("workspace", workspace), ("pi_signs", pi_signs), ("gate", gate),
+                    ("out", out)):
+        _dev(t, name)
     if out is None:
         out = torch.empty((num_seqs, num_heads, head_size), dtype=torch.bfloat16,
                           device=workspace.device)
@@ -329,10 +467,12 @@ __all__ = [
     "TQ4Error", "lib", "status_string", "reshape_and_cache_a8", "reshape_and_cache_bf16",
     "reshape_scatter", "decode_workspace_bytes", "auto_splits", "decode_workspace",
     "paged_decode", "paged_decode_partials", "splitk_combine", "icdf_quantize",
+    "decode_workspace_init",
     "lloydmax_quantize", "TQ4_DECODE_QUERY_ROTATED", "TQ4_MAX_SPLITS",
     "Kv4Fp8Launch", "Kv4Fp8Buffers", "Kv4Fp8RawQueryBuffers", "fused_decode_opt_launch",
     "kv4fp8_workspace_bytes", "kv4fp8_workspace_init", "kv4fp8_decode", "kv4fp8_decode_raw_query",
-    "fp8_e4m3_round",
+    "fp8_e4m3_round", "decode_poll_timeouts", "kv4fp8_poll_timeouts", "TQ4_DECODE_TEST_POLL_BOUND",
+    "TQ4_DECODE_TEST_WITHHOLD", "TQ4_KV4FP8_TEST_POLL_BOUND", "TQ4_KV4FP8_TEST_WITHHOLD",
 ]
 
 
@@ -347,7 +487,8 @@ class Kv4Fp8Launch(C.Structure):
         [("scale", _F32), ("inv_sqrt_len", _F32)] + \
         [(n, _U32) for n in ("prologue_vectors_per_block", "prologue_cube_chunk_vectors",
                              "output_stage", "element_type", "probe_page", "probe_tile",
-                             "num_blocks")] + [("workspace_bytes", C.c_uint64)]
+                             "num_blocks")] + [("workspace_bytes", C.c_uint64),
+                                               ("test_flags", _U32)]
 
 
 class Kv4Fp8Buffers(C.Structure):
@@ -390,6 +531,19 @@ def kv4fp8_workspace_bytes(launch):
     return int(lib().tq4_kv4fp8_workspace_bytes(C.byref(launch)))
 
 
+def kv4fp8_poll_timeouts(workspace, tokens, heads, kv_heads, block_size, max_blocks,
+                         num_blocks, stream=None):
+    """Rows whose KV4/FP8 combiner gave up its bounded poll since the
+    workspace was last zeroed (tq4_kv4fp8_poll_timeouts), for a workspace
+    sized for this geometry. Synchronises the stream."""
+    _dev(workspace, "workspace")
+    L = fused_decode_opt_launch(tokens, heads, kv_heads, block_size, max_blocks,
+                                num_blocks=num_blocks)
+    L.workspace_bytes = workspace.numel() * workspace.element_size()
+    return _read_count(lambda dst: lib().tq4_kv4fp8_poll_timeouts(
+        _stream(stream), C.byref(L), _ptr(workspace), dst), "kv4fp8_poll_timeouts", stream)
+
+
 def kv4fp8_workspace_init(workspace, stream=None):
     """Zero a KV4/FP8 decode workspace (tq4_kv4fp8_workspace_init): needed
     once before its first call; every call leaves it zero again."""
@@ -398,6 +552,23 @@ def kv4fp8_workspace_init(workspace, stream=None):
                                            workspace.numel() * workspace.element_size()),
            "kv4fp8_workspace_init")
     return workspace
+
+
+def _kv4_check(what, q, key_cache, value_cache, scales, block_table, context_lens, kv_heads,
+               block_size, num_blocks):
+    """The KV4/FP8 operand contract (include/tq4_kv4fp8.h): NZ byte pools of
+    num_blocks * block_size * kv_heads * 128 bytes, an eight-lane FP32 scale
+    slot per row, int32 tables [T][max_blocks] and lengths [T]."""
+    T = q.shape[0]
+    rows = num_blocks * block_size
+    _need(what, "key_cache", key_cache, _CACHE_BYTES, min_numel=rows * kv_heads * 128)
+    _need(what, "value_cache", value_cache, _CACHE_BYTES, min_numel=rows * kv_heads * 128)
+    _need(what, "scales", scales, (torch.float32,), min_numel=rows * 8)
+    _need(what, "block_table", block_table, (torch.int32,), ndim=2)
+    if block_table.shape[0] != T:
+        raise ValueError(f"{what}: block_table must have {T} rows, got shape "
+                         f"{tuple(block_table.shape)}")
+    _need(what, "context_lens", context_lens, (torch.int32,), numel=T)
 
 
 def _kv4_prepare(launch, tensors, workspace, device, stream):
@@ -415,8 +586,14 @@ def _kv4_prepare(launch, tensors, workspace, device, stream):
 def kv4fp8_decode(query, key_cache, value_cache, scales, block_table, context_lens, kv_heads,
                   block_size, num_blocks, out=None, workspace=None, out_dtype=torch.float16,
                   splits=1, heads_per_task=16, fused_context_limit=4096, scale=None,
-                  inv_sqrt_len=None, stream=None):
-    """The pre-rotated entry: query FP32 [T][Hq][256] -> out [T][Hq][256] (FP16/BF16)."""
+                  inv_sqrt_len=None, test_flags=0, stream=None):
+    """The pre-rotated entry: query FP32 [T][Hq][256] -> out [T][Hq][256] (FP16/BF16).
+    test_flags: the bounded wait's test hooks (TQ4_KV4FP8_TEST_*), 0 in use."""
+    what = "kv4fp8_decode"
+    _need(what, "query", query, (torch.float32,), ndim=3)
+    _kv4_check(what, query, key_cache, value_cache, scales, block_table, context_lens,
+               kv_heads, block_size, num_blocks)
+    _need(what, "out", out, (torch.float16, torch.bfloat16), numel=query.numel(), optional=True)
     T, Hq, d = query.shape
     element = 1 if (out.dtype if out is not None else out_dtype) == torch.bfloat16 else 0
     if out is None:
@@ -426,6 +603,7 @@ def kv4fp8_decode(query, key_cache, value_cache, scales, block_table, context_le
                                 1.0 / math.sqrt(d) if scale is None else scale,
                                 1.0 / math.sqrt(d) if inv_sqrt_len is None else inv_sqrt_len,
                                 0, element, False, num_blocks)
+    L.test_flags = test_flags
     workspace = _kv4_prepare(L, (("query", query), ("key_cache", key_cache),
                                  ("value_cache", value_cache), ("scales", scales),
                                  ("block_table", block_table), ("context_lens", context_lens),
@@ -444,6 +622,16 @@ def kv4fp8_decode_raw_query(raw_query, pi_signs, key_cache, value_cache, scales,
                             inv_sqrt_len=None, stream=None):
     """The raw-query entry: raw_query FP16/BF16 [T][Hq][256] in the original
     basis -> out (same element type); query_out receives the rotated FP32 query."""
+    what = "kv4fp8_decode_raw_query"
+    _need(what, "raw_query", raw_query, (torch.float16, torch.bfloat16), ndim=3)
+    _kv4_check(what, raw_query, key_cache, value_cache, scales, block_table, context_lens,
+               kv_heads, block_size, num_blocks)
+    _need(what, "pi_signs", pi_signs, (torch.float32,), min_numel=raw_query.shape[2])
+    # the gate and the output share the raw query's element type
+    _need(what, "gate", gate, (raw_query.dtype,), numel=raw_query.numel(), optional=True)
+    _need(what, "out", out, (raw_query.dtype,), numel=raw_query.numel(), optional=True)
+    _need(what, "query_out", query_out, (torch.float32,), numel=raw_query.numel(),
+          optional=True)
     T, Hq, d = raw_query.shape
     element = 1 if raw_query.dtype == torch.bfloat16 else 0
     if out is None:

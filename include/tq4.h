@@ -46,7 +46,8 @@ typedef enum {
     TQ4_ERR_ROTATION = -8,      /* neither pi_signs nor tables given */
     TQ4_ERR_LAUNCH = -9,        /* the HIP runtime refused the launch */
     TQ4_ERR_RANGE = -10,        /* a size exceeds what the kernels index */
-    TQ4_ERR_CODEBOOK = -11      /* codebook leaf: bits, mode or element count */
+    TQ4_ERR_CODEBOOK = -11,     /* codebook leaf: bits, mode or element count */
+    TQ4_ERR_FLAGS = -12         /* unknown flag bits, or a test hook without its bound */
 } tq4_status;
 
 /* Human-readable name of a tq4_status. */
@@ -139,6 +140,14 @@ int tq4_reshape_scatter(void* stream, uint32_t block_dim, const uint16_t* key,
  * flags: TQ4_DECODE_QUERY_ROTATED = q already holds Pi q (no rotation).
  */
 #define TQ4_DECODE_QUERY_ROTATED 1u
+/* Test hooks of the fused entry's bounded wait (never set in production):
+ * TQ4_DECODE_TEST_POLL_BOUND cuts a combiner's record poll to 16 attempts
+ * (from 2^20); TQ4_DECODE_TEST_WITHHOLD (accepted only together with the
+ * bound) makes the split holding ticket 0 of every (seq, kv head) with more
+ * than one live split skip its record, so that group's combiner gives up and
+ * is counted (tq4_decode_poll_timeouts). Every workgroup still exits. */
+#define TQ4_DECODE_TEST_POLL_BOUND (1u << 30)
+#define TQ4_DECODE_TEST_WITHHOLD (1u << 31)
 #define TQ4_MAX_SPLITS 256u
 /* A split walks at most this many 16-token strips (its block-table window is
  * staged on chip): num_splits must be at least
@@ -163,6 +172,19 @@ uint32_t tq4_decode_auto_splits(uint32_t num_seqs, uint32_t num_kv_heads,
  * workspace that tq4_paged_decode_partials has written since must be zeroed
  * again before tq4_paged_decode uses it. */
 int tq4_decode_workspace_init(void* stream, void* workspace, size_t workspace_bytes);
+
+/* The fused entry's timeout count: rows (times 16-split record chunks) whose
+ * combiner stopped polling at its bound with records still missing, summed
+ * over every call since the workspace was last zeroed. Nonzero means those
+ * calls' outputs include rows combined from incomplete records, and the
+ * workspace no longer holds the all-zero state the next call needs: zero it
+ * again (tq4_decode_workspace_init). The count is copied to *count
+ * (host or device memory) in stream order; read it after synchronising the
+ * stream. num_seqs and num_kv_heads are those the workspace was sized for.
+ * Reports the reference's watchdog timeout to the host
+ * (kernels/ops/turboquant/turboquant_splitk_reduce.cpp:34-45). */
+int tq4_decode_poll_timeouts(void* stream, const void* workspace, size_t workspace_bytes,
+                             uint32_t num_seqs, uint32_t num_kv_heads, uint32_t* count);
 
 /* Fused decode: partials, then one workgroup of each (seq, kv head) -- the
  * last of its splits to start -- waits for the others' records, LSE-combines

@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-/* ascend_micro::fused_decode_opt::Launch, field for field, followed by two
+/* ascend_micro::fused_decode_opt::Launch, field for field, followed by three
  * fields of this library:
  *   num_blocks       physical pages in the key/value/scale caches; every page
  *                    index read from the block table is checked against it
@@ -47,7 +47,15 @@ extern "C" {
  *                    skipped -- the reference refuses such a table in its
  *                    host tiling, build_decode_tiling's kUnmappedPage);
  *   workspace_bytes  the size of buffers->workspace
- *                    (>= tq4_kv4fp8_workspace_bytes(launch)).
+ *                    (>= tq4_kv4fp8_workspace_bytes(launch));
+ *   test_flags       0 in production. Test hooks of the combiners' bounded
+ *                    wait: TQ4_KV4FP8_TEST_POLL_BOUND cuts a combiner's
+ *                    record poll to 16 attempts (from 2^20);
+ *                    TQ4_KV4FP8_TEST_WITHHOLD (only with the bound) makes the
+ *                    part holding ticket 0 of every group with more than one
+ *                    live part skip its record exports, so the combiners that
+ *                    need them give up and are counted
+ *                    (tq4_kv4fp8_poll_timeouts). Every workgroup still exits.
  * grid, tasks_per_block and reduce_tasks_per_block are the NPU dispatch; they
  * are checked as valid_launch checks them (except its grid <= 32 bound) and
  * do not change the result. heads_per_task, splits and fused_context_limit
@@ -66,7 +74,11 @@ typedef struct tq4_kv4fp8_launch {
     uint32_t probe_page, probe_tile;
     uint32_t num_blocks;
     uint64_t workspace_bytes;
+    uint32_t test_flags;
 } tq4_kv4fp8_launch;
+
+#define TQ4_KV4FP8_TEST_POLL_BOUND 1u
+#define TQ4_KV4FP8_TEST_WITHHOLD 2u
 
 /* ascend_micro::fused_decode_opt::Buffers. query: FP32 [tokens][heads][256]
  * in the rotated basis; block_table int32 [tokens][max_blocks];
@@ -90,8 +102,9 @@ typedef struct tq4_kv4fp8_raw_query_buffers {
 } tq4_kv4fp8_raw_query_buffers;
 
 /* Workspace this decode needs for `launch` (bytes, 256-aligned): a part
- * ticket per (token, kv head, 16-head chunk) and the partial records of every
- * (token, q head, part). It must be zero before its first call
+ * ticket per (token, kv head, 16-head chunk), the partial records of every
+ * (token, q head, part) and a 256-byte status block (the poll-timeout count).
+ * It must be zero before its first call
  * (tq4_kv4fp8_workspace_init); every call leaves it zero again, so one
  * workspace serves calls of any geometry it is large enough for. Calls that
  * overlap in time need their own workspaces. */
@@ -101,6 +114,19 @@ uint64_t tq4_kv4fp8_workspace_bytes(const tq4_kv4fp8_launch* launch);
  * graph). workspace 16-byte aligned. No reference counterpart: the
  * reference's host code allocates its workspace per call. */
 int tq4_kv4fp8_workspace_init(void* stream, void* workspace, uint64_t workspace_bytes);
+
+/* The combiners' timeout count: rows whose bounded record poll gave up with
+ * records still missing, summed over every call since the workspace was
+ * zeroed. Nonzero means those calls' outputs include rows merged from
+ * incomplete records (possible only when a combiner waits on a part that
+ * cannot start, e.g. a process confined to fewer compute units than the
+ * device reports), and the workspace must be zeroed again before the next
+ * call. Copied to *count (host or device memory) in stream order; read it
+ * after synchronising the stream. `launch` is the one the workspace was
+ * sized for (workspace_bytes set). Reports the reference's watchdog timeout
+ * to the host (kernels/ops/turboquant/turboquant_splitk_reduce.cpp:34-45). */
+int tq4_kv4fp8_poll_timeouts(void* stream, const tq4_kv4fp8_launch* launch,
+                             const void* workspace, uint32_t* count);
 
 /* The pre-rotated entry (launch_fused_decode_opt): output_stage is not read. */
 int tq4_kv4fp8_decode(void* stream, const tq4_kv4fp8_launch* launch,

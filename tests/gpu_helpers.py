@@ -43,3 +43,14 @@ def bf16_out_error(got_bits, want_f32):
     want = bf16_to_f32(f32_to_bf16(want_f32)).astype(np.float64)
     diff = np.abs(got - want)
     return float(diff.max()), float(diff.sum() / max(np.abs(want).sum(), 1e-30))
+
+
+# (label, max-abs, mean-rel, max-abs budget, mean-rel budget) of every decode
+# output compared; conftest prints them as fractions of the budget at the end
+# of the session, the way the reference rig reports its margins
+# (tests/npu/turboquant_splitk_rigs.hpp:103-215).
+MARGINS = []
+
+
+def record_margin(label, mx, mr, mx_budget, mr_budget):
+    MARGINS.append((str(label), float(mx), float(mr), float(mx_budget), float(mr_budget)))

@@ -34,7 +34,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 def test_status_strings_and_version(lib):
     assert lib.tq4_status_string(0) == b"ok"
-    for st in range(-11, 0):
+    for st in range(-12, 0):
         assert lib.tq4_status_string(st) != b"unknown status"
     assert lib.tq4_version() >> 16 == 1
 
@@ -166,3 +166,27 @@ def test_kv4fp8_refusals_and_workspace(tq4, lib):
     x.prologue_vectors_per_block = 0
     assert raw(x) == -3                                    # prologue share
     assert lib.tq4_fp8_e4m3_round(None, d, d, 3) == -10   # odd count
+
+
+def test_flag_and_timeout_refusals(lib):
+    """Unknown decode flags, the withhold hook without its poll bound, and a
+    timeout read of a missing or too small workspace are refused before any
+    HIP call."""
+    d = C.c_void_p(16)
+    dec = lib.tq4_paged_decode
+    ws = 1 << 20
+
+    def call(flags):
+        return dec(None, d, d, d, d, d, d, d, None, d, ws, d, 1, 8, 2, 128, 16, 64, 4, 2,
+                   C.c_float(0.1), C.c_float(0.1), 1, flags)
+    assert call(1 << 5) == -12
+    assert call(1 << 31) == -12                      # withhold without the bound
+    part = lib.tq4_paged_decode_partials
+    assert part(None, d, d, d, d, d, d, d, d, ws, 1, 8, 2, 128, 16, 64, 4, 2, C.c_float(0.1),
+                C.c_float(0.1), 1 << 30) == -12       # partials: no poll, no hook
+    cnt = C.c_uint32(0)
+    to = lib.tq4_decode_poll_timeouts
+    assert to(None, None, ws, 1, 2, C.byref(cnt)) == -1
+    assert to(None, d, ws, 1, 2, None) == -1
+    assert to(None, d, 100, 1, 2, C.byref(cnt)) == -6  # smaller than the tail
+    assert to(None, d, ws, 0, 2, C.byref(cnt)) == -6

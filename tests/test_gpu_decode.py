@@ -17,7 +17,7 @@ import math
 import numpy as np
 import pytest
 
-from gpu_helpers import bf16_out_error, canary_bytes, canary_floats, dev, host
+from gpu_helpers import bf16_out_error, canary_bytes, canary_floats, dev, host, record_margin
 from oracle_bindings import FLAG_QUERY_ROTATED, IN_BF16, bf16_to_f32, f32_to_bf16
 
 pytestmark = pytest.mark.gpu
@@ -81,10 +81,11 @@ def run_decode(tq4, oracle, rng, ctx_lens, Hq, H, d, S, P, K, stage=1, gate=None
     return host(out), want, (q, kc, vc, sc, tables, ctx, signs, isl, scale)
 
 
-def check_out(got, want, label=""):
+def check_out(got, want, label="", max_abs=MAX_ABS, mean_rel=MEAN_REL):
     mx, mr = bf16_out_error(got, want)
+    record_margin(label, mx, mr, max_abs, mean_rel)
     assert np.all(np.isfinite(bf16_to_f32(got))), f"{label}: non-finite output"
-    assert mx <= MAX_ABS and mr <= MEAN_REL, f"{label}: max-abs {mx:.3g} mean-rel {mr:.3g}"
+    assert mx <= max_abs and mr <= mean_rel, f"{label}: max-abs {mx:.3g} mean-rel {mr:.3g}"
     return mx, mr
 
 
@@ -96,12 +97,14 @@ def test_config3_single_sequence_ctx4096(tq4, oracle):
 
 
 @pytest.mark.parametrize("ctx", [4096, 16384, 4103])
-@pytest.mark.parametrize("K", [2, 4, 8, 16])
+@pytest.mark.parametrize("K", [2, 4, 8, 16, 0])
 def test_config4_split_sweep(tq4, oracle, ctx, K):
-    """split-K sweep incl. ragged ctx 4103 (NaN canaries in the tail)."""
+    """split-K sweep incl. ragged ctx 4103 (NaN canaries
+    in the tail); K = 0 is the auto count the bench times."""
     rng = np.random.default_rng(0x71340004 + ctx + K)
-    got, want, _ = run_decode(tq4, oracle, rng, [ctx], 32, 8, 128, 16, (ctx + 15) // 16 + 8, K)
-    check_out(got, want, f"ctx {ctx} K {K}")
+    kk = K or tq4.auto_splits(1, 8, (ctx + 15) // 16, 16)
+    got, want, _ = run_decode(tq4, oracle, rng, [ctx], 32, 8, 128, 16, (ctx + 15) // 16 + 8, kk)
+    check_out(got, want, f"ctx {ctx} K {kk}{' (auto)' if K == 0 else ''}")
 
 
 @pytest.mark.parametrize("K", [24, 40, 64])
@@ -128,10 +131,29 @@ def test_multi_chunk_combine_one_launch(tq4, oracle, K):
         check_out(host(out), want, f"K {K} call {call}")
 
 
-def test_config4_ctx32768(tq4, oracle):
+@pytest.fixture(scope="module")
+def long_context(oracle):
+    """One ctx-32768 sequence (configs[3]'s longest), cache built once."""
     rng = np.random.default_rng(0x71340004)
-    got, want, _ = run_decode(tq4, oracle, rng, [32768], 32, 8, 128, 16, 2048 + 8, 16)
-    check_out(got, want, "ctx 32768")
+    P = 2048 + 8
+    kc, vc, sc, tables, signs, isl = build_cache(oracle, rng, [32768], 8, 128, 16, P)
+    q = f32_to_bf16(rng.standard_normal((1, 32, 128)).astype(np.float32))
+    return P, q, kc, vc, sc, tables, signs, isl
+
+
+@pytest.mark.parametrize("K", [2, 4, 8, 16, 32, 0])
+def test_config4_ctx32768(tq4, oracle, long_context, K):
+    """configs[3] at ctx 32768, every split count of the sweep and the auto
+    count the bench times there (0 = tq4_decode_auto_splits)."""
+    P, q, kc, vc, sc, tables, signs, isl = long_context
+    ctx = np.array([32768], np.int32)
+    kk = K or tq4.auto_splits(1, 8, tables.shape[1], 16)
+    scale = np.float32(1.0 / math.sqrt(128))
+    _, want = oracle.paged_decode(q, kc, vc, sc, tables, ctx, signs, None, 32, 8, 128, 16, P,
+                                  kk, scale, isl, 1, threads=16)
+    out = tq4.paged_decode(dev(q), dev(kc), dev(vc), dev(sc), dev(tables), dev(ctx), dev(signs),
+                           8, 16, P, num_splits=K, scale=float(scale), inv_sqrt_len=float(isl))
+    check_out(host(out), want, f"ctx 32768 K {kk}{' (auto)' if K == 0 else ''}")
 
 
 @pytest.mark.parametrize("G", [1, 4, 6, 16])

@@ -73,6 +73,27 @@ def test_bf16_integer_equals_a8(tq4, oracle, d):
     assert_images_equal(bf, a8)
 
 
+def test_config2_bf16_integer_1024(tq4, oracle):
+    """BASELINE config 2 (integer run): 1024 BF16 tokens with integer values
+    in [-64, 64] into the 4096-page pool at permuted pages must equal the A8
+    writer on the same integers byte for byte, and the oracle."""
+    rng = np.random.default_rng(0x71340012)
+    H, d, S, P, T = 8, 128, 16, 4096, 1024
+    ints = rng.integers(-64, 65, (2, T, H, d), dtype=np.int8)
+    pages = rng.permutation(P)[: T // 16]
+    slots = (pages[:, None] * 16 + np.arange(16)).reshape(-1).astype(np.int32)
+    signs = oracle.canonical_signs(d)
+    a8, want, skipped = run_pair(tq4, oracle, IN_INT8, ints[0], ints[1], slots, H, d, S, P,
+                                 signs=signs)
+    assert skipped == 0
+    bf, want_bf, _ = run_pair(tq4, oracle, IN_BF16, f32_to_bf16(ints[0].astype(np.float32)),
+                              f32_to_bf16(ints[1].astype(np.float32)), slots, H, d, S, P,
+                              signs=signs)
+    assert_images_equal(a8, want)
+    assert_images_equal(bf, want_bf)
+    assert_images_equal(bf, a8)
+
+
 def test_config2_bf16_normal_1024(tq4, oracle):
     """BASELINE config 2 (N(0,1) run): 1024 tokens, 4096-page pool, permuted pages."""
     rng = np.random.default_rng(0x71340002)
