@@ -73,6 +73,8 @@ const char* tq4_status_string(int status)
         case TQ4_ERR_RANGE: return "a size exceeds the kernels' index range";
         case TQ4_ERR_CODEBOOK: return "codebook leaf: bits must be 2 or 4, mode 0..5, elements a multiple of 8";
         case TQ4_ERR_FLAGS: return "unknown flag bits, or a test hook without its poll bound";
+        case TQ4_ERR_SCRATCH:
+            return "the call needs more than the no-allocation entry's 16 MiB static scratch";
         default: return "unknown status";
     }
 }
@@ -316,6 +318,48 @@ int tq4_paged_decode(void* stream, const uint16_t* q, const int8_t* key_cache,
         p.timeouts = p.queue + 1;
     }
     return launched(tq4::launch_decode((hipStream_t)stream, p, 1));
+}
+
+int tq4_paged_decode_noalloc(void* stream, const uint16_t* q, const int8_t* key_cache,
+                             const int8_t* value_cache, const float* scale_cache,
+                             const int32_t* block_tables, const int32_t* context_lens,
+                             const float* pi_signs, const float* gate, uint16_t* out,
+                             uint32_t num_seqs, uint32_t num_heads, uint32_t num_kv_heads,
+                             uint32_t head_size, uint32_t block_size, uint32_t num_blocks,
+                             uint32_t max_blocks_per_seq, uint32_t num_splits, float scale,
+                             float inv_sqrt_len, uint32_t output_stage, uint32_t flags)
+{
+    // Everything tq4_paged_decode refuses is refused here first, so a call
+    // that would not fit the static scratch is refused before any HIP call.
+    int rc = decode_checks(q, key_cache, value_cache, scale_cache, block_tables, context_lens,
+                           pi_signs, num_seqs, num_heads, num_kv_heads, head_size, block_size,
+                           num_blocks, max_blocks_per_seq, flags);
+    if (rc != TQ4_OK) return rc;
+    if (flags & ~TQ4_DECODE_QUERY_ROTATED) return TQ4_ERR_FLAGS;  // no test hooks here
+    if (!out) return TQ4_ERR_NULL_POINTER;
+    if (output_stage > 2 || (output_stage == 2 && !gate)) return TQ4_ERR_OUTPUT_STAGE;
+    if (output_stage >= 1 && !pi_signs) return TQ4_ERR_ROTATION;
+    if (num_splits == 0)
+        num_splits = tq4_decode_auto_splits(num_seqs, num_kv_heads, max_blocks_per_seq, block_size);
+    if (num_splits > TQ4_MAX_SPLITS || !split_pages_ok(max_blocks_per_seq, block_size, num_splits))
+        return TQ4_ERR_SPLITS;
+    if ((uint64_t)num_seqs * num_kv_heads * num_splits > 0x7fffffffull) return TQ4_ERR_RANGE;
+    void* ws = nullptr;
+    if (num_splits > 1) {
+        if (tq4_decode_workspace_bytes(num_seqs, num_heads, num_kv_heads, head_size,
+                                       num_splits) > tq4::kNoAllocScratchBytes)
+            return TQ4_ERR_SCRATCH;
+        if (tq4::noalloc_scratch((hipStream_t)stream, &ws) != hipSuccess) return TQ4_ERR_LAUNCH;
+    }
+    // The whole scratch is the workspace: its tail (queue, timeout word,
+    // tickets) sits at the end whatever the geometry, and between calls
+    // every word the decode uses is zero again, so calls of any geometry
+    // can follow each other.
+    return tq4_paged_decode(stream, q, key_cache, value_cache, scale_cache, block_tables,
+                            context_lens, pi_signs, gate, ws, ws ? tq4::kNoAllocScratchBytes : 0,
+                            out, num_seqs, num_heads, num_kv_heads, head_size, block_size,
+                            num_blocks, max_blocks_per_seq, num_splits, scale, inv_sqrt_len,
+                            output_stage, flags);
 }
 
 int tq4_paged_decode_partials(void* stream, const uint16_t* q, const int8_t* key_cache,

@@ -54,6 +54,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <mutex>
+
 #include "../../include/tq4.h"
 #include "tq4_device.hpp"
 #include "tq4_internal.hpp"
@@ -1273,6 +1275,41 @@ hipError_t launch_combine(hipStream_t stream, const DecodeParams& p)
         case 256: return launch_combine_t<256>(stream, p);
         default: return hipErrorInvalidValue;
     }
+}
+
+// The no-allocation decode's workspace: a static device array, one copy per
+// GPU the library runs on, held until the process ends. In host code its
+// name is only a stand-in; its device address comes from
+// hipGetSymbolAddress, once per device, and only that address is handed to
+// kernels and fills.
+static __device__ __align__(256) uint32_t scratch[kNoAllocScratchBytes / sizeof(uint32_t)];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices] = {};
+}  // namespace
+
+hipError_t noalloc_scratch(hipStream_t stream, void** ptr)
+{
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        if (p == nullptr) return hipErrorInvalidSymbol;
+        // the decode's tickets, queue and records start at zero; every call
+        // leaves them zero again (a fill kernel: it may be captured)
+        e = launch_fill_zero(stream, p, kNoAllocScratchBytes);
+        if (e != hipSuccess) return e;
+        g_scratch_ptr[dev] = p;
+    }
+    *ptr = g_scratch_ptr[dev];
+    return hipSuccess;
 }
 
 hipError_t launch_fill_zero(hipStream_t stream, void* ptr, size_t bytes)

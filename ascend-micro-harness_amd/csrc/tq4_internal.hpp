@@ -86,4 +86,10 @@ hipError_t launch_fp8_probe(hipStream_t stream, const float* in, uint16_t* out, 
 // Byte offset of the counter region inside a workspace of K splits.
 size_t decode_records_bytes(uint32_t B, uint32_t Hq, uint32_t D, uint32_t K);
 
+// The no-allocation decode's static scratch (tq4_decode.hip): its size, and
+// its device address on the current device (set up, and zeroed on `stream`,
+// at the first call on each device).
+constexpr size_t kNoAllocScratchBytes = (size_t)16 << 20;
+hipError_t noalloc_scratch(hipStream_t stream, void** ptr);
+
 }  // namespace tq4

@@ -86,6 +86,8 @@ def lib():
     L.tq4_kv4fp8_poll_timeouts.argtypes = [_P, _P, _P, _P]
     L.tq4_paged_decode.restype = _I32
     L.tq4_paged_decode.argtypes = [_P] * 10 + [_SZ, _P] + [_U32] * 8 + [_F32, _F32, _U32, _U32]
+    L.tq4_paged_decode_noalloc.restype = _I32
+    L.tq4_paged_decode_noalloc.argtypes = [_P] * 10 + [_U32] * 8 + [_F32, _F32, _U32, _U32]
     L.tq4_paged_decode_partials.restype = _I32
     L.tq4_paged_decode_partials.argtypes = [_P] * 9 + [_SZ] + [_U32] * 8 + [_F32, _F32, _U32]
     L.tq4_splitk_combine.restype = _I32
@@ -368,6 +370,35 @@ def paged_decode(q, key_cache, value_cache, scale_cache, block_tables, context_l
     return out
 
 
+def paged_decode_noalloc(q, key_cache, value_cache, scale_cache, block_tables, context_lens,
+                         pi_signs, num_kv_heads, block_size, num_blocks, out, gate=None,
+                         num_splits=0, scale=None, inv_sqrt_len=None, output_stage=1, flags=0,
+                         stream=None):
+    """paged_decode on the library's static 16 MiB scratch
+    (tq4_paged_decode_noalloc): no workspace, nothing allocated -- `out` is
+    required. Calls that overlap on one GPU race."""
+    _check_decode_inputs("paged_decode_noalloc", q, key_cache, value_cache, scale_cache,
+                         block_tables, context_lens, pi_signs, num_kv_heads, block_size,
+                         num_blocks,
+                         pi_needed=output_stage >= 1 or not (flags & TQ4_DECODE_QUERY_ROTATED))
+    _need("paged_decode_noalloc", "gate", gate, (torch.float32,), numel=q.numel(), optional=True)
+    _need("paged_decode_noalloc", "out", out, (torch.bfloat16,), numel=q.numel())
+    for name, t in (("q", q), ("key_cache", key_cache), ("value_cache", value_cache),
+                    ("scale_cache", scale_cache), ("block_tables", block_tables),
+                    ("context_lens", context_lens), ("pi_signs", pi_signs), ("gate", gate),
+                    ("out", out)):
+        _dev(t, name)
+    B, Hq, d = q.shape
+    st = lib().tq4_paged_decode_noalloc(
+        _stream(stream), _ptr(q), _ptr(key_cache), _ptr(value_cache), _ptr(scale_cache),
+        _ptr(block_tables), _ptr(context_lens), _ptr(pi_signs), _ptr(gate), _ptr(out), B, Hq,
+        num_kv_heads, d, block_size, num_blocks, block_tables.shape[1], num_splits,
+        1.0 / math.sqrt(d) if scale is None else scale,
+        1.0 / math.sqrt(d) if inv_sqrt_len is None else inv_sqrt_len, output_stage, flags)
+    _check(st, "paged_decode_noalloc")
+    return out
+
+
 def paged_decode_partials(q, key_cache, value_cache, scale_cache, block_tables, context_lens,
                           pi_signs, num_kv_heads, block_size, num_blocks, num_splits,
                           workspace=None, scale=None, inv_sqrt_len=None, flags=0, stream=None):
@@ -467,7 +498,7 @@ __all__ = [
     "TQ4Error", "lib", "status_string", "reshape_and_cache_a8", "reshape_and_cache_bf16",
     "reshape_scatter", "decode_workspace_bytes", "auto_splits", "decode_workspace",
     "paged_decode", "paged_decode_partials", "splitk_combine", "icdf_quantize",
-    "decode_workspace_init",
+    "decode_workspace_init", "paged_decode_noalloc",
     "lloydmax_quantize", "TQ4_DECODE_QUERY_ROTATED", "TQ4_MAX_SPLITS",
     "Kv4Fp8Launch", "Kv4Fp8Buffers", "Kv4Fp8RawQueryBuffers", "fused_decode_opt_launch",
     "kv4fp8_workspace_bytes", "kv4fp8_workspace_init", "kv4fp8_decode", "kv4fp8_decode_raw_query",

@@ -47,7 +47,8 @@ typedef enum {
     TQ4_ERR_LAUNCH = -9,        /* the HIP runtime refused the launch */
     TQ4_ERR_RANGE = -10,        /* a size exceeds what the kernels index */
     TQ4_ERR_CODEBOOK = -11,     /* codebook leaf: bits, mode or element count */
-    TQ4_ERR_FLAGS = -12         /* unknown flag bits, or a test hook without its bound */
+    TQ4_ERR_FLAGS = -12,        /* unknown flag bits, or a test hook without its bound */
+    TQ4_ERR_SCRATCH = -13       /* beyond the no-allocation entry's static scratch */
 } tq4_status;
 
 /* Human-readable name of a tq4_status. */
@@ -209,6 +210,29 @@ int tq4_paged_decode(void* stream, const uint16_t* q, const int8_t* key_cache,
                      uint32_t block_size, uint32_t num_blocks, uint32_t max_blocks_per_seq,
                      uint32_t num_splits, float scale, float inv_sqrt_len,
                      uint32_t output_stage, uint32_t flags);
+
+/* tq4_paged_decode without a workspace argument, for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc). No counterpart in the reference. Same arguments and
+ * result as tq4_paged_decode; the workspace is a static 16 MiB device array
+ * inside libtq4.so, one per GPU, held until the process ends (set up and
+ * zeroed on `stream` at the first call on each device; no allocation ever).
+ * A call whose workspace (tq4_decode_workspace_bytes) exceeds 16 MiB is
+ * refused with TQ4_ERR_SCRATCH (e.g. 64 sequences x 32 q heads at d = 128 fit
+ * up to 15 splits). Every call on one GPU shares that array: calls that
+ * overlap in time on one GPU (two streams, two threads) race and must be
+ * serialised by the caller. The test hooks are refused (TQ4_ERR_FLAGS), and
+ * the poll-timeout count is not reported: a combiner waits only for
+ * workgroups that are already running, so a give-up (2^20 polls) would mean
+ * a stalled device; callers that need that report use tq4_paged_decode. */
+int tq4_paged_decode_noalloc(void* stream, const uint16_t* q, const int8_t* key_cache,
+                             const int8_t* value_cache, const float* scale_cache,
+                             const int32_t* block_tables, const int32_t* context_lens,
+                             const float* pi_signs, const float* gate, uint16_t* out,
+                             uint32_t num_seqs, uint32_t num_heads, uint32_t num_kv_heads,
+                             uint32_t head_size, uint32_t block_size, uint32_t num_blocks,
+                             uint32_t max_blocks_per_seq, uint32_t num_splits, float scale,
+                             float inv_sqrt_len, uint32_t output_stage, uint32_t flags);
 
 /* Partials only: workspace record (seq, q head, split) at float offset
  * ((seq*num_heads + head)*num_splits + split)*(head_size + 4) holds

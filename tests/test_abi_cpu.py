@@ -190,3 +190,18 @@ def test_flag_and_timeout_refusals(lib):
     assert to(None, d, ws, 1, 2, None) == -1
     assert to(None, d, 100, 1, 2, C.byref(cnt)) == -6  # smaller than the tail
     assert to(None, d, ws, 0, 2, C.byref(cnt)) == -6
+
+
+def test_noalloc_refusals_before_any_hip_call(lib):
+    """The no-allocation entry refuses a call beyond its static scratch, and
+    the test hooks, before touching the device."""
+    d = C.c_void_p(16)
+    na = lib.tq4_paged_decode_noalloc
+
+    def call(B, K, flags=0):
+        return na(None, d, d, d, d, d, d, d, None, d, B, 32, 8, 128, 16, 4096, 512, K,
+                  C.c_float(0.1), C.c_float(0.1), 1, flags)
+    assert call(64, 16) == -13                       # 17.3 MB of workspace > 16 MiB
+    assert call(1, 4, 1 << 30) == -12                # no test hooks
+    assert call(1, 300) == -5                        # splits
+    assert lib.tq4_status_string(-13) != b"unknown status"
