@@ -420,6 +420,43 @@ int tq4_splitk_combine(void* stream, const float* workspace, const float* pi_sig
 
 }  // extern "C"
 
+// ------------------------------------------------------------- RMS codec
+extern "C" int tq4_rms_reshape_and_cache(void* stream, int type, uint32_t block_dim,
+                                         const void* key, const void* value, int8_t* key_cache,
+                                         int8_t* value_cache, float* scale_cache,
+                                         const int32_t* slot_mapping, const float* pi_signs,
+                                         const int32_t* tables, uint32_t num_tokens,
+                                         uint32_t num_kv_heads, uint32_t head_size,
+                                         uint32_t block_size, uint32_t num_blocks,
+                                         uint32_t tokens_per_core, float inv_sqrt_len)
+{
+    (void)tables;  // the gather and centroid tables are built into the kernel
+    if (type != 0 && type != 1) return TQ4_ERR_GEOMETRY;  // FP16 or BF16 activations
+    if (!head_size_ok(head_size)) return TQ4_ERR_HEAD_SIZE;
+    if (num_kv_heads == 0 || num_blocks == 0 || block_size == 0) return TQ4_ERR_GEOMETRY;
+    // the reference's grid covers block_dim * tokens_per_core tokens
+    uint64_t tokens = num_tokens;
+    if (block_dim != 0 && (uint64_t)block_dim * tokens_per_core < tokens)
+        tokens = (uint64_t)block_dim * tokens_per_core;
+    if (tokens == 0) return TQ4_OK;
+    if (!key || !value || !key_cache || !value_cache || !scale_cache || !slot_mapping ||
+        !pi_signs)
+        return TQ4_ERR_NULL_POINTER;
+    if (tokens * 2u * num_kv_heads > 0x7fffffffull * 16u) return TQ4_ERR_RANGE;
+    return launched(tq4::launch_rms_writer(
+        (hipStream_t)stream, type, (const uint16_t*)key, (const uint16_t*)value, key_cache,
+        value_cache, scale_cache, slot_mapping, pi_signs, (uint32_t)tokens, num_kv_heads,
+        head_size, (uint64_t)num_blocks * block_size, inv_sqrt_len));
+}
+
+extern "C" int tq4_rms_dequantize(void* stream, const int8_t* packed, float* out, uint64_t n)
+{
+    if (n % 2) return TQ4_ERR_CODEBOOK;
+    if (n == 0) return TQ4_OK;
+    if (!packed || !out) return TQ4_ERR_NULL_POINTER;
+    return launched(tq4::launch_rms_dequantize((hipStream_t)stream, packed, out, n / 2));
+}
+
 // ------------------------------------------------------------- codebooks
 int tq4_icdf_quantize(void* stream, int in_bf16, const uint16_t* in, uint8_t* out, uint32_t tiles)
 {

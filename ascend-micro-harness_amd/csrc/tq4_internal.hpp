@@ -57,6 +57,16 @@ hipError_t launch_codebook_quantize(hipStream_t stream, uint32_t book, uint32_t 
 hipError_t launch_codebook_dequantize(hipStream_t stream, uint32_t bits, const uint8_t* codes,
                                       float* recon, uint64_t count);
 
+// The vllm-ascend RMS + threshold codec (tq4_rms.hip): the baseline writer
+// over tokens [0, tokens), and the centroid decode of `bytes` packed bytes.
+hipError_t launch_rms_writer(hipStream_t stream, int in_bf16, const uint16_t* key,
+                             const uint16_t* value, int8_t* key_cache, int8_t* value_cache,
+                             float* scale_cache, const int32_t* slots, const float* pi_signs,
+                             uint32_t tokens, uint32_t H, uint32_t D, uint64_t slot_count,
+                             float inv_sqrt_len);
+hipError_t launch_rms_dequantize(hipStream_t stream, const int8_t* packed, float* out,
+                                 uint64_t bytes);
+
 // KV4/FP8 NZ-tiled decode (kv4fp8_decode.hip); filled by the ABI layer.
 struct Kv4Params {
     const float* query;          // rotated FP32 [T][Hq][256] (pre-rotated entry)

@@ -92,6 +92,10 @@ def lib():
     L.tq4_paged_decode_partials.argtypes = [_P] * 9 + [_SZ] + [_U32] * 8 + [_F32, _F32, _U32]
     L.tq4_splitk_combine.restype = _I32
     L.tq4_splitk_combine.argtypes = [_P] * 5 + [_U32] * 4 + [_F32, _U32]
+    L.tq4_rms_reshape_and_cache.restype = _I32
+    L.tq4_rms_reshape_and_cache.argtypes = [_P, _I32, _U32] + [_P] * 8 + [_U32] * 6 + [_F32]
+    L.tq4_rms_dequantize.restype = _I32
+    L.tq4_rms_dequantize.argtypes = [_P, _P, _P, C.c_uint64]
     L.tq4_icdf_quantize.restype = _I32
     L.tq4_icdf_quantize.argtypes = [_P, _I32, _P, _P, _U32]
     L.tq4_lloydmax_quantize.restype = _I32
@@ -456,6 +460,59 @@ def splitk_combine(workspace, pi_signs, num_seqs, num_heads, head_size, num_spli
     return out
 
 
+# ------------------------------------------------------------ RMS codec
+def rms_scale_slot_floats(num_kv_heads):
+    """Floats per slot of the baseline cache's scale record: 2H rounded up to 8."""
+    return (2 * num_kv_heads + 7) // 8 * 8
+
+
+def rms_reshape_and_cache(key, value, key_cache, value_cache, scale_cache, slot_mapping,
+                          pi_signs, num_blocks=None, block_size=16, inv_sqrt_len=None,
+                          block_dim=0, tokens_per_core=0, tables=None, stream=None):
+    """The vllm-ascend baseline writer (turboquant_reshape_and_cache_impl):
+    FP16/BF16 K/V [tokens][kv_heads][head_size] -> int8 rows [slot][kv_heads]
+    [head_size/2] and the scale record [slot][ceil(2 kv_heads / 8) * 8]."""
+    what = "rms_reshape_and_cache"
+    _need(what, "key", key, (torch.float16, torch.bfloat16), ndim=3)
+    _need(what, "value", value, (key.dtype,), numel=key.numel())
+    T, H, d = key.shape
+    if num_blocks is None:
+        num_blocks = key_cache.numel() // (block_size * H * (d // 2))
+    slots = num_blocks * block_size
+    _need(what, "key_cache", key_cache, _CACHE_BYTES, min_numel=slots * H * d // 2)
+    _need(what, "value_cache", value_cache, _CACHE_BYTES, min_numel=slots * H * d // 2)
+    _need(what, "scale_cache", scale_cache, (torch.float32,),
+          min_numel=slots * rms_scale_slot_floats(H))
+    _need(what, "slot_mapping", slot_mapping, (torch.int32,), min_numel=T)
+    _need(what, "pi_signs", pi_signs, (torch.float32,), min_numel=d)
+    for name, t in (("key", key), ("value", value), ("key_cache", key_cache),
+                    ("value_cache", value_cache), ("scale_cache", scale_cache),
+                    ("slot_mapping", slot_mapping), ("pi_signs", pi_signs), ("tables", tables)):
+        _dev(t, name)
+    if inv_sqrt_len is None:
+        inv_sqrt_len = 1.0 / math.sqrt(d)
+    st = lib().tq4_rms_reshape_and_cache(
+        _stream(stream), 1 if key.dtype == torch.bfloat16 else 0, block_dim, _ptr(key),
+        _ptr(value), _ptr(key_cache), _ptr(value_cache), _ptr(scale_cache), _ptr(slot_mapping),
+        _ptr(pi_signs), _ptr(tables), T, H, d, block_size, num_blocks, tokens_per_core,
+        inv_sqrt_len)
+    _check(st, what)
+
+
+def rms_dequantize(packed, out=None, stream=None):
+    """Packed codes (int8, two per byte) -> their centroids (float32)."""
+    _need("rms_dequantize", "packed", packed, _CACHE_BYTES)
+    n = 2 * packed.numel()
+    _need("rms_dequantize", "out", out, (torch.float32,), numel=n, optional=True)
+    _dev(packed, "packed")
+    _dev(out, "out")
+    if out is None:
+        out = torch.empty(n, dtype=torch.float32, device=packed.device)
+    _check(lib().tq4_rms_dequantize(_stream(stream), _ptr(packed), _ptr(out), n),
+           "rms_dequantize")
+    return out
+
+
 # ------------------------------------------------------------ codebooks
 def icdf_quantize(x, out=None, stream=None):
     """FP16 or BF16 values (a multiple of 1024) -> packed signed INT4 codes of
@@ -498,7 +555,8 @@ __all__ = [
     "TQ4Error", "lib", "status_string", "reshape_and_cache_a8", "reshape_and_cache_bf16",
     "reshape_scatter", "decode_workspace_bytes", "auto_splits", "decode_workspace",
     "paged_decode", "paged_decode_partials", "splitk_combine", "icdf_quantize",
-    "decode_workspace_init", "paged_decode_noalloc",
+    "decode_workspace_init", "paged_decode_noalloc", "rms_reshape_and_cache", "rms_dequantize",
+    "rms_scale_slot_floats",
     "lloydmax_quantize", "TQ4_DECODE_QUERY_ROTATED", "TQ4_MAX_SPLITS",
     "Kv4Fp8Launch", "Kv4Fp8Buffers", "Kv4Fp8RawQueryBuffers", "fused_decode_opt_launch",
     "kv4fp8_workspace_bytes", "kv4fp8_workspace_init", "kv4fp8_decode", "kv4fp8_decode_raw_query",

@@ -293,6 +293,36 @@ int tq4_lloydmax_quantize(void* stream, const void* src, float* dst, uint8_t* co
                           uint32_t* guards, uint32_t bits, uint32_t mode, uint32_t n,
                           uint32_t rows);
 
+/* ----------------------------------------------------------------------
+ * The vllm-ascend RMS + threshold codec (TurboQuantCodec<4>) and its
+ * baseline writer. Per (token, plane, kv head) vector x of head_size:
+ *   y = Pi x, Pi = diag(pi_signs) H diag(pi_signs) * inv_sqrt_len (FWHT);
+ *   scale = sqrt(sum y^2) * inv_sqrt_len + 1e-20;
+ *   level = #{i : t_i < y / scale} over the 15 Lloyd-Max 4-bit thresholds t;
+ *   byte = (level[2j] | level[2j+1] << 4) - 128 (int8).
+ * Cache: key/value int8 [num_blocks * block_size slots][num_kv_heads]
+ * [head_size / 2]; scale_cache float [slots][ceil(2 * num_kv_heads / 8) * 8]
+ * = the K heads' scales, then the V heads', then zeros. type: 0 FP16, 1 BF16
+ * (the reference's AscendType). Tokens whose slot is negative or past the
+ * pool write nothing; when block_dim is not 0 only the first block_dim *
+ * tokens_per_core tokens are written (the reference's grid covers those).
+ * `tables` (the reference's gather/centroid tables) is not read. Summation
+ * order of sum y^2: per 16th of the vector sequentially, then a pairwise tree.
+ * Replaces turboquant_reshape_and_cache_impl of the baseline
+ * (kernels/ops/turboquant/baseline/turboquant_paged_attention.cpp:754-771;
+ * codec kernels/ops/turboquant/baseline/common/turboquant_codec_950.h:115-248). */
+int tq4_rms_reshape_and_cache(void* stream, int type, uint32_t block_dim, const void* key,
+                              const void* value, int8_t* key_cache, int8_t* value_cache,
+                              float* scale_cache, const int32_t* slot_mapping,
+                              const float* pi_signs, const int32_t* tables, uint32_t num_tokens,
+                              uint32_t num_kv_heads, uint32_t head_size, uint32_t block_size,
+                              uint32_t num_blocks, uint32_t tokens_per_core, float inv_sqrt_len);
+
+/* The codec's decode: n (even) codes packed as above -> their centroids,
+ * out[2j] from byte j's low nibble. Replaces TurboQuantCodec<4>::Dequantize4Bit
+ * (kernels/ops/turboquant/baseline/common/turboquant_codec_950.h:165-172,251-285). */
+int tq4_rms_dequantize(void* stream, const int8_t* packed, float* out, uint64_t n);
+
 #ifdef __cplusplus
 }
 #endif

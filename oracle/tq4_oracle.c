@@ -977,3 +977,153 @@ int tq4o_icdf_quantize(int in_bf16, const uint16_t* in, uint64_t n, uint8_t* pac
     }
     return 0;
 }
+
+/* ==================================================================== RMS codec
+ * The vllm-ascend baseline codec, TurboQuantCodec<4>
+ * (kernels/ops/turboquant/baseline/common/turboquant_codec_950.h), applied by
+ * the baseline writer to every (token, plane, kv head) vector
+ * (kernels/ops/turboquant/baseline/turboquant_paged_attention.cpp:98-246):
+ *   ApplyPi     x * s, FWHT at strides 1, 2, 4, ..., n/2 (a + b | a - b),
+ *               * inv_sqrt_len, * s                       codec_950.h:115-151
+ *   scale       sqrt(sum y^2) * inv_sqrt_len + 1e-20       codec_950.h:186-197
+ *   level       #{i : y * (-1/scale) + t_i has its sign bit set}
+ *               = #{i : t_i < y * (1/scale)}               codec_950.h:199-231
+ *   byte        (even level + 16 * odd level) - 128, int8  codec_950.h:234-248
+ *   dequantize  byte + 128 -> even/odd level -> centroid   codec_950.h:251-285
+ * (-1/s rounds to -(1/s) and y * (-r) to -(y * r), and t - z rounds to a
+ * value of the exact difference's sign, never -0 since t_7 is +0, so the
+ * sign-bit count is the strict count.) The 15 thresholds and 16 centroids
+ * are the Lloyd-Max 4-bit codebook (codec_950.h:43-51; centroid table
+ * tests/npu/bench/bench_turboquant_reshape_and_cache.cpp:55-61).
+ * The sum of squares runs in this library's order -- 16 sequential partial
+ * sums over n/16 consecutive elements, then a pairwise tree over the
+ * partials (xor 1, 2, 4, 8), the GPU kernel's lane reduction; the
+ * reference device's ReduceSum order belongs to CANN and is not restated.
+ * Pins: ApplyPi equals tq4o_kv4fp8_apply_pi (pinned to the reference's
+ * fixture) bit for bit; the scale equals the FP64 closed form to a few ulp;
+ * the tables equal the pinned Lloyd-Max codebook; levels against a
+ * brute-force count at every threshold and its neighbours. */
+
+static const float kRmsThresholds[15] = {
+    -2.4008033987632817f, -1.8435318062766393f, -1.4371387916845330f, -1.0992858269170722f,
+    -0.7995497875097155f, -0.5224037090113789f, -0.2582216646707196f, 0.0f,
+    0.2582216646707196f,  0.5224037090113789f,  0.7995497875097155f,  1.0992858269170722f,
+    1.4371387916845330f,  1.8435318062766393f,  2.4008033987632817f};
+static const float kRmsCentroids[16] = {
+    -2.7325895709951710f, -2.0690172265313920f, -1.6180463860218863f, -1.2562311973471796f,
+    -0.9423404564869651f, -0.6567591185324659f, -0.3880482994902919f, -0.1283950298511473f,
+    0.1283950298511473f,  0.3880482994902919f,  0.6567591185324659f,  0.9423404564869651f,
+    1.2562311973471796f,  1.6180463860218863f,  2.0690172265313920f,  2.7325895709951710f};
+
+float tq4o_rms_threshold(uint32_t i) { return kRmsThresholds[i % 15u]; }
+float tq4o_rms_centroid(uint32_t level) { return kRmsCentroids[level & 15u]; }
+
+void tq4o_rms_apply_pi(float* x, const float* signs, float inv_sqrt_len, uint32_t n)
+{
+    for (uint32_t i = 0; i < n; ++i) x[i] = x[i] * signs[i];
+    for (uint32_t s = 1; s < n; s <<= 1)
+        for (uint32_t i = 0; i < n; ++i)
+            if (!(i & s)) {
+                const float a = x[i], b = x[i | s];
+                x[i] = a + b;
+                x[i | s] = a - b;
+            }
+    for (uint32_t i = 0; i < n; ++i) x[i] = x[i] * inv_sqrt_len;
+    for (uint32_t i = 0; i < n; ++i) x[i] = x[i] * signs[i];
+}
+
+float tq4o_rms_scale(const float* y, uint32_t n, float inv_sqrt_len)
+{
+    float part[16];
+    const uint32_t per = n / 16u;
+    for (uint32_t l = 0; l < 16u; ++l) {
+        float s = y[l * per] * y[l * per];
+        for (uint32_t j = 1; j < per; ++j) s = s + y[l * per + j] * y[l * per + j];
+        part[l] = s;
+    }
+    for (uint32_t m = 1; m < 16u; m <<= 1) {
+        float nxt[16];
+        for (uint32_t l = 0; l < 16u; ++l) nxt[l] = part[l] + part[l ^ m];
+        memcpy(part, nxt, sizeof(part));
+    }
+    return sqrtf(part[0]) * inv_sqrt_len + 1e-20f;
+}
+
+uint32_t tq4o_rms_level(float y, float rcp)
+{
+    const float z = y * rcp;
+    uint32_t q = 0;
+    for (uint32_t i = 0; i < 15u; ++i) q += kRmsThresholds[i] < z;
+    return q;
+}
+
+/* One vector: ApplyPi on a copy, scale, levels, packed bytes. */
+void tq4o_rms_quantize_row(const float* x, const float* signs, uint32_t n, float inv_sqrt_len,
+                           uint8_t* levels, int8_t* packed, float* scale)
+{
+    float y[256];
+    memcpy(y, x, n * sizeof(float));
+    tq4o_rms_apply_pi(y, signs, inv_sqrt_len, n);
+    const float s = tq4o_rms_scale(y, n, inv_sqrt_len);
+    const float r = 1.0f / s;
+    for (uint32_t p = 0; p < n / 2u; ++p) {
+        const uint32_t lo = tq4o_rms_level(y[2 * p], r), hi = tq4o_rms_level(y[2 * p + 1], r);
+        if (levels) {
+            levels[2 * p] = (uint8_t)lo;
+            levels[2 * p + 1] = (uint8_t)hi;
+        }
+        packed[p] = (int8_t)(uint8_t)((lo | (hi << 4)) ^ 0x80u);
+    }
+    *scale = s;
+}
+
+uint32_t tq4o_rms_scale_slot_floats(uint32_t num_kv_heads)
+{
+    return (2u * num_kv_heads + 7u) / 8u * 8u;
+}
+
+/* The baseline writer (TurboQuantReshapeAndCache, turboquant_paged_attention.cpp:98-246):
+ * tokens below token_limit whose slot lies in [0, num_blocks * block_size)
+ * write key row slot*H*(d/2) + h*(d/2), the value row likewise, and the
+ * slot's scale record [2H scales (K heads, then V heads), zero padding to
+ * a multiple of 8]. in_dtype 0 FP16, 1 BF16. Returns the rows written. */
+int64_t tq4o_rms_reshape_and_cache(int in_dtype, const uint16_t* key, const uint16_t* value,
+                                   int8_t* key_cache, int8_t* value_cache, float* scale_cache,
+                                   const int32_t* slots, const float* signs, uint32_t num_tokens,
+                                   uint32_t H, uint32_t d, uint32_t S, uint32_t P,
+                                   uint32_t token_limit, float inv_sqrt_len)
+{
+    if ((d != 64 && d != 128 && d != 256) || !H || !S || !P) return -1;
+    const uint64_t slots_total = (uint64_t)P * S;
+    const uint32_t ssf = tq4o_rms_scale_slot_floats(H);
+    const uint32_t T = token_limit < num_tokens ? token_limit : num_tokens;
+    int64_t written = 0;
+    for (uint32_t t = 0; t < T; ++t) {
+        const int32_t slot = slots[t];
+        if (slot < 0 || (uint64_t)slot >= slots_total) continue;
+        float* rec = scale_cache + (uint64_t)slot * ssf;
+        for (uint32_t i = 0; i < ssf; ++i) rec[i] = 0.0f;
+        for (uint32_t plane = 0; plane < 2u * H; ++plane) {
+            const uint16_t* src = (plane < H ? key : value) + ((uint64_t)t * H + plane % H) * d;
+            float x[256];
+            for (uint32_t c = 0; c < d; ++c)
+                x[c] = in_dtype ? tq4o_bf16_to_f32(src[c]) : tq4o_f16_to_f32(src[c]);
+            int8_t* dst = (plane < H ? key_cache : value_cache) +
+                          ((uint64_t)slot * H + plane % H) * (d / 2u);
+            tq4o_rms_quantize_row(x, signs, d, inv_sqrt_len, NULL, dst, &rec[plane]);
+            ++written;
+        }
+    }
+    return written;
+}
+
+/* Dequantize4Bit: packed bytes -> centroids, element 2j from byte j's low
+ * nibble (after the +128 bias), 2j+1 from its high nibble. */
+void tq4o_rms_dequantize(const int8_t* packed, uint64_t n, float* out)
+{
+    for (uint64_t j = 0; j < n / 2u; ++j) {
+        const uint32_t v = (uint32_t)(uint8_t)packed[j] ^ 0x80u;
+        out[2 * j] = kRmsCentroids[v & 15u];
+        out[2 * j + 1] = kRmsCentroids[v >> 4];
+    }
+}

@@ -150,6 +150,24 @@ float tq4o_f16_to_f32(uint16_t h);
 int tq4o_icdf_code(double x);
 int tq4o_icdf_quantize(int in_bf16, const uint16_t* in, uint64_t n, uint8_t* packed);
 
+/* ------------------------------------------------------------- RMS codec
+ * The vllm-ascend baseline codec (TurboQuantCodec<4>) and its writer:
+ * ApplyPi, RMS scale, 15-threshold levels, biased int8 packing, centroids. */
+float tq4o_rms_threshold(uint32_t i);
+float tq4o_rms_centroid(uint32_t level);
+void tq4o_rms_apply_pi(float* x, const float* signs, float inv_sqrt_len, uint32_t n);
+float tq4o_rms_scale(const float* y, uint32_t n, float inv_sqrt_len);
+uint32_t tq4o_rms_level(float y, float rcp);
+void tq4o_rms_quantize_row(const float* x, const float* signs, uint32_t n, float inv_sqrt_len,
+                           uint8_t* levels, int8_t* packed, float* scale);
+uint32_t tq4o_rms_scale_slot_floats(uint32_t num_kv_heads);
+int64_t tq4o_rms_reshape_and_cache(int in_dtype, const uint16_t* key, const uint16_t* value,
+                                   int8_t* key_cache, int8_t* value_cache, float* scale_cache,
+                                   const int32_t* slots, const float* signs, uint32_t num_tokens,
+                                   uint32_t H, uint32_t d, uint32_t S, uint32_t P,
+                                   uint32_t token_limit, float inv_sqrt_len);
+void tq4o_rms_dequantize(const int8_t* packed, uint64_t n, float* out);
+
 #ifdef __cplusplus
 }
 #endif

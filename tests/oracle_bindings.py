@@ -137,6 +137,21 @@ class Oracle:
         L.tq4o_f32_to_elem.restype = C.c_uint16
         L.tq4o_f32_to_elem.argtypes = [U32, F32]
         L.tq4o_kv4fp8_apply_pi.argtypes = [P, P, F32, U32]
+        L.tq4o_rms_threshold.restype = F32
+        L.tq4o_rms_threshold.argtypes = [U32]
+        L.tq4o_rms_centroid.restype = F32
+        L.tq4o_rms_centroid.argtypes = [U32]
+        L.tq4o_rms_apply_pi.argtypes = [P, P, F32, U32]
+        L.tq4o_rms_scale.restype = F32
+        L.tq4o_rms_scale.argtypes = [P, U32, F32]
+        L.tq4o_rms_level.restype = U32
+        L.tq4o_rms_level.argtypes = [F32, F32]
+        L.tq4o_rms_quantize_row.argtypes = [P, P, U32, F32, P, P, P]
+        L.tq4o_rms_scale_slot_floats.restype = U32
+        L.tq4o_rms_scale_slot_floats.argtypes = [U32]
+        L.tq4o_rms_reshape_and_cache.restype = C.c_int64
+        L.tq4o_rms_reshape_and_cache.argtypes = [I32] + [P] * 7 + [U32] * 6 + [F32]
+        L.tq4o_rms_dequantize.argtypes = [P, U64, P]
         L.tq4o_kv4fp8_rotate_query.argtypes = [U32, P, P, F32, U64, U32, P]
         L.tq4o_kv4fp8_partial_floats.restype = U32
         L.tq4o_kv4fp8_partial_floats.argtypes = [U32]
@@ -204,6 +219,40 @@ class Oracle:
         in_bits = np.ascontiguousarray(in_bits, np.uint16).reshape(-1)
         out = np.zeros(in_bits.size // 2, np.uint8)
         assert self.lib.tq4o_icdf_quantize(int(bf16), ptr(in_bits), in_bits.size, ptr(out)) == 0
+        return out
+
+    # ------------------------------------------------------------ RMS codec
+    def rms_apply_pi(self, x, signs, inv_sqrt_len):
+        y = np.ascontiguousarray(x, np.float32).copy()
+        self.lib.tq4o_rms_apply_pi(ptr(y), ptr(np.ascontiguousarray(signs, np.float32)),
+                                   inv_sqrt_len, y.size)
+        return y
+
+    def rms_quantize_row(self, x, signs, inv_sqrt_len):
+        """(levels uint8[n], packed int8[n/2], scale float32) of one vector."""
+        x = np.ascontiguousarray(x, np.float32)
+        lv = np.zeros(x.size, np.uint8)
+        pk = np.zeros(x.size // 2, np.int8)
+        sc = np.zeros(1, np.float32)
+        self.lib.tq4o_rms_quantize_row(ptr(x), ptr(np.ascontiguousarray(signs, np.float32)),
+                                       x.size, inv_sqrt_len, ptr(lv), ptr(pk), ptr(sc))
+        return lv, pk, sc[0]
+
+    def rms_reshape_and_cache(self, in_dtype, key, value, key_cache, value_cache, scale_cache,
+                              slots, signs, H, d, S, P, token_limit, inv_sqrt_len):
+        """In place on the cache arrays; returns the rows written."""
+        a = [np.ascontiguousarray(x) for x in (key, value)]
+        n = self.lib.tq4o_rms_reshape_and_cache(
+            in_dtype, ptr(a[0]), ptr(a[1]), ptr(key_cache), ptr(value_cache), ptr(scale_cache),
+            ptr(np.ascontiguousarray(slots, np.int32)), ptr(np.ascontiguousarray(signs, np.float32)),
+            a[0].shape[0], H, d, S, P, token_limit, inv_sqrt_len)
+        assert n >= 0
+        return n
+
+    def rms_dequantize(self, packed):
+        packed = np.ascontiguousarray(packed, np.int8).reshape(-1)
+        out = np.zeros(2 * packed.size, np.float32)
+        self.lib.tq4o_rms_dequantize(ptr(packed), out.size, ptr(out))
         return out
 
     # ------------------------------------------------------------ rotation
