@@ -372,9 +372,14 @@ __host__ __device__ constexpr size_t region_floats(uint32_t G, uint32_t D)
 // OWN (MODE 1): the combining split keeps its own record in registers instead
 // of storing and polling it (the one-launch kernel; the persistent kernel
 // stores it, which keeps that kernel's register budget).
-template <int D, int MODE, bool OWN = true>
+struct NoHook {
+    __device__ void operator()() const {}
+};
+
+template <int D, int MODE, bool OWN = true, class Hook = NoHook>
 __device__ __forceinline__ void decode_item(const DecodeParams& p, const uint32_t seq,
-                                            const uint32_t kvh, const uint32_t split)
+                                            const uint32_t kvh, const uint32_t split,
+                                            Hook&& after_issue = Hook())
 {
     constexpr int CPL = D / 64;   // channels per lane in the row layout
     constexpr int NJ = D / 32;    // score MFMAs per token set (one per key dword)
@@ -467,6 +472,7 @@ __device__ __forceinline__ void decode_item(const DecodeParams& p, const uint32_
                                       lane);
                     }
                 }
+                after_issue();  // exactly once per item, whichever way it leaves
                 return;
             }
         }
@@ -495,14 +501,6 @@ __device__ __forceinline__ void decode_item(const DecodeParams& p, const uint32_
     // lgkmcnt left at their maxima) keeps the compiler's wait analysis from
     // later waiting on them -- and so on the strip loads queued after them.
     __builtin_amdgcn_s_waitcnt(0x0F70);
-    // Fused entry: this split's ticket. Its round trip overlaps the strip
-    // loads; the value is first needed at the merge.
-    uint32_t ticket = 0;
-    if constexpr (MODE == 1) {
-        if (p.K > 1 && tid == 0)
-            ticket = __hip_atomic_fetch_add(p.counters + (size_t)seq * p.Hkv + kvh, 1u,
-                                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
     const uint32_t np_total = (ltok + 2 * kStrip - 1) / (2 * kStrip);
     const uint32_t np_full = bad ? 0u : ltok / (2 * kStrip);
     const uint32_t nws = pc * spp;  // strips in the window
@@ -558,6 +556,20 @@ __device__ __forceinline__ void decode_item(const DecodeParams& p, const uint32_
         fetch(b0, gp_of(0), false);
         if constexpr (NBUF == 3) fetch(b1, gp_of(1), false);
     }
+    // Fused entry: this split's ticket, and the caller's atomics (the
+    // persistent kernel's queue fetch), issued only now: atomics on one
+    // counter queue behind each other (about 50 ns per earlier one), and a
+    // wave's loads complete in issue order, so an atomic issued before the
+    // first strip loads would hold their processing until its return. Issued
+    // after them, it is first waited for at the wave's third pair or at the
+    // merge, where the ticket is read.
+    uint32_t ticket = 0;
+    if constexpr (MODE == 1) {
+        if (p.K > 1 && tid == 0)
+            ticket = __hip_atomic_fetch_add(p.counters + (size_t)seq * p.Hkv + kvh, 1u,
+                                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    after_issue();
 
     // ---- phase 1: rotate q (Pi = M * inv_sqrt_len), fold the softmax scale,
     // normalise each row by a power of two, stage in LDS.
@@ -1022,8 +1034,9 @@ __global__ TQ4_DECODE_ATTRS void decode_kernel(DecodeParams p)
 // kLptMaxSeqs sequences, so their spread of sizes packs the tail. Every
 // workgroup derives the order from the context lengths (a prefix over
 // sequences and a rank of the last splits, staged in LDS). A workgroup takes item blockIdx.x,
-// then one item at a time from an agent-scope queue counter, fetched as the
-// current item starts so the round trip hides under it. Each of the n_items
+// then one item at a time from an agent-scope queue counter, fetched once the
+// current item's first strip loads are out, so its round trip -- long when
+// many workgroups fetch at once -- hides under the item. Each of the n_items
 // fetches returns a distinct value and the one that returns n_items - 1 is
 // the last: it resets the counter (every workgroup's final fetch is its
 // failing one, so the fetches number exactly n_items). Nothing waits on a
@@ -1130,9 +1143,6 @@ void decode_persistent_kernel(DecodeParams p)
     uint32_t item = blockIdx.x;
     while (item < n_items) {
         uint32_t fetched = 0;
-        if (tid == 0)
-            fetched = __hip_atomic_fetch_add(p.queue, 1u, __ATOMIC_RELAXED,
-                                             __HIP_MEMORY_SCOPE_AGENT);
         uint32_t seq, kvh, split;
         if (item < n_full) {
             // a full split: its sequence is the first s with full[s] > item
@@ -1157,7 +1167,13 @@ void decode_persistent_kernel(DecodeParams p)
             kvh = r % p.Hkv;
             split = splits[seq] - 1;
         }
-        decode_item<D, 1, false>(p, seq, kvh, split);
+        // the next item's queue fetch goes out after this item's first strip
+        // loads (decode_item's hook); its value is read after the item
+        decode_item<D, 1, false>(p, seq, kvh, split, [&]() {
+            if (tid == 0)
+                fetched = __hip_atomic_fetch_add(p.queue, 1u, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT);
+        });
         if (tid == 0) {
             if (fetched == n_items - 1)
                 __hip_atomic_store(p.queue, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
