@@ -11,27 +11,36 @@ GPU reshape_and_cache from N(0,1) BF16 K/V.
 Cold reads without a flush kernel: SLICES independent config-3 sequences
 (each its own 256 random pages of one shared pool, its own q) are decoded in
 turn, so a sequence's 4.47 MB is read again only after SLICES-1 others
-(572 MB, more than the 256 MiB Infinity Cache) have been. The timed steps are
-captured once in a HIP graph and replayed back to back; HIP events on the
-launch stream bracket the replays, so ms_per_step is the average launch
-duration including the dispatch gap between consecutive kernels.
+(568 MB, more than the 256 MiB Infinity Cache) have been.
+
+Timing (every row, `time_launches`): the W warmup launches and then exactly
+the K timed launches are captured as two HIP graphs and replayed back to
+back; HIP events on the replay stream bracket the timed graph, so
+ms_per_step is the average launch duration including the dispatch gap
+between consecutive kernels. The spread (min / median / p99) comes from
+further replays of graphs of `chunk` launches, each bracketed by events: one
+sample is the per-launch time of one replay.
 
 Also reported: reshape_and_cache tokens/s on BASELINE configs[1] (1024 BF16
-tokens into a 4096-page pool, seeded page permutation; and the same tokens at
-token-granular slots through the scatter writer), the configs[0] A8 strip,
-the configs[3] split sweep (ctx 4096 / 16384 / 32768 x 2..16 splits, ragged
-4103), the batched decode step of configs[4] (64 sequences, ctx ~U[512,
-8192]), and the CPU baseline: the C oracle's decode of the same sequence on
-the host cores (kind "port"), on all of them and on one.
+tokens into a 4096-page pool; and the same tokens at token-granular slots
+through the scatter writer), the RMS codec writer on the same tokens, the
+configs[0] A8 strip, the configs[3] split sweep, the configs[4] batched step
+(64 sequences, ctx ~U[512, 8192], two batches rotated so each is read cold),
+the codebook leaves and the KV4/FP8 decode; and per row the CPU baseline:
+the C oracle (oracle/*.c, kind "port") on one thread and on every core this
+process may run on, each on a bounded sample of the row's workload.
 
 Usage:
   python bench.py [--gpus 1] [--steps K] [--warmup W]
-  python bench.py --pmc-run            # workload for rocprofv3 --pmc passes
-  python bench.py --summarize-pmc FETCH_DB WRITE_DB   # -> profiles/*traffic*
+  python bench.py --pmc-run              # workload for rocprofv3 --pmc passes
+  python bench.py --summarize-pmc DIR    # DIR/<pass>/run_counter_collection.csv
+  python bench.py --summarize-trace DIR  # a rocprofv3 --kernel-trace csv run
 """
 from __future__ import annotations
 
 import argparse
+import csv
+import glob
 import json
 import math
 import os
@@ -51,8 +60,14 @@ PAGES = CTX // S
 SLICES = 128
 SEED = 0x71340003
 CALIB_BYTES = 64 << 20  # plain copy (x * 2) of known size for the PMC scale factors
-TRAFFIC_FILE = os.path.join(REPO, "profiles", "decode_config3_traffic.json")
-DECODE_KERNEL = "decode_kernel<128, 1>"
+PMC_FILE = os.path.join(REPO, "profiles", "pmc_summary.json")
+PMC_KERNELS = {  # kernel-name fragment -> key in profiles/pmc_summary.json
+    "decode_kernel<128, 1>": "decode_kernel<128,1>",
+    "decode_persistent_kernel<128>": "decode_persistent_kernel<128>",
+    "strip_writer<128, unsigned short, 1>": "strip_writer<128,bf16,1>",
+}
+CALIB_KERNEL = "MulFunctor<float"
+DECODE_KERNEL = "decode_kernel<128,1>@128"  # PMC key: kernel@workgroups (16 splits x 8 heads)
 
 
 def log(*a):
@@ -75,60 +90,304 @@ def writer_algorithmic_bytes(tokens, hkv, d, in_bytes):
     return tokens * (2 * hkv * d * in_bytes + hkv * d + 2 * hkv * 4 + 4)
 
 
-# ---------------------------------------------------------------- PMC summary
-def _pmc_per_dispatch(db, counter):
-    """Mean value of `counter` per dispatch, by kernel name (rocprofv3 db)."""
-    import sqlite3
-    con = sqlite3.connect(db)
-    cols = {r[1] for r in con.execute("pragma table_info(counters_collection)")}
-    name_col = "kernel_name" if "kernel_name" in cols else "name"
-    q = (f"select {name_col}, avg(value) , count(*) from counters_collection "
-         f"where counter_name = ? group by {name_col}")
-    rows = list(con.execute(q, (counter,)))
-    con.close()
-    return {r[0]: (float(r[1]), int(r[2])) for r in rows}
+def rms_writer_algorithmic_bytes(tokens, hkv, d, in_bytes):
+    """Inputs read + packed codes + the slot's scale record written + slot read."""
+    return tokens * (2 * hkv * d * in_bytes + hkv * d + 4 * ((2 * hkv + 7) // 8 * 8) + 4)
 
 
-def summarize_pmc(fetch_db, write_db):
-    """FETCH_SIZE / WRITE_SIZE (KiB per dispatch) of the decode kernel, each
-    scaled by what the counter reads for a plain copy of CALIB_BYTES."""
-    fetch = _pmc_per_dispatch(fetch_db, "FETCH_SIZE")
-    write = _pmc_per_dispatch(write_db, "WRITE_SIZE")
-
-    def pick(tab, key):
-        hits = [(k, v) for k, v in tab.items() if key in k]
-        if not hits:
-            raise SystemExit(f"no kernel matching {key!r} in {sorted(tab)}")
-        return hits[0]
-
-    dn, (dec_f, nf) = pick(fetch, "decode_kernel")
-    _, (dec_w, nw) = pick(write, "decode_kernel")
-    cn, (cp_f, _) = pick(fetch, "MulFunctor")
-    _, (cp_w, _) = pick(write, "MulFunctor")
-    f_scale = CALIB_BYTES / (cp_f * 1024.0)
-    w_scale = CALIB_BYTES / (cp_w * 1024.0)
-    fetch_b = dec_f * 1024.0 * f_scale
-    write_b = dec_w * 1024.0 * w_scale
-    out = {"kernel": dn, "dispatches": [nf, nw], "fetch_kib_raw": dec_f, "write_kib_raw": dec_w,
-           "calib_kernel": cn, "calib_bytes": CALIB_BYTES, "fetch_scale": f_scale,
-           "write_scale": w_scale, "fetch_bytes": fetch_b, "write_bytes": write_b,
-           "traffic_bytes": fetch_b + write_b,
-           "algorithmic_bytes": decode_algorithmic_bytes([CTX], HQ, HKV, D, S)}
-    os.makedirs(os.path.dirname(TRAFFIC_FILE), exist_ok=True)
-    with open(TRAFFIC_FILE, "w") as f:
-        json.dump(out, f, indent=1)
-    print(json.dumps(out))
+# ---------------------------------------------------------------- timing
+def _graph(torch, stream, fns):
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        for f in fns:
+            f()
+    return g
 
 
-def read_traffic():
+def _pct(v, q):
+    return float(np.percentile(np.asarray(v), q))
+
+
+def time_launches(torch, fns, steps, warmup, samples=32, chunk=32, after_timed=None):
+    """Throughput and spread of launches over a rotation of input sets.
+
+    fns[i] launches one step on input set i; launch j takes set j % len(fns),
+    so a set is read again only after len(fns) - 1 others. Launch 0 runs
+    eagerly (any first-call set-up stays outside capture); launches 1 ..
+    warmup-1 form the warmup graph and launches warmup .. warmup+steps-1 the
+    timed graph, replayed right after it; HIP events on the replay stream
+    bracket the timed replay. Then `samples` replays of graphs of `chunk`
+    launches (continuing the rotation), each bracketed by events, give the
+    spread of the per-launch time. after_timed() runs once the timed replay
+    has finished, before the spread's launches."""
+    n = len(fns)
+    warmup = max(1, warmup)
+    rot = lambda a, b: [fns[i % n] for i in range(a, b)]  # noqa: E731
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        fns[0]()
+    torch.cuda.synchronize()
+    gw = _graph(torch, stream, rot(1, warmup)) if warmup > 1 else None
+    gt = _graph(torch, stream, rot(warmup, warmup + steps))
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    with torch.cuda.stream(stream):
+        if gw is not None:
+            gw.replay()
+        e0.record(stream)
+        gt.replay()
+        e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = e0.elapsed_time(e1) / steps
+    del gw, gt
+    if after_timed is not None:
+        after_timed()
+    # spread: graphs of `chunk` consecutive launches, covering the rotation
+    start = warmup + steps
+    ngraphs = max(1, math.ceil(n / chunk))
+    graphs = [_graph(torch, stream, rot(start + k * chunk, start + (k + 1) * chunk))
+              for k in range(ngraphs)]
+    torch.cuda.synchronize()
+    evs = []
+    with torch.cuda.stream(stream):
+        for s_ in range(samples):
+            a = torch.cuda.Event(enable_timing=True)
+            b = torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            graphs[s_ % ngraphs].replay()
+            b.record(stream)
+            evs.append((a, b))
+    torch.cuda.synchronize()
+    per = [a.elapsed_time(b) * 1e3 / chunk for a, b in evs]
+    spread = {"min_us": round(min(per), 3), "median_us": round(float(np.median(per)), 3),
+              "p99_us": round(_pct(per, 99), 3), "samples": samples, "launches_per_sample": chunk}
+    return {"ms": ms, "wall_s": wall, "steps": steps, "warmup": warmup, "spread": spread}
+
+
+def row_times(res):
+    return {"us": round(res["ms"] * 1e3, 3), "steps": res["steps"], "warmup": res["warmup"],
+            "spread_us": res["spread"]}
+
+
+# ---------------------------------------------------------------- PMC
+def read_pmc():
     try:
-        with open(TRAFFIC_FILE) as f:
+        with open(PMC_FILE) as f:
             return json.load(f)
     except (OSError, ValueError):
-        return None
+        return {}
 
 
-# -------------------------------------------------------------------- workload
+def roofline(nbytes, ms, kernel, pmc=None):
+    """The roofline object of a row: algorithmic bytes over the measured
+    launch time against the HBM peak; traffic from the committed PMC summary
+    (FETCH_SIZE + WRITE_SIZE per dispatch, each scaled by a plain copy)."""
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    t = (pmc or {}).get(kernel, {})
+    return {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4),
+            "traffic": round(t["traffic_bytes"]) if "traffic_bytes" in t else None,
+            "kernel": kernel, "algorithmic_bytes": nbytes,
+            "traffic_ratio": round(t["traffic_bytes"] / nbytes, 3) if "traffic_bytes" in t else None,
+            "traffic_source": "profiles/pmc_summary.json" if "traffic_bytes" in t else None}
+
+
+def summarize_pmc(root):
+    """Mean counter value per dispatch for the profiled kernels over every
+    pass under root (rocprofv3 --output-format csv), by kernel and grid
+    ("name@workgroups"), FETCH_SIZE / WRITE_SIZE scaled to bytes by what they
+    read for the plain copy of CALIB_BYTES (the largest-grid float multiply)."""
+    vals = {}
+    meta = {}
+    for f in sorted(glob.glob(os.path.join(root, "*", "run_counter_collection.csv"))):
+        with open(f) as fh:
+            for row in csv.DictReader(fh):
+                name = row.get("Kernel_Name", "")
+                key = next((v for k, v in PMC_KERNELS.items() if k in name), None)
+                if key is None and CALIB_KERNEL in name:
+                    key = "copy"
+                if key is None:
+                    continue
+                grid, wg = int(row["Grid_Size"]), int(row["Workgroup_Size"])
+                kg = (key, grid)
+                vals.setdefault(kg, {}).setdefault(row["Counter_Name"], []).append(
+                    float(row["Counter_Value"]))
+                meta.setdefault(kg, {"workgroups": grid // max(1, wg), "workgroup_size": wg,
+                                     "vgprs": int(row["VGPR_Count"]),
+                                     "agprs": int(row["Accum_VGPR_Count"]),
+                                     "sgprs": int(row["SGPR_Count"]),
+                                     "lds_bytes": int(row["LDS_Block_Size"]),
+                                     "scratch_bytes": int(row["Scratch_Size"])})
+    copies = [kg for kg in vals if kg[0] == "copy"]
+    if not copies:
+        raise SystemExit(f"no calibration copy among the profiled kernels under {root}")
+    cal_kg = max(copies, key=lambda kg: kg[1])
+    cal = {c: float(np.mean(v)) for c, v in vals[cal_kg].items()}
+    f_scale = CALIB_BYTES / (cal["FETCH_SIZE"] * 1024.0)
+    w_scale = CALIB_BYTES / (cal["WRITE_SIZE"] * 1024.0)
+    out = {"calibration": {"kernel": "torch.mul(x, 2.0) over CALIB_BYTES of float32",
+                           "bytes_read_and_written": CALIB_BYTES,
+                           "dispatches": len(vals[cal_kg]["FETCH_SIZE"]),
+                           "fetch_kib_raw": cal["FETCH_SIZE"], "write_kib_raw": cal["WRITE_SIZE"],
+                           "fetch_scale": f_scale, "write_scale": w_scale}}
+    for (key, grid), cv in sorted(vals.items()):
+        if key == "copy":
+            continue
+        e = {"kernel": key, **meta[(key, grid)],
+             "dispatches": max(len(v) for v in cv.values()),
+             "counters": {c: float(np.mean(v)) for c, v in cv.items()}}
+        if "FETCH_SIZE" in cv and "WRITE_SIZE" in cv:
+            e["fetch_bytes"] = e["counters"]["FETCH_SIZE"] * 1024.0 * f_scale
+            e["write_bytes"] = e["counters"]["WRITE_SIZE"] * 1024.0 * w_scale
+            e["traffic_bytes"] = e["fetch_bytes"] + e["write_bytes"]
+        out[f"{key}@{e['workgroups']}"] = e
+    os.makedirs(os.path.dirname(PMC_FILE), exist_ok=True)
+    with open(PMC_FILE, "w") as f:
+        json.dump(out, f, indent=1)
+    print_pmc_table(out)
+
+
+def print_pmc_table(out):
+    """Markdown view of the PMC summary."""
+    cal = out["calibration"]
+    print(f"Calibration copy: FETCH_SIZE {cal['fetch_kib_raw']:.0f} KiB and WRITE_SIZE "
+          f"{cal['write_kib_raw']:.0f} KiB for {CALIB_BYTES >> 10} KiB read and written "
+          f"(scales {cal['fetch_scale']:.3f}, {cal['write_scale']:.3f}).\n")
+    keys = [k for k in out if k != "calibration"]
+
+    def c(e, n):
+        return e["counters"].get(n, float("nan"))
+
+    lines = [
+        ("dispatches", lambda e: f"{e['dispatches']}"),
+        ("workgroups x size", lambda e: f"{e['workgroups']} x {e['workgroup_size']}"),
+        ("arch VGPRs / AGPRs / SGPRs", lambda e: f"{e['vgprs']} / {e['agprs']} / {e['sgprs']}"),
+        ("LDS bytes / scratch bytes", lambda e: f"{e['lds_bytes']} / {e['scratch_bytes']}"),
+        ("FETCH_SIZE KiB raw -> bytes", lambda e: f"{c(e, 'FETCH_SIZE'):.1f} -> {e.get('fetch_bytes', 0):.0f}"),
+        ("WRITE_SIZE KiB raw -> bytes", lambda e: f"{c(e, 'WRITE_SIZE'):.1f} -> {e.get('write_bytes', 0):.0f}"),
+        ("HBM traffic bytes", lambda e: f"{e.get('traffic_bytes', 0):.0f}"),
+        ("SQ_LDS_BANK_CONFLICT / SQ_LDS_IDX_ACTIVE (cycles)",
+         lambda e: f"{c(e, 'SQ_LDS_BANK_CONFLICT'):.0f} / {c(e, 'SQ_LDS_IDX_ACTIVE'):.0f}"),
+        ("bank-conflict share of LDS-active cycles",
+         lambda e: f"{c(e, 'SQ_LDS_BANK_CONFLICT') / max(1.0, c(e, 'SQ_LDS_IDX_ACTIVE')):.3f}"),
+        ("LDSBankConflict (derived)", lambda e: f"{c(e, 'LDSBankConflict'):.3f}"),
+        ("SQ_INSTS_LDS", lambda e: f"{c(e, 'SQ_INSTS_LDS'):.0f}"),
+        ("MeanOccupancyPerActiveCU (derived)", lambda e: f"{c(e, 'MeanOccupancyPerActiveCU'):.3f}"),
+        ("SQ_WAVES / SQ_WAVE_CYCLES", lambda e: f"{c(e, 'SQ_WAVES'):.0f} / {c(e, 'SQ_WAVE_CYCLES'):.0f}"),
+        ("SQ_BUSY_CU_CYCLES / GRBM_GUI_ACTIVE",
+         lambda e: f"{c(e, 'SQ_BUSY_CU_CYCLES'):.0f} / {c(e, 'GRBM_GUI_ACTIVE'):.0f}"),
+        ("SQ_INSTS_VALU / SQ_INSTS_MFMA", lambda e: f"{c(e, 'SQ_INSTS_VALU'):.0f} / {c(e, 'SQ_INSTS_MFMA'):.0f}"),
+        ("SQ_VALU_MFMA_BUSY_CYCLES", lambda e: f"{c(e, 'SQ_VALU_MFMA_BUSY_CYCLES'):.0f}"),
+        ("SQ_INSTS_VMEM_RD", lambda e: f"{c(e, 'SQ_INSTS_VMEM_RD'):.0f}"),
+        ("SQ_WAIT_INST_ANY / SQ_WAIT_ANY", lambda e: f"{c(e, 'SQ_WAIT_INST_ANY'):.0f} / {c(e, 'SQ_WAIT_ANY'):.0f}"),
+    ]
+    print("| per dispatch | " + " | ".join(f"`{k}`" for k in keys) + " |")
+    print("|---|" + "---|" * len(keys))
+    for label, fn in lines:
+        print(f"| {label} | " + " | ".join(fn(out[k]) for k in keys) + " |")
+
+
+def summarize_trace(root, limit=0):
+    """Per (kernel, grid) launch statistics of a rocprofv3 --kernel-trace run
+    (--output-format csv) under root: calls, mean, median, p99, min, max (us).
+    limit > 0: only the first `limit` dispatches of each (kernel, grid), in
+    dispatch order."""
+    rows = {}
+    for f in sorted(glob.glob(os.path.join(root, "**", "*kernel_trace.csv"), recursive=True)):
+        with open(f) as fh:
+            for r in csv.DictReader(fh):
+                try:
+                    blocks = 1
+                    for ax in "XYZ":
+                        blocks *= int(r[f"Grid_Size_{ax}"]) // max(1, int(r[f"Workgroup_Size_{ax}"]))
+                except (KeyError, ValueError):
+                    blocks = r.get("Grid_Size", "?")
+                us = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) * 1e-3
+                rows.setdefault((r["Kernel_Name"], blocks), []).append(
+                    (int(r.get("Dispatch_Id") or 0), us))
+    print("| kernel | workgroups | calls | mean us | median us | p99 us | min us | max us |")
+    print("|---|---|---|---|---|---|---|---|")
+    for key in rows:
+        v = [us for _, us in sorted(rows[key])]
+        rows[key] = v[:limit] if limit > 0 else v
+    for (name, blocks), v in sorted(rows.items(), key=lambda kv: -sum(kv[1])):
+        if len(v) < 4:
+            continue
+        short = name.replace("(anonymous namespace)::", "").replace("void ", "").split("(")[0]
+        print(f"| `{short}` | {blocks} | {len(v)} | {np.mean(v):.2f} | {np.median(v):.2f} | "
+              f"{_pct(v, 99):.2f} | {min(v):.2f} | {max(v):.2f} |")
+
+
+# ---------------------------------------------------------------- CPU leg
+def cpu_threads():
+    """Cores this process may run on (its affinity mask)."""
+    try:
+        return len(os.sched_getaffinity(0))
+    except AttributeError:
+        return os.cpu_count() or 1
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
+def cpu_host():
+    quota = None
+    try:
+        with open("/sys/fs/cgroup/cpu.max") as f:
+            quota = f.read().strip()
+    except OSError:
+        pass
+    return {"affinity_cores": cpu_threads(), "os_cpu_count": os.cpu_count(),
+            "cpu_model": cpu_model(), "cgroup_cpu_max": quota}
+
+
+def cpu_run(fn, budget):
+    """Call fn until `budget` seconds have passed (at least once)."""
+    it, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        it += 1
+        el = time.perf_counter() - t0
+        if el >= budget:
+            return it, el
+
+
+def cpu_leg(fn_threads, amount, unit, sample, budget, max_tasks):
+    """The oracle on one thread and on every core (capped at its number of
+    independent tasks); `amount` is the row's measure per call (bytes for
+    GB/s, tokens for tokens/s)."""
+    scale = 1e-9 if unit == "GB/s" else 1.0
+    it1, el1 = cpu_run(lambda: fn_threads(1), budget / 2)
+    n = max(1, min(cpu_threads(), max_tasks))
+    itn, eln = cpu_run(lambda: fn_threads(n), budget / 2)
+    return {"value": round(amount * itn / eln * scale, 4), "unit": unit, "cores": n,
+            "kind": "port", "us_per_call": round(eln / itn * 1e6, 1),
+            "sample": f"{sample}: {itn} calls in {eln:.2f} s on {n} threads",
+            "single_thread": {"value": round(amount * it1 / el1 * scale, 4), "unit": unit,
+                              "us_per_call": round(el1 / it1 * 1e6, 1),
+                              "sample": f"{it1} calls in {el1:.2f} s on 1 thread"},
+            **cpu_host()}
+
+
+def oracle():
+    sys.path.insert(0, os.path.join(REPO, "tests"))
+    from oracle_bindings import Oracle
+    return Oracle()
+
+
+# ---------------------------------------------------------------- workloads
 class Workload:
     """SLICES config-3 sequences in one page pool, prefilled on the GPU."""
 
@@ -166,67 +425,110 @@ class Workload:
         self.ws = tq4.decode_workspace(B, HQ, HKV, D, self.splits)
 
     def decode(self, i, out=None):
-        tq4 = self.tq4
-        tq4.paged_decode(self.q[i], self.kc, self.vc, self.sc, self.tables[i], self.ctx,
-                         self.signs, HKV, S, self.pool, out=self.out if out is None else out,
-                         workspace=self.ws, num_splits=self.splits, scale=self.scale,
-                         inv_sqrt_len=self.isl)
+        self.tq4.paged_decode(self.q[i], self.kc, self.vc, self.sc, self.tables[i], self.ctx,
+                              self.signs, HKV, S, self.pool,
+                              out=self.out if out is None else out, workspace=self.ws,
+                              num_splits=self.splits, scale=self.scale, inv_sqrt_len=self.isl)
 
 
-def graph_time(torch, fns, steps, warmup):
-    """Capture fns (a list of launch closures) once in a HIP graph, replay it
-    until `steps` launches have run, and time the replays with events on the
-    launch stream. Returns (ms per launch, wall seconds of the timed region)."""
-    n = len(fns)
-    reps = max(1, steps // n)
-    stream = torch.cuda.Stream()
-    stream.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(stream):
-        for _ in range(max(1, warmup // n)):
-            for f in fns:
-                f()
-    torch.cuda.current_stream().wait_stream(stream)
-    torch.cuda.synchronize()
-    g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g, stream=stream):
-        for f in fns:
-            f()
-    g.replay()
-    torch.cuda.synchronize()
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
-    t0 = time.perf_counter()
-    with torch.cuda.stream(stream):
-        e0.record(stream)
-        for _ in range(reps):
-            g.replay()
-        e1.record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    return e0.elapsed_time(e1) / (reps * n), wall, reps * n
+class Batch:
+    """One configs[4] batch: 64 sequences, ctx ~U[512, 8192] (seeded), their
+    own page pool of random bytes (value-range-neutral for the decode's
+    bandwidth), one new token per sequence for the step's scatter."""
+
+    K = 3  # splits: measured best for this batch (K = 1..8); the persistent
+    # kernel orders the last splits longest first
+
+    def __init__(self, tq4, torch, dev, seed, signs):
+        S_ = S
+        self.tq4 = tq4
+        r = np.random.default_rng(0x71340005)
+        self.ctxs = [int(x) for x in r.integers(512, 8193, 64)]  # the shape is the config's
+        rb = np.random.default_rng(seed)
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(seed)
+        bsz = len(self.ctxs)
+        npages = [(c + 1 + S_ - 1) // S_ for c in self.ctxs]  # room for the step's token
+        self.pool = int(sum(npages) * 1.1) + 16
+        perm = rb.permutation(self.pool).astype(np.int32)
+        tab = np.zeros((bsz, max(npages)), np.int32)
+        at = 0
+        for b, n in enumerate(npages):
+            tab[b, :n] = perm[at:at + n]
+            at += n
+        self.tab_np = tab
+        self.tables = torch.from_numpy(tab).to(dev)
+        nb = self.pool * HKV * S_ * D // 2
+        self.kc = torch.randint(-128, 127, (nb,), dtype=torch.int8, device=dev, generator=gen)
+        self.vc = torch.randint(-128, 127, (nb,), dtype=torch.int8, device=dev, generator=gen)
+        self.sc = torch.rand(2 * self.pool * HKV * S_, device=dev, generator=gen) * 0.05 + 0.01
+        self.ctx_now = torch.tensor([c + 1 for c in self.ctxs], dtype=torch.int32, device=dev)
+        self.slots = torch.from_numpy(np.array(
+            [tab[b, c // S_] * S_ + c % S_ for b, c in enumerate(self.ctxs)], np.int32)).to(dev)
+        self.q = torch.randn((bsz, HQ, D), generator=gen, device=dev).to(torch.bfloat16)
+        self.kn = torch.randn((bsz, HKV, D), generator=gen, device=dev).to(torch.bfloat16)
+        self.vn = torch.randn((bsz, HKV, D), generator=gen, device=dev).to(torch.bfloat16)
+        self.out = torch.empty_like(self.q)
+        self.ws = tq4.decode_workspace(bsz, HQ, HKV, D, self.K)
+        self.signs = signs
+        self.isl = 1.0 / math.sqrt(D)
+
+    def scatter(self):
+        self.tq4.reshape_scatter(self.kn, self.vn, self.kc, self.vc, self.sc, self.slots,
+                                 self.signs, num_blocks=self.pool, block_size=S,
+                                 inv_sqrt_len=self.isl)
+
+    def decode(self):
+        self.tq4.paged_decode(self.q, self.kc, self.vc, self.sc, self.tables, self.ctx_now,
+                              self.signs, HKV, S, self.pool, out=self.out, workspace=self.ws,
+                              num_splits=self.K, scale=self.isl, inv_sqrt_len=self.isl)
+
+    def step(self):
+        self.scatter()
+        self.decode()
+
+    def decode_bytes(self):
+        return decode_algorithmic_bytes([c + 1 for c in self.ctxs], HQ, HKV, D, S)
+
+    def step_bytes(self):
+        bsz = len(self.ctxs)
+        # + the scatter: inputs, nibbles, scales, slots, and the value-strip RMW
+        return self.decode_bytes() + bsz * (2 * HKV * D * 2 + HKV * D // 2 + 2 * HKV * 4 + 4) \
+            + bsz * HKV * 1024
 
 
+# ---------------------------------------------------------------- main
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=1024)
     ap.add_argument("--warmup", type=int, default=128)
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-seconds", type=float, default=4.0,
+                    help="CPU-leg budget of the headline row (other rows use less)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="headline decode only")
     ap.add_argument("--pmc-run", action="store_true",
-                    help="a few cold decodes plus a plain copy of known size, for rocprofv3 --pmc")
-    ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DB", "WRITE_DB"))
+                    help="the profiled kernels' workloads plus a plain copy of known size, "
+                         "for rocprofv3 --pmc")
+    ap.add_argument("--summarize-pmc", metavar="DIR")
+    ap.add_argument("--summarize-trace", metavar="DIR")
+    ap.add_argument("--trace-limit", type=int, default=0,
+                    help="with --summarize-trace: the first N dispatches of each kernel and grid")
     args = ap.parse_args()
 
     if args.summarize_pmc:
-        summarize_pmc(*args.summarize_pmc)
+        summarize_pmc(args.summarize_pmc)
+        return
+    if args.summarize_trace:
+        summarize_trace(args.summarize_trace, args.trace_limit)
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}): the TQ4 path is "
               "built and measured on a single MI355X; no multi-GPU figure is produced.",
               file=sys.stderr)
         sys.exit(2)
+    if args.steps < 1:
+        raise SystemExit("--steps must be at least 1")
 
     import torch
 
@@ -236,59 +538,55 @@ def main():
     torch.cuda.set_device(dev)
 
     if args.pmc_run:
-        w = Workload(tq4, torch, dev, 32)
-        torch.cuda.synchronize()
-        for i in range(32):
-            w.decode(i)
-        src = torch.ones(CALIB_BYTES // 4, dtype=torch.float32, device=dev)
-        dst = torch.empty_like(src)
-        torch.cuda.synchronize()
-        for _ in range(4):
-            torch.mul(src, 2.0, out=dst)  # the calibration copy: reads and writes CALIB_BYTES
-        torch.cuda.synchronize()
-        log("pmc workload done")
+        pmc_workload(tq4, torch, dev)
         return
 
     log(f"prefilling {SLICES} config-3 sequences ({SLICES * PAGES} pages)")
     w = Workload(tq4, torch, dev, SLICES)
     torch.cuda.synchronize()
 
-    # correctness gates: finite output, and the last graph replay (slice
-    # SLICES-1) bit-identical to an eager decode of the same slice
+    # correctness gate: the last timed launch (slice (W + K - 1) % SLICES)
+    # must equal an eager decode of that slice, bit for bit
+    warm_n = max(1, args.warmup)
+    last = (warm_n + args.steps - 1) % SLICES
     ref = torch.empty_like(w.out)
-    w.decode(SLICES - 1, out=ref)
+    w.decode(last, out=ref)
     torch.cuda.synchronize()
     assert torch.isfinite(ref.float()).all(), "decode produced non-finite values"
 
-    cold_ms, wall, nsteps = graph_time(torch, [lambda i=i: w.decode(i) for i in range(SLICES)],
-                                       args.steps, args.warmup)
-    torch.cuda.synchronize()
-    assert torch.equal(w.out.view(torch.int16), ref.view(torch.int16)), \
-        "graph replays changed the decode result"
-    warm_ms, _, _ = graph_time(torch, [lambda: w.decode(0)] * 64, 512, 64)
+    def gate():
+        assert torch.equal(w.out.view(torch.int16), ref.view(torch.int16)), \
+            "graph replays changed the decode result"
+
+    res = time_launches(torch, [lambda i=i: w.decode(i) for i in range(SLICES)], args.steps,
+                        args.warmup, samples=48, chunk=32, after_timed=gate)
+    timeouts = tq4.decode_poll_timeouts(w.ws, B, HKV)
+    cold_ms = res["ms"]
+    warm = time_launches(torch, [lambda: w.decode(0)], 256, 16, samples=16, chunk=64)
+    timeouts += tq4.decode_poll_timeouts(w.ws, B, HKV)
     dec_bytes = decode_algorithmic_bytes([CTX], HQ, HKV, D, S)
     gbs = dec_bytes / (cold_ms * 1e-3) / 1e9
-    log(f"decode cold: {cold_ms * 1e3:.2f} us/step -> {gbs:.1f} GB/s "
-        f"({100 * gbs / HBM_PEAK_GBS:.1f}% of HBM peak); warm {warm_ms * 1e3:.2f} us; "
-        f"splits={w.splits}")
+    log(f"decode cold: {cold_ms * 1e3:.2f} us/step ({res['steps']} steps) -> {gbs:.1f} GB/s "
+        f"({100 * gbs / HBM_PEAK_GBS:.1f}% of HBM peak); spread {res['spread']}; "
+        f"warm {warm['ms'] * 1e3:.2f} us; splits={w.splits}")
 
+    pmc = read_pmc()
     extra = {}
     if not args.no_extra:
-        extra = extra_workloads(tq4, torch, dev, w, cpu=not args.no_cpu)
+        extra = extra_workloads(tq4, torch, dev, w, pmc, cpu=not args.no_cpu)
 
     cpu = None
     if not args.no_cpu:
-        cpu = cpu_baseline(torch, w, dec_bytes, args.cpu_seconds)
+        cpu = cpu_decode_leg(torch, w, dec_bytes, args.cpu_seconds)
         log(f"cpu baseline: {cpu}")
 
-    traffic = read_traffic()
     result = {
         "metric": METRIC,
         "value": round(gbs, 2),
         "unit": "GB/s",
         "n_gpus": 1,
-        "steps": nsteps,
-        "warmup": args.warmup,
+        "steps": res["steps"],
+        "warmup": res["warmup"],
         "ms_per_step": round(cold_ms, 6),
         "higher_is_better": True,
         "scaling": "weak",
@@ -299,78 +597,182 @@ def main():
                    "q_heads": HQ, "kv_heads": HKV, "head_dim": D, "ctx": CTX, "page_size": S,
                    "splits": w.splits, "cache": f"cold ({SLICES} rotated sequences)",
                    "parallelism": "single GPU"},
-        "decode_us": {"cold": round(cold_ms * 1e3, 3), "warm": round(warm_ms * 1e3, 3)},
+        "valid": timeouts == 0,
+        "poll_timeouts": timeouts,
+        "decode_us": {"cold": round(cold_ms * 1e3, 3), "cold_spread": res["spread"],
+                      "warm": round(warm["ms"] * 1e3, 3), "warm_spread": warm["spread"]},
         "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
-        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
-                     "traffic": round(traffic["traffic_bytes"]) if traffic else None,
-                     "kernel": DECODE_KERNEL, "algorithmic_bytes": dec_bytes},
+        "roofline": roofline(dec_bytes, cold_ms, DECODE_KERNEL, pmc),
+        "launch_floor_note": "a back-to-back graph launch of an empty kernel costs about 2 us; "
+                             "one launch moving 4.47 MB therefore tops out near 28 % of peak",
         "cpu_baseline": cpu,
-        "wall_s_timed": round(wall, 3),
+        "wall_s_timed": round(res["wall_s"], 3),
     }
+    if timeouts:
+        result["INVALID"] = f"{timeouts} combine rows gave up their bounded poll"
     result.update(extra)
     print(json.dumps(result), flush=True)
 
 
-def extra_workloads(tq4, torch, dev, w, cpu=True):
-    """reshape_and_cache tokens/s (configs[1], and its scatter variant), the A8
-    strip, the split sweep, the batched step
-    (configs[4]), the codebook leaves and the KV4/FP8 decode."""
+def pmc_workload(tq4, torch, dev):
+    """A few launches of each profiled kernel on the bench's own inputs
+    (cold where the bench is cold), then a plain copy of CALIB_BYTES."""
+    w = Workload(tq4, torch, dev, 32)
+    torch.cuda.synchronize()
+    for i in range(32):
+        w.decode(i)
+    torch.cuda.synchronize()
+    bats = [Batch(tq4, torch, dev, 0x71340050 + k, w.signs) for k in range(2)]
+    for _ in range(2):
+        for b in bats:
+            b.decode()
+    torch.cuda.synchronize()
+    del bats
+    wr = WriterInputs(tq4, torch, dev, w, 4)
+    for i in range(4):
+        wr.write(i)
+    torch.cuda.synchronize()
+    src = torch.ones(CALIB_BYTES // 4, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(4):
+        torch.mul(src, 2.0, out=dst)  # the calibration copy: reads and writes CALIB_BYTES
+    torch.cuda.synchronize()
+    log("pmc workload done")
+
+
+class WriterInputs:
+    """1024 BF16 tokens per launch into a 4096-page pool at the
+    pages of a seeded permutation; `n` input sets rotated."""
+
+    def __init__(self, tq4, torch, dev, w, n, tokens=1024, pool=4096):
+        self.tq4, self.w, self.tokens, self.pool = tq4, w, tokens, pool
+        rng = np.random.default_rng(0x71340002)
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(0x71340002)
+        self.kc = torch.zeros(pool * HKV * S * D // 2, dtype=torch.int8, device=dev)
+        self.vc = torch.zeros_like(self.kc)
+        self.sc = torch.zeros(2 * pool * HKV * S, device=dev)
+        ar = torch.arange(S, device=dev, dtype=torch.int32)
+        self.ins = []
+        for _ in range(n):
+            pages = torch.from_numpy(rng.permutation(pool)[: tokens // S].astype(np.int32)).to(dev)
+            slots = (pages[:, None] * S + ar[None, :]).reshape(-1).contiguous()
+            k = torch.randn((tokens, HKV, D), generator=gen, device=dev).to(torch.bfloat16)
+            v = torch.randn((tokens, HKV, D), generator=gen, device=dev).to(torch.bfloat16)
+            self.ins.append((k, v, slots))
+        self.rng = rng
+
+    def write(self, i):
+        k, v, slots = self.ins[i]
+        self.tq4.reshape_and_cache_bf16(k, v, self.kc, self.vc, self.sc, slots,
+                                        pi_signs=self.w.signs, num_blocks=self.pool,
+                                        block_size=S, inv_sqrt_len=self.w.isl)
+
+
+def extra_workloads(tq4, torch, dev, w, pmc, cpu=True):
+    """Every other BASELINE row, each with its spread and CPU leg."""
     out = {}
-    rng = np.random.default_rng(0x71340002)
     gen = torch.Generator(device=dev)
-    gen.manual_seed(0x71340002)
+    gen.manual_seed(0x71340006)
+    orc = oracle() if cpu else None
     # --- configs[1]: 1024 BF16 tokens, 4096-page pool, permuted pages; 32 input sets rotated
-    wt, pool, nin = 1024, 4096, 32
-    wkc = torch.zeros(pool * HKV * S * D // 2, dtype=torch.int8, device=dev)
-    wvc, wsc = torch.zeros_like(wkc), torch.zeros(2 * pool * HKV * S, device=dev)
-    ar = torch.arange(S, device=dev, dtype=torch.int32)
-    ins = []
-    for _ in range(nin):
-        pages = torch.from_numpy(rng.permutation(pool)[: wt // S].astype(np.int32)).to(dev)
-        slots = (pages[:, None] * S + ar[None, :]).reshape(-1).contiguous()
-        k = torch.randn((wt, HKV, D), generator=gen, device=dev).to(torch.bfloat16)
-        v = torch.randn((wt, HKV, D), generator=gen, device=dev).to(torch.bfloat16)
-        ins.append((k, v, slots))
-
-    def write(i):
-        k, v, slots = ins[i]
-        tq4.reshape_and_cache_bf16(k, v, wkc, wvc, wsc, slots, pi_signs=w.signs,
-                                   num_blocks=pool, block_size=S, inv_sqrt_len=w.isl)
-
-    wms, _, _ = graph_time(torch, [lambda i=i: write(i) for i in range(nin)], 512, 64)
+    wt, nin = 1024, 32
+    wr = WriterInputs(tq4, torch, dev, w, nin, wt)
+    res = time_launches(torch, [lambda i=i: wr.write(i) for i in range(nin)], 512, 64)
     wbytes = writer_algorithmic_bytes(wt, HKV, D, 2)
-    out["reshape_and_cache"] = {"workload": "configs[1] BF16 1024 tokens", "us": round(wms * 1e3, 3),
-                                "tokens_per_s": round(wt / (wms * 1e-3), 1),
-                                "GBps": round(wbytes / (wms * 1e-3) / 1e9, 2),
-                                "algorithmic_bytes": wbytes}
-    log(f"reshape_and_cache: {wms * 1e3:.2f} us -> {wt / (wms * 1e-3) / 1e6:.1f} M tokens/s")
+    row = {"workload": "configs[1] BF16 1024 tokens -> 4096-page pool", **row_times(res),
+           "tokens_per_s": round(wt / (res["ms"] * 1e-3), 1),
+           "GBps": round(wbytes / (res["ms"] * 1e-3) / 1e9, 2), "algorithmic_bytes": wbytes,
+           "roofline": roofline(wbytes, res["ms"], "strip_writer<128,bf16,1>@512", pmc)}
+    if cpu:
+        from oracle_bindings import IN_BF16
+        k, v, slots = (t.cpu() for t in wr.ins[0])
+        hk = k.view(torch.int16).numpy().view(np.uint16)
+        hv = v.view(torch.int16).numpy().view(np.uint16)
+        hs = slots.numpy()
+        nbytes = wr.pool * HKV * S * D // 2
+        ck, cv = np.zeros(nbytes, np.int8), np.zeros(nbytes, np.int8)
+        cs = np.zeros(2 * wr.pool * HKV * S, np.float32)
+        row["cpu_baseline"] = cpu_leg(
+            lambda t: orc.reshape_and_cache(IN_BF16, hk, hv, ck, cv, cs, hs, w.signs_np, HKV, D, S,
+                                            wr.pool, np.float32(w.isl), threads=t),
+            wt, "tokens/s", "oracle/tq4_oracle.c writer, the same 1024 tokens", 2.0, wt // 16)
+    out["reshape_and_cache"] = row
+    log(f"reshape_and_cache: {res['ms'] * 1e3:.2f} us -> {wt / (res['ms'] * 1e-3) / 1e6:.1f} "
+        f"M tokens/s")
 
-    # --- configs[1], secondary: the same 1024 tokens at token-granular slots
+    # --- configs[1], secondary: the same tokens at token-granular slots
     # through the scatter writer, which merges each token into its value
     # strip (RMW). The writer's contract gives a strip one owner per launch,
     # so the slots are a random token position in each of 1024 distinct
     # strips (of the pool's 4096).
+    rng = wr.rng
     sins = []
     for i in range(nin):
-        k, v, _ = ins[i]
-        strips = rng.permutation(pool * S // 16)[:wt]
+        k, v, _ = wr.ins[i]
+        strips = rng.permutation(wr.pool * S // 16)[:wt]
         sl = torch.from_numpy((strips * 16 + rng.integers(0, 16, wt)).astype(np.int32)).to(dev)
         sins.append((k, v, sl))
 
     def scatter(i):
         k, v, sl = sins[i]
-        tq4.reshape_scatter(k, v, wkc, wvc, wsc, sl, w.signs, num_blocks=pool, block_size=S,
-                            inv_sqrt_len=w.isl)
+        tq4.reshape_scatter(k, v, wr.kc, wr.vc, wr.sc, sl, w.signs, num_blocks=wr.pool,
+                            block_size=S, inv_sqrt_len=w.isl)
 
-    sms_, _, _ = graph_time(torch, [lambda i=i: scatter(i) for i in range(nin)], 512, 64)
-    sbytes_ = wbytes + wt * HKV * 2 * (D * S // 2)  # + the value-strip read and write-back
-    out["reshape_scatter"] = {"workload": "configs[1] secondary: 1024 BF16 tokens, one per "
-                                          "strip at random positions (value-strip RMW)", "us": round(sms_ * 1e3, 3),
-                              "tokens_per_s": round(wt / (sms_ * 1e-3), 1),
-                              "GBps": round(sbytes_ / (sms_ * 1e-3) / 1e9, 2),
-                              "algorithmic_bytes": sbytes_}
-    log(f"reshape_scatter: {sms_ * 1e3:.2f} us -> {wt / (sms_ * 1e-3) / 1e6:.1f} M tokens/s")
+    res = time_launches(torch, [lambda i=i: scatter(i) for i in range(nin)], 512, 64)
+    sbytes = wbytes + wt * HKV * 2 * (D * S // 2)  # + the value-strip read and write-back
+    row = {"workload": "configs[1] secondary: 1024 BF16 tokens, one per strip at random "
+                       "positions (value-strip RMW)", **row_times(res),
+           "tokens_per_s": round(wt / (res["ms"] * 1e-3), 1),
+           "GBps": round(sbytes / (res["ms"] * 1e-3) / 1e9, 2), "algorithmic_bytes": sbytes}
+    if cpu:
+        k, v, sl = (t.cpu() for t in sins[0])
+        hk = k.view(torch.int16).numpy().view(np.uint16)
+        hv = v.view(torch.int16).numpy().view(np.uint16)
+        hs = sl.numpy()
+        cu = np.array([0, wt], np.int32)
+        row["cpu_baseline"] = cpu_leg(
+            lambda t: orc.reshape_scatter(hk, hv, ck, cv, cs, hs, w.signs_np, cu, 1, HKV, D, S,
+                                          wr.pool, 0, HKV, np.float32(w.isl)),
+            wt, "tokens/s", "oracle/tq4_oracle.c scatter writer (single-threaded; the "
+            "'all cores' run is the same call), the same 1024 tokens", 1.0, 1)
+    out["reshape_scatter"] = row
+    log(f"reshape_scatter: {res['ms'] * 1e3:.2f} us")
+
+    # --- N2: the vllm-ascend RMS codec writer on the same 1024 BF16 tokens
+    # (rows at slot * kv_heads, the slot's 8-float scale record)
+    rpool = wr.pool * S
+    rkc = torch.zeros(rpool * HKV * D // 2, dtype=torch.int8, device=dev)
+    rvc = torch.zeros_like(rkc)
+    rsc = torch.zeros(rpool * tq4.rms_scale_slot_floats(HKV), device=dev)
+
+    def rms(i):
+        k, v, slots = wr.ins[i]
+        tq4.rms_reshape_and_cache(k, v, rkc, rvc, rsc, slots, w.signs, num_blocks=wr.pool,
+                                  block_size=S, inv_sqrt_len=w.isl)
+
+    res = time_launches(torch, [lambda i=i: rms(i) for i in range(nin)], 512, 64)
+    rbytes = rms_writer_algorithmic_bytes(wt, HKV, D, 2)
+    row = {"workload": "N2 RMS + threshold codec writer, 1024 BF16 tokens (the reference "
+                       "bench's baseline writer)", **row_times(res),
+           "tokens_per_s": round(wt / (res["ms"] * 1e-3), 1),
+           "GBps": round(rbytes / (res["ms"] * 1e-3) / 1e9, 2), "algorithmic_bytes": rbytes}
+    if cpu:
+        k, v, slots = (t.cpu() for t in wr.ins[0])
+        hk = k.view(torch.int16).numpy().view(np.uint16)
+        hv = v.view(torch.int16).numpy().view(np.uint16)
+        hs = slots.numpy()
+        ok = np.zeros(rpool * HKV * D // 2, np.int8)
+        ov = np.zeros_like(ok)
+        os_ = np.zeros(rpool * tq4.rms_scale_slot_floats(HKV), np.float32)
+        row["cpu_baseline"] = cpu_leg(
+            lambda t: orc.rms_reshape_and_cache(1, hk, hv, ok, ov, os_, hs, w.signs_np, HKV, D,
+                                                S, wr.pool, wt, np.float32(w.isl)),
+            wt, "tokens/s", "oracle/tq4_oracle.c RMS codec writer (single-threaded; the "
+            "'all cores' run is the same call), the same 1024 tokens", 1.0, 1)
+    out["rms_reshape_and_cache"] = row
+    log(f"rms writer: {res['ms'] * 1e3:.2f} us")
 
     # --- configs[0]: one 16-token A8 strip, uniform ints in [-127, 127], slot = identity
     # into page 0 (latency-bound: one strip x 8 heads)
@@ -381,70 +783,70 @@ def extra_workloads(tq4, torch, dev, w, cpu=True):
 
     def write_a8(i):
         k, v = a8[i]
-        tq4.reshape_and_cache_a8(k, v, wkc, wvc, wsc, ident, pi_signs=w.signs, num_blocks=pool,
-                                 block_size=S, inv_sqrt_len=w.isl)
+        tq4.reshape_and_cache_a8(k, v, wr.kc, wr.vc, wr.sc, ident, pi_signs=w.signs,
+                                 num_blocks=wr.pool, block_size=S, inv_sqrt_len=w.isl)
 
-    ams, _, _ = graph_time(torch, [lambda i=i: write_a8(i) for i in range(8)], 512, 64)
+    res = time_launches(torch, [lambda i=i: write_a8(i) for i in range(8)], 512, 64,
+                        chunk=64)
     abytes = writer_algorithmic_bytes(S, HKV, D, 1)
-    out["reshape_and_cache_a8"] = {"workload": "configs[0] A8, one 16-token strip",
-                                   "us": round(ams * 1e3, 3),
-                                   "tokens_per_s": round(S / (ams * 1e-3), 1),
-                                   "algorithmic_bytes": abytes}
-    log(f"reshape_and_cache A8 strip: {ams * 1e3:.2f} us")
+    row = {"workload": "configs[0] A8, one 16-token strip", **row_times(res),
+           "tokens_per_s": round(S / (res["ms"] * 1e-3), 1), "algorithmic_bytes": abytes}
+    if cpu:
+        from oracle_bindings import IN_INT8
+        hk, hv = a8[0][0].cpu().numpy(), a8[0][1].cpu().numpy()
+        hs = ident.cpu().numpy()
+        row["cpu_baseline"] = cpu_leg(
+            lambda t: orc.reshape_and_cache(IN_INT8, hk, hv, ck, cv, cs, hs, w.signs_np, HKV, D,
+                                            S, wr.pool, np.float32(w.isl), threads=t),
+            S, "tokens/s", "oracle/tq4_oracle.c writer, the same A8 strip (one task: the "
+            "'all cores' run uses one thread)", 1.0, 1)
+    out["reshape_and_cache_a8"] = row
+    log(f"reshape_and_cache A8 strip: {res['ms'] * 1e3:.2f} us")
 
-    # --- split sweep. Sequences at ctx 4096 / 16384 / 32768 (and
-    # the ragged 4096 + 7) over random pages of the headline pool; each time
-    # rotates over enough sequences that >= 512 MB are read between re-reads.
-    out["split_sweep"] = split_sweep(tq4, torch, dev, w)
+    # --- split sweep over the headline pool
+    out["split_sweep"] = split_sweep(tq4, torch, dev, w, orc)
 
-    # --- batched decode step, 64 sequences, ctx ~U[512, 8192]
-    r = np.random.default_rng(0x71340005)
-    ctxs = [int(x) for x in r.integers(512, 8193, 64)]
-    bsz = len(ctxs)
-    npages = [(c + 1 + S - 1) // S for c in ctxs]  # room for the step's new token
-    pool5 = int(sum(npages) * 1.1) + 16
-    maxb = max(npages)
-    perm = r.permutation(pool5).astype(np.int32)
-    tab = np.zeros((bsz, maxb), np.int32)
-    at = 0
-    for b, n in enumerate(npages):
-        tab[b, :n] = perm[at:at + n]
-        at += n
-    tables = torch.from_numpy(tab).to(dev)
-    kc5 = torch.randint(-128, 127, (pool5 * HKV * S * D // 2,), dtype=torch.int8, device=dev,
-                        generator=gen)
-    vc5 = torch.randint(-128, 127, kc5.shape, dtype=torch.int8, device=dev, generator=gen)
-    sc5 = torch.rand(2 * pool5 * HKV * S, device=dev, generator=gen) * 0.05 + 0.01
-    ctx_now = torch.tensor([c + 1 for c in ctxs], dtype=torch.int32, device=dev)
-    slot_np = np.array([tab[b, c // S] * S + c % S for b, c in enumerate(ctxs)], np.int32)
-    slots5 = torch.from_numpy(slot_np).to(dev)
-    q5 = torch.randn((bsz, HQ, D), generator=gen, device=dev).to(torch.bfloat16)
-    kn = torch.randn((bsz, HKV, D), generator=gen, device=dev).to(torch.bfloat16)
-    vn = torch.randn((bsz, HKV, D), generator=gen, device=dev).to(torch.bfloat16)
-    out5 = torch.empty_like(q5)
-    # configs[4] asks for a split-K decode. tq4_decode_auto_splits picks one
-    # split here (its rule knows the batch's longest context, not the spread);
-    # three splits, with the persistent kernel ordering the last splits
-    # longest first, measured best for this batch (K = 1..8 sweep).
-    k5 = 3
-    ws5 = tq4.decode_workspace(bsz, HQ, HKV, D, k5)
-
-    def step():
-        tq4.reshape_scatter(kn, vn, kc5, vc5, sc5, slots5, w.signs, num_blocks=pool5,
-                            block_size=S, inv_sqrt_len=w.isl)
-        tq4.paged_decode(q5, kc5, vc5, sc5, tables, ctx_now, w.signs, HKV, S, pool5, out=out5,
-                         workspace=ws5, num_splits=k5, scale=w.scale, inv_sqrt_len=w.isl)
-
-    sms, _, _ = graph_time(torch, [step] * 8, 64, 16)
-    sbytes = decode_algorithmic_bytes([c + 1 for c in ctxs], HQ, HKV, D, S) + bsz * (
-        2 * HKV * D * 2 + HKV * D // 2 + 2 * HKV * 4 + 4) + bsz * HKV * 1024  # + value-strip RMW
-    out["batched_step"] = {"workload": "configs[4] 64 seqs ctx~U[512,8192]: scatter 64 tokens + "
-                                       "split-K decode", "us": round(sms * 1e3, 3),
-                           "tokens_per_s": round(bsz / (sms * 1e-3), 1),
-                           "GBps": round(sbytes / (sms * 1e-3) / 1e9, 2),
-                           "pct_hbm_peak": round(100 * sbytes / (sms * 1e-3) / 1e9 / HBM_PEAK_GBS, 2),
-                           "splits": k5, "algorithmic_bytes": sbytes, "cache": "warm (one step)"}
-    log(f"batched step: {sms * 1e3:.2f} us -> {sbytes / (sms * 1e-3) / 1e9:.0f} GB/s")
+    # --- the batched step, two batches rotated (each 0.3 GB,
+    # more than the Infinity Cache, so each step reads its batch cold)
+    bats = [Batch(tq4, torch, dev, 0x71340050 + k, w.signs) for k in range(2)]
+    res = time_launches(torch, [b.step for b in bats], 32, 4, samples=16, chunk=8)
+    t_step = sum(tq4.decode_poll_timeouts(b.ws, 64, HKV) for b in bats)
+    resd = time_launches(torch, [b.decode for b in bats], 32, 4, samples=16, chunk=8)
+    t_step += sum(tq4.decode_poll_timeouts(b.ws, 64, HKV) for b in bats)
+    sbytes, dbytes = bats[0].step_bytes(), bats[0].decode_bytes()
+    bsz = len(bats[0].ctxs)
+    row = {"workload": "configs[4] 64 seqs ctx~U[512,8192]: scatter 64 tokens + split-K decode",
+           **row_times(res), "tokens_per_s": round(bsz / (res["ms"] * 1e-3), 1),
+           "GBps": round(sbytes / (res["ms"] * 1e-3) / 1e9, 2),
+           "pct_hbm_peak": round(100 * sbytes / (res["ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 2),
+           "splits": Batch.K, "algorithmic_bytes": sbytes,
+           "cache": "cold (2 batches of 0.3 GB rotated)",
+           "decode_only": {**row_times(resd), "GBps": round(dbytes / (resd["ms"] * 1e-3) / 1e9, 2),
+                           "algorithmic_bytes": dbytes},
+           "roofline": roofline(dbytes, resd["ms"], "decode_persistent_kernel<128>@512", pmc),
+           "poll_timeouts": t_step}
+    if t_step:
+        row["INVALID"] = f"{t_step} combine rows gave up their bounded poll"
+    if cpu:
+        # a bounded sample: the first 8 sequences of batch 0 (decode + their scatter)
+        b0 = bats[0]
+        nseq = 8
+        hq = b0.q[:nseq].cpu().view(torch.int16).numpy().view(np.uint16)
+        hk, hv, hs = b0.kc.cpu().numpy(), b0.vc.cpu().numpy(), b0.sc.cpu().numpy()
+        htab = np.ascontiguousarray(b0.tab_np[:nseq])
+        hctx = b0.ctx_now[:nseq].cpu().numpy()
+        sample_bytes = decode_algorithmic_bytes([c + 1 for c in b0.ctxs[:nseq]], HQ, HKV, D, S)
+        row["cpu_baseline"] = cpu_leg(
+            lambda t: orc.paged_decode(hq, hk, hv, hs, htab, hctx, w.signs_np, None, HQ, HKV, D,
+                                       S, b0.pool, Batch.K, np.float32(b0.isl),
+                                       np.float32(b0.isl), 1, threads=t),
+            sample_bytes, "GB/s", f"oracle/tq4_oracle.c decode of sequences 0..{nseq - 1} of the "
+            f"batch (ctx sum {sum(b0.ctxs[:nseq]) + nseq}, {Batch.K} splits)", 3.0,
+            nseq * HKV * Batch.K)
+    out["batched_step"] = row
+    log(f"batched step: {res['ms'] * 1e3:.2f} us -> {sbytes / (res['ms'] * 1e-3) / 1e9:.0f} GB/s; "
+        f"decode only {resd['ms'] * 1e3:.2f} us")
+    del bats
 
     # --- codebook leaves (HBM streams): Lloyd-Max 4-bit over 32M FP32 values
     # (in + centroids + codes), ICDF over 64M FP16 values (in + codes)
@@ -452,21 +854,23 @@ def extra_workloads(tq4, torch, dev, w, cpu=True):
     xl = torch.randn(nl, generator=gen, device=dev)
     rl = torch.empty_like(xl)
     cl = torch.empty(nl // 2, dtype=torch.uint8, device=dev)
-    lms, _, _ = graph_time(torch, [lambda: tq4.lloydmax_quantize(xl, 4, 0, dst=rl, codes=cl)],
-                           20, 4)
+    res_l = time_launches(torch, [lambda: tq4.lloydmax_quantize(xl, 4, 0, dst=rl, codes=cl)],
+                          20, 4, samples=8, chunk=4)
     lbytes = nl * (4 + 4) + nl // 2
     xi = torch.randn(2 * nl, generator=gen, device=dev).to(torch.float16)
     ci = torch.empty(nl, dtype=torch.uint8, device=dev)
-    ims, _, _ = graph_time(torch, [lambda: tq4.icdf_quantize(xi, out=ci)], 20, 4)
+    res_i = time_launches(torch, [lambda: tq4.icdf_quantize(xi, out=ci)], 20, 4, samples=8,
+                          chunk=4)
     ibytes = 2 * nl * 2 + nl
     out["codebook"] = {
-        "lloydmax4_32M_fp32": {"us": round(lms * 1e3, 2), "GBps": round(lbytes / (lms * 1e-3) / 1e9, 1),
+        "lloydmax4_32M_fp32": {**row_times(res_l),
+                               "GBps": round(lbytes / (res_l["ms"] * 1e-3) / 1e9, 1),
                                "algorithmic_bytes": lbytes},
-        "icdf_64M_fp16": {"us": round(ims * 1e3, 2), "GBps": round(ibytes / (ims * 1e-3) / 1e9, 1),
+        "icdf_64M_fp16": {**row_times(res_i), "GBps": round(ibytes / (res_i["ms"] * 1e-3) / 1e9, 1),
                           "algorithmic_bytes": ibytes}}
-    log(f"codebook: Lloyd-Max {lbytes / (lms * 1e-3) / 1e9:.0f} GB/s, "
-        f"ICDF {ibytes / (ims * 1e-3) / 1e9:.0f} GB/s")
-    out["kv4fp8_decode"] = kv4fp8_workloads(tq4, torch, dev, cpu)
+    log(f"codebook: Lloyd-Max {lbytes / (res_l['ms'] * 1e-3) / 1e9:.0f} GB/s, "
+        f"ICDF {ibytes / (res_i['ms'] * 1e-3) / 1e9:.0f} GB/s")
+    out["kv4fp8_decode"] = kv4fp8_workloads(tq4, torch, dev, orc)
     return out
 
 
@@ -477,7 +881,7 @@ def kv4fp8_cache_bytes(tokens, ctx, kv_heads):
     return tokens * ctx * (kv_heads * 256 + 32)
 
 
-def kv4fp8_workloads(tq4, torch, dev, cpu=True):
+def kv4fp8_workloads(tq4, torch, dev, orc=None):
     """The KV4/FP8 NZ-tiled decode: the reference benchmark's shape
     (bench_turboquant_decode_splitk --impl fused-opt: 1 request, 16 q heads over
     one KV head, D=256, 128-row pages, FP32 pre-rotated query, FP16 output) at
@@ -486,67 +890,63 @@ def kv4fp8_workloads(tq4, torch, dev, cpu=True):
     gen = torch.Generator(device=dev)
     gen.manual_seed(0x4B5F8)
     gain = 2.9832882881
-    for name, (T, H, G, S, ctx) in (("ref_shape_1x16q1kv_ctx4096", (1, 1, 16, 128, 4096)),
-                                     ("batched_32x64q4kv_ctx8192", (32, 4, 16, 128, 8192))):
-        pages = (ctx + S - 1) // S
+    for name, (T, H, G, S_, ctx) in (("ref_shape_1x16q1kv_ctx4096", (1, 1, 16, 128, 4096)),
+                                      ("batched_32x64q4kv_ctx8192", (32, 4, 16, 128, 8192))):
+        pages = (ctx + S_ - 1) // S_
         P = T * pages
-        key = torch.randint(0, 256, (P * S * H * 128,), dtype=torch.uint8, device=dev,
+        key = torch.randint(0, 256, (P * S_ * H * 128,), dtype=torch.uint8, device=dev,
                             generator=gen)
         val = torch.randint(0, 256, key.shape, dtype=torch.uint8, device=dev, generator=gen)
-        sc = (torch.rand(P * S * 8, device=dev, generator=gen) * 1.5 + 0.5) * gain
+        sc = (torch.rand(P * S_ * 8, device=dev, generator=gen) * 1.5 + 0.5) * gain
         tb = torch.randperm(P, device=dev, generator=gen).to(torch.int32).view(T, pages)
         ln = torch.full((T,), ctx, dtype=torch.int32, device=dev)
         q = torch.randn((T, H * G, 256), device=dev, generator=gen)
         o = torch.empty((T, H * G, 256), dtype=torch.float16, device=dev)
-        L = tq4.fused_decode_opt_launch(T, H * G, H, S, pages, num_blocks=P)
+        L = tq4.fused_decode_opt_launch(T, H * G, H, S_, pages, num_blocks=P)
         ws = torch.zeros(tq4.kv4fp8_workspace_bytes(L), dtype=torch.uint8, device=dev)
-        run = lambda: tq4.kv4fp8_decode(q, key, val, sc, tb, ln, H, S, P, out=o,  # noqa: E731
+        run = lambda: tq4.kv4fp8_decode(q, key, val, sc, tb, ln, H, S_, P, out=o,  # noqa: E731
                                         workspace=ws)
         run()
         torch.cuda.synchronize()
         assert torch.isfinite(o.float()).all(), "kv4fp8 decode produced non-finite values"
-        ms, _, _ = graph_time(torch, [run] * 16, 256 if T == 1 else 64, 32 if T == 1 else 8)
+        r = time_launches(torch, [run], 256 if T == 1 else 64, 32 if T == 1 else 8,
+                          samples=16, chunk=16)
+        timeouts = tq4.kv4fp8_poll_timeouts(ws, T, H * G, H, S_, pages, P)
         nbytes = kv4fp8_cache_bytes(T, ctx, H) + T * H * G * 256 * (4 + 2) + T * pages * 4
-        gbs = nbytes / (ms * 1e-3) / 1e9
-        res[name] = {"us": round(ms * 1e3, 3), "GBps": round(gbs, 1),
+        gbs = nbytes / (r["ms"] * 1e-3) / 1e9
+        res[name] = {**row_times(r), "GBps": round(gbs, 1),
                      "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
                      "tokens": T, "q_heads": H * G, "kv_heads": H, "head_dim": 256,
-                     "ctx": ctx, "page_size": S, "algorithmic_bytes": nbytes,
-                     "cache": "warm" if nbytes < (256 << 20) else "beyond the Infinity Cache"}
-        log(f"kv4fp8 {name}: {ms * 1e3:.2f} us -> {gbs:.0f} GB/s")
-        if cpu and T == 1:
-            # the C oracle (oracle/kv4fp8_oracle.c) on the same inputs, bounded at ~2 s
-            sys.path.insert(0, os.path.join(REPO, "tests"))
-            from oracle_bindings import Oracle
-            orc = Oracle()
-            threads = min(16, os.cpu_count() or 1)
+                     "ctx": ctx, "page_size": S_, "algorithmic_bytes": nbytes,
+                     "cache": "warm" if nbytes < (256 << 20) else "beyond the Infinity Cache",
+                     "poll_timeouts": timeouts}
+        if timeouts:
+            res[name]["INVALID"] = f"{timeouts} combine rows gave up their bounded poll"
+        log(f"kv4fp8 {name}: {r['ms'] * 1e3:.2f} us -> {gbs:.0f} GB/s")
+        if orc is not None and T == 1:
             h = [x.cpu().numpy() for x in (q, key, val, sc, tb, ln)]
-            iters, t0 = 0, time.perf_counter()
-            while time.perf_counter() - t0 < 2.0:
-                orc.kv4fp8_decode(*h, heads=H * G, kv_heads=H, block_size=S, max_blocks=pages,
-                                  num_blocks=P, threads=threads)
-                iters += 1
-            el = time.perf_counter() - t0
-            res[name]["cpu_baseline"] = {
-                "value": round(nbytes * iters / el / 1e9, 4), "unit": "GB/s",
-                "cores": min(threads, T * H),
-                "kind": "port", "us_per_decode": round(el / iters * 1e6, 1),
-                "sample": f"{iters} decodes of this shape by oracle/kv4fp8_oracle.c in "
-                          f"{el:.1f} s (FP64 products; one task per (token, kv head), so "
-                          f"{min(threads, T * H)} thread(s) busy)"}
+            res[name]["cpu_baseline"] = cpu_leg(
+                lambda t: orc.kv4fp8_decode(*h, heads=H * G, kv_heads=H, block_size=S_,
+                                            max_blocks=pages, num_blocks=P, threads=t),
+                nbytes, "GB/s", "oracle/kv4fp8_oracle.c decode of this shape (FP64 products; "
+                "one task per (token, kv head))", 2.0, T * H)
     return res
 
 
-def split_sweep(tq4, torch, dev, w):
-    """the fused decode at ctx {4096, 16384, 32768} x K {2, 4, 8,
-    16, auto}, plus the ragged ctx 4103 at auto."""
+def split_sweep(tq4, torch, dev, w, orc=None):
+    """the fused decode at ctx {4096, 16384, 32768, 65536} x K
+    {2, 4, 8, 16, auto}, plus the ragged ctx 4103 at auto; cold (each time
+    rotates over enough sequences that >= 512 MB are read between re-reads).
+    The CPU leg runs the auto-K row of each context."""
     rng = np.random.default_rng(0x71340004)
     gen = torch.Generator(device=dev)
     gen.manual_seed(0x71340004)
     rows = []
     for ctx, ks in ((4096, (2, 4, 8, 16, 0)), (16384, (2, 4, 8, 16, 0)),
-                    (32768, (2, 4, 8, 16, 0)), (4103, (0,))):
+                    (32768, (2, 4, 8, 16, 0)), (65536, (8, 16, 0)), (4103, (0,))):
         pages = (ctx + S - 1) // S
+        if pages > w.pool:
+            continue
         nseq = max(4, (512 << 20) // (ctx * HKV * (D + 8)))
         tabs = [torch.from_numpy(rng.permutation(w.pool)[:pages].astype(np.int32)[None, :]).to(dev)
                 for _ in range(nseq)]
@@ -564,66 +964,54 @@ def split_sweep(tq4, torch, dev, w):
                                  out=out, workspace=ws, num_splits=kk, scale=w.scale,
                                  inv_sqrt_len=w.isl)
 
-            ms, _, _ = graph_time(torch, [lambda i=i: dec(i) for i in range(nseq)],
-                                  max(256, nseq), max(32, nseq))
-            gbs = nbytes / (ms * 1e-3) / 1e9
-            rows.append({"ctx": ctx, "splits": kk, "auto": k == 0, "us": round(ms * 1e3, 2),
-                         "GBps": round(gbs, 1),
-                         "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
-                         "algorithmic_bytes": nbytes})
+            r = time_launches(torch, [lambda i=i: dec(i) for i in range(nseq)], max(128, nseq),
+                              max(16, nseq // 4), samples=16, chunk=max(8, min(32, nseq)))
+            timeouts = tq4.decode_poll_timeouts(ws, 1, HKV)
+            gbs = nbytes / (r["ms"] * 1e-3) / 1e9
+            row = {"ctx": ctx, "splits": kk, "auto": k == 0, **row_times(r),
+                   "GBps": round(gbs, 1), "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
+                   "algorithmic_bytes": nbytes, "poll_timeouts": timeouts}
+            if timeouts:
+                row["INVALID"] = f"{timeouts} combine rows gave up their bounded poll"
+            if orc is not None and k == 0:
+                hq = qs[0].cpu().view(torch.int16).numpy().view(np.uint16)
+                htab = tabs[0].cpu().numpy()
+                hctx = ctx_t.cpu().numpy()
+                hk, hv, hs = w.host_cache()
+                row["cpu_baseline"] = cpu_leg(
+                    lambda t: orc.paged_decode(hq, hk, hv, hs, htab, hctx, w.signs_np, None, HQ,
+                                               HKV, D, S, w.pool, kk, np.float32(w.scale),
+                                               np.float32(w.isl), 1, threads=t),
+                    nbytes, "GB/s", f"oracle/tq4_oracle.c decode, ctx {ctx}, {kk} splits",
+                    2.0, HKV * kk)
+            rows.append(row)
             log(f"split sweep ctx {ctx} K {kk}{' (auto)' if k == 0 else ''}: "
-                f"{ms * 1e3:.2f} us -> {gbs:.0f} GB/s")
+                f"{r['ms'] * 1e3:.2f} us -> {gbs:.0f} GB/s")
     return {"workload": "configs[3] single-sequence decode, 32q:8kv, d128, page 16, cold "
                         "(rotated sequences)", "rows": rows}
 
 
-def cpu_model():
-    try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    return line.split(":", 1)[1].strip()
-    except OSError:
-        pass
-    return None
+def _host_cache(self):
+    if not hasattr(self, "_host"):
+        self._host = (self.kc.cpu().numpy(), self.vc.cpu().numpy(), self.sc.cpu().numpy())
+    return self._host
 
 
-def cpu_baseline(torch, w, dec_bytes, seconds):
+Workload.host_cache = _host_cache
+
+
+def cpu_decode_leg(torch, w, dec_bytes, seconds):
     """The C oracle's decode of slice 0 on the host cores, bounded in time."""
-    sys.path.insert(0, os.path.join(REPO, "tests"))
-    from oracle_bindings import Oracle
-    o = Oracle()
-    threads = min(16, os.cpu_count() or 1)
+    o = oracle()
     h_q = w.q[0].view(torch.int16).cpu().numpy().view(np.uint16)
-    h_kc, h_vc, h_sc = w.kc.cpu().numpy(), w.vc.cpu().numpy(), w.sc.cpu().numpy()
+    h_kc, h_vc, h_sc = w.host_cache()
     h_tab, h_ctx = w.tables[0].cpu().numpy(), w.ctx.cpu().numpy()
-
-    def timed(nthreads, budget):
-        iters, t0 = 0, time.perf_counter()
-        while True:
-            o.paged_decode(h_q, h_kc, h_vc, h_sc, h_tab, h_ctx, w.signs_np, None, HQ, HKV, D, S,
-                           w.pool, w.splits, np.float32(w.scale), np.float32(w.isl), 1,
-                           threads=nthreads)
-            iters += 1
-            el = time.perf_counter() - t0
-            if el >= budget:
-                return iters, el
-
-    iters1, el1 = timed(1, seconds / 2)
-    iters, el = timed(threads, seconds)
-    try:
-        nproc = len(os.sched_getaffinity(0))
-    except AttributeError:
-        nproc = os.cpu_count()
-    return {"value": round(dec_bytes * iters / el / 1e9, 4), "unit": "GB/s", "cores": threads,
-            "kind": "port",
-            "sample": f"{iters} configs[2] decodes (B=1, 32q:8kv, d128, ctx4096, {w.splits} "
-                      f"splits) by oracle/tq4_oracle.c in {el:.1f} s on {threads} threads",
-            "us_per_decode": round(el / iters * 1e6, 1),
-            "single_thread": {"value": round(dec_bytes * iters1 / el1 / 1e9, 4), "unit": "GB/s",
-                              "us_per_decode": round(el1 / iters1 * 1e6, 1),
-                              "sample": f"{iters1} decodes in {el1:.1f} s on 1 thread"},
-            "nproc": nproc, "cpu_model": cpu_model()}
+    return cpu_leg(
+        lambda t: o.paged_decode(h_q, h_kc, h_vc, h_sc, h_tab, h_ctx, w.signs_np, None, HQ, HKV,
+                                 D, S, w.pool, w.splits, np.float32(w.scale), np.float32(w.isl),
+                                 1, threads=t),
+        dec_bytes, "GB/s", f"oracle/tq4_oracle.c decode of one configs[2] sequence (B=1, "
+        f"32q:8kv, d128, ctx4096, {w.splits} splits)", seconds, HKV * w.splits)
 
 
 if __name__ == "__main__":
