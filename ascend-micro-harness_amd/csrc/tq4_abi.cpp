@@ -19,15 +19,19 @@ bool head_size_ok(uint32_t d) { return d == 64 || d == 128 || d == 256; }
 
 int launched(hipError_t e) { return e == hipSuccess ? TQ4_OK : TQ4_ERR_LAUNCH; }
 
-// Fused-decode workspace tail: one 256-byte block holding the work-queue
-// counter of the persistent kernel (word 0) and the sticky poll-timeout count
-// (word 1), then one split-ticket word per (seq, kv head).
-constexpr size_t kQueueBytes = 256;
+// Fused-decode workspace tail: one 1 KiB block holding the persistent
+// kernel's work-queue counters (word 32x for sub-queue x, one 128-byte line
+// each) and the sticky poll-timeout count (word 1), then one split ticket per
+// (seq, kv head), each on its own 128-byte line: atomics on one line are
+// served one after another, so counters that many workgroups hit at once
+// must not share one.
+constexpr size_t kQueueBytes = 1024;
 constexpr uint32_t kFlagsKnown = TQ4_DECODE_QUERY_ROTATED | TQ4_DECODE_TEST_POLL_BOUND |
                                  TQ4_DECODE_TEST_WITHHOLD;
 size_t ticket_bytes(uint32_t num_seqs, uint32_t num_kv_heads)
 {
-    return ((size_t)num_seqs * num_kv_heads * sizeof(uint32_t) + 255) & ~(size_t)255;
+    return ((size_t)num_seqs * num_kv_heads * tq4::kTicketStride * sizeof(uint32_t) + 255) &
+           ~(size_t)255;
 }
 
 int writer_checks(const void* key, const void* value, const int8_t* key_cache,

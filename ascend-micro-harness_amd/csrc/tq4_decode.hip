@@ -566,8 +566,8 @@ __device__ __forceinline__ void decode_item(const DecodeParams& p, const uint32_
     uint32_t ticket = 0;
     if constexpr (MODE == 1) {
         if (p.K > 1 && tid == 0)
-            ticket = __hip_atomic_fetch_add(p.counters + (size_t)seq * p.Hkv + kvh, 1u,
-                                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            ticket = __hip_atomic_fetch_add(p.counters + ((size_t)seq * p.Hkv + kvh) * kTicketStride,
+                                            1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     after_issue();
 
@@ -843,8 +843,8 @@ __device__ __forceinline__ void decode_item(const DecodeParams& p, const uint32_
             // never the combiner's when more than one split is live).
             const int last = ticket == k_live - 1;
             if (last)
-                __hip_atomic_store(p.counters + (size_t)seq * p.Hkv + kvh, 0u, __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(p.counters + ((size_t)seq * p.Hkv + kvh) * kTicketStride, 0u,
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             *flag = last | (p.withhold && ticket == 0 && !last ? 2 : 0);
         }
     }
@@ -1033,13 +1033,16 @@ __global__ TQ4_DECODE_ATTRS void decode_kernel(DecodeParams p)
 // zero-context item of an empty sequence), longest first for batches of up to
 // kLptMaxSeqs sequences, so their spread of sizes packs the tail. Every
 // workgroup derives the order from the context lengths (a prefix over
-// sequences and a rank of the last splits, staged in LDS). A workgroup takes item blockIdx.x,
-// then one item at a time from an agent-scope queue counter, fetched once the
-// current item's first strip loads are out, so its round trip -- long when
-// many workgroups fetch at once -- hides under the item. Each of the n_items
-// fetches returns a distinct value and the one that returns n_items - 1 is
-// the last: it resets the counter (every workgroup's final fetch is its
-// failing one, so the fetches number exactly n_items). Nothing waits on a
+// sequences and a rank of the last splits, staged in LDS). The items are
+// dealt over kSubQueues interleaved sub-queues (items x, x + nq, ...), each
+// an agent-scope counter on its own 128-byte line serving workgroups x,
+// x + nq, ...: one counter for the whole launch serves its fetches one at a
+// time. A workgroup takes item blockIdx.x, then one item at a time from its
+// sub-queue, fetched once the current item's first strip loads are out, so
+// its round trip hides under the item. Each of a sub-queue's `count`
+// fetches returns a distinct value and the one that returns count - 1 is the
+// last: it resets the counter (every workgroup's final fetch is its failing
+// one, so the fetches number exactly `count`). Nothing waits on a
 // workgroup that has not started: the combiner of a (seq, kv head) waits only
 // for splits that took their ticket before it, each in the hands of a running
 // workgroup that only streams and exports before it fetches again.
@@ -1140,6 +1143,14 @@ void decode_persistent_kernel(DecodeParams p)
     }
     const uint32_t n_full = full[p.B - 1];
     const uint32_t n_items = n_full + p.B * p.Hkv;
+    // kSubQueues interleaved queues (one counter line each): sub-queue x
+    // holds items x, x + nq, x + 2nq, ... and serves workgroups x, x + nq,
+    // ...; one shared counter would serve every fetch of the launch in turn.
+    const uint32_t nq = gridDim.x < kSubQueues ? gridDim.x : kSubQueues;
+    const uint32_t x = blockIdx.x % nq;
+    const uint32_t nwg = (gridDim.x - x + nq - 1) / nq;  // workgroups of sub-queue x
+    const uint32_t count = n_items > x ? (n_items - x + nq - 1) / nq : 0u;  // its items
+    uint32_t* subq = p.queue + kTicketStride * x;
     uint32_t item = blockIdx.x;
     while (item < n_items) {
         uint32_t fetched = 0;
@@ -1171,13 +1182,13 @@ void decode_persistent_kernel(DecodeParams p)
         // loads (decode_item's hook); its value is read after the item
         decode_item<D, 1, false>(p, seq, kvh, split, [&]() {
             if (tid == 0)
-                fetched = __hip_atomic_fetch_add(p.queue, 1u, __ATOMIC_RELAXED,
+                fetched = __hip_atomic_fetch_add(subq, 1u, __ATOMIC_RELAXED,
                                                  __HIP_MEMORY_SCOPE_AGENT);
         });
         if (tid == 0) {
-            if (fetched == n_items - 1)
-                __hip_atomic_store(p.queue, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            *next_lds = gridDim.x + fetched;
+            if (fetched == count - 1)
+                __hip_atomic_store(subq, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            *next_lds = x + nq * (nwg + fetched);
         }
         // LDS-only barriers: the item's record stores are not waited for
         // here; the next item's phase-0 loads go out first.

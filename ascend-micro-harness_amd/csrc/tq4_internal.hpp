@@ -96,6 +96,11 @@ hipError_t launch_fp8_probe(hipStream_t stream, const float* in, uint16_t* out, 
 // Byte offset of the counter region inside a workspace of K splits.
 size_t decode_records_bytes(uint32_t B, uint32_t Hq, uint32_t D, uint32_t K);
 
+// Words between consecutive split tickets (one 128-byte line each), and
+// between the persistent kernel's work-queue counters (up to kSubQueues).
+constexpr uint32_t kTicketStride = 32;
+constexpr uint32_t kSubQueues = 4;
+
 // The no-allocation decode's static scratch (tq4_decode.hip): its size, and
 // its device address on the current device (set up, and zeroed on `stream`,
 // at the first call on each device).
