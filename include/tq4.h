@@ -238,8 +238,14 @@ int tq4_paged_decode_noalloc(void* stream, const uint16_t* q, const int8_t* key_
  * ((seq*num_heads + head)*num_splits + split)*(head_size + 4) holds
  * [m, l, 0, 0, acc[head_size]] -- m the running max of the natural-log score,
  * l = sum exp(s - m), acc = sum exp(s - m) * v in the rotated basis.
- * Replaces launch_turboquant_paged_decode_splitk_aic
- * (kernels/ops/turboquant/turboquant_paged_decode_attention.cpp:1727-1766). */
+ * Modelled on launch_turboquant_paged_decode_splitk_aic
+ * (kernels/ops/turboquant/turboquant_paged_decode_attention.cpp:1727-1766):
+ * the same Partition and recurrence, but not its argument list or record --
+ * per-sequence context lengths instead of one seq_len and a page window, a
+ * [num_seqs][max_blocks_per_seq] table, pi_signs instead of a 256 x 256
+ * pi_table, one [m, l, 0, 0, acc] record per (seq, q head, split) instead of
+ * [m(8) | l(8) | acc] per packed row, and an FP16 q operand (finer than the
+ * reference device's BF16 q_rot). */
 int tq4_paged_decode_partials(void* stream, const uint16_t* q, const int8_t* key_cache,
                               const int8_t* value_cache, const float* scale_cache,
                               const int32_t* block_tables, const int32_t* context_lens,
