@@ -285,13 +285,25 @@ __device__ void combine_records(const float* rr, uint32_t K, int lane, float (&v
         float lw = 0.0f;
 #pragma unroll
         for (int j = 0; j < CC; ++j) a[j] *= sc;
+        if (k0 + 2 * NS <= K) {
+            // every slot of the chunk holds a split (wave-uniform): one
+            // decode and one fma per word, no select
 #pragma unroll
-        for (int i = 0; i < NS; ++i) {
-            const float w = __builtin_amdgcn_exp2f(mk[i] - Mn);
-            lw += vi[i] ? __uint_as_float(hw[i][1] ^ x) * w : 0.0f;
+            for (int i = 0; i < NS; ++i) {
+                const float w = __builtin_amdgcn_exp2f(mk[i] - Mn);
+                lw = fmaf(__uint_as_float(hw[i][1] ^ x), w, lw);
 #pragma unroll
-            for (int j = 0; j < CC; ++j)
-                a[j] += vi[i] ? __uint_as_float(aw[i][j] ^ x) * w : 0.0f;
+                for (int j = 0; j < CC; ++j) a[j] = fmaf(__uint_as_float(aw[i][j] ^ x), w, a[j]);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < NS; ++i) {
+                const float w = __builtin_amdgcn_exp2f(mk[i] - Mn);
+                lw += vi[i] ? __uint_as_float(hw[i][1] ^ x) * w : 0.0f;
+#pragma unroll
+                for (int j = 0; j < CC; ++j)
+                    a[j] += vi[i] ? __uint_as_float(aw[i][j] ^ x) * w : 0.0f;
+            }
         }
         L = L * sc + (lw + xor_lanes(lw, 32));
         M = Mn;
