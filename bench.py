@@ -284,6 +284,10 @@ def print_pmc_table(out):
         ("SQ_VALU_MFMA_BUSY_CYCLES", lambda e: f"{c(e, 'SQ_VALU_MFMA_BUSY_CYCLES'):.0f}"),
         ("SQ_INSTS_VMEM_RD", lambda e: f"{c(e, 'SQ_INSTS_VMEM_RD'):.0f}"),
         ("SQ_WAIT_INST_ANY / SQ_WAIT_ANY", lambda e: f"{c(e, 'SQ_WAIT_INST_ANY'):.0f} / {c(e, 'SQ_WAIT_ANY'):.0f}"),
+        ("SQ_VMEM_TA_ADDR_FIFO_FULL / _CMD_FIFO_FULL",
+         lambda e: f"{c(e, 'SQ_VMEM_TA_ADDR_FIFO_FULL'):.0f} / {c(e, 'SQ_VMEM_TA_CMD_FIFO_FULL'):.0f}"),
+        ("TA_ADDR_STALLED_BY_TC_CYCLES_sum / TA_BUSY_avr",
+         lambda e: f"{c(e, 'TA_ADDR_STALLED_BY_TC_CYCLES_sum'):.0f} / {c(e, 'TA_BUSY_avr'):.0f}"),
     ]
     print("| per dispatch | " + " | ".join(f"`{k}`" for k in keys) + " |")
     print("|---|" + "---|" * len(keys))
