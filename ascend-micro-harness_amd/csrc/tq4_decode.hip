@@ -657,6 +657,9 @@ __device__ __forceinline__ void decode_item(const DecodeParams& p, const uint32_
     float mo = m_used;
     float lpart = 0.0f;
     float thr = kTau + sh;
+    // No rescale has happened yet in this stream (wave-uniform): the first
+    // one moves the maximum from -inf and has nothing accumulated to scale.
+    bool virgin = true;
 
     auto process = [&](const PairRegs<D>& r, uint32_t gp, bool masked) {
         f4_t c1 = bias4, c2 = bias4;
@@ -718,6 +721,19 @@ __device__ __forceinline__ void decode_item(const DecodeParams& p, const uint32_
 #pragma unroll
             for (int i = 0; i < 8; ++i) ymax = fmaxf(ymax, __builtin_amdgcn_exp2f(sc8[i] - mn) * vs[i]);
             ymax = col_max(ymax);
+            if (virgin) {
+                // The stream's first rescale: nothing is accumulated yet
+                // (acc, cr and lpart are zero), so there is no mass to keep
+                // and nothing to re-scale -- only the row's maximum and shift.
+                float shn = sh;
+                if (row_live && ymax > 0.0f)
+                    shn = fminf(fmaxf(-(float)exponent_of(ymax), -kShiftLimit), kShiftLimit);
+                m_used = mn;
+                mo = mn - shn;
+                sh = shn;
+                thr = kTau + shn;
+                virgin = false;
+            } else {
             // the row's mass so far (its offset-column sum, P.V layout row n)
             const int src = 16 * (n >> 2);
             const float r0 = __shfl(cr[0], src, 64), r1 = __shfl(cr[1], src, 64);
@@ -750,6 +766,7 @@ __device__ __forceinline__ void decode_item(const DecodeParams& p, const uint32_
             mo = mon;
             sh = shn;
             thr = kTau + shn;
+            }
         }
         _Float16 x[8];
         float psum = 0.0f;
