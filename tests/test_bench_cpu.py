@@ -1,5 +1,6 @@
-"""bench.py's host logic, on the CPU: the algorithmic byte counts against the
-figures BASELINE.md lists per config, the one-GPU refusal, and the PMC and
+"""bench.py's host logic, on the CPU: the algorithmic byte counts of each
+benchmarked configuration (1,088 cache bytes per token at d = 128 and 8 kv
+heads, plus tables, q and out), the one-GPU refusal, and the PMC and
 kernel-trace summaries on small synthetic rocprofv3 CSV files."""
 import csv
 import json
@@ -15,7 +16,8 @@ import bench  # noqa: E402
 
 
 def test_algorithmic_bytes_match_the_baseline_table():
-    # C1, C2, C3 and the C4 contexts
+    # the A8 strip, the 1024-token BF16 writer, and the decode at ctx 4096,
+    # 16384, 32768 and the ragged 4103
     assert bench.writer_algorithmic_bytes(16, 8, 128, 1) == 50_240
     assert bench.writer_algorithmic_bytes(1024, 8, 128, 2) == 5_312_512
     for ctx, want in ((4096, 4_473_860), (16384, 17_846_276), (32768, 35_676_164),
