@@ -309,6 +309,20 @@ def test_persistent_head_sizes_and_pages(tq4, oracle, d):
     check_out(got, want, f"persistent d {d}")
 
 
+@pytest.mark.parametrize("S", [48, 64, 128])
+@pytest.mark.parametrize("K", [1, 5, 0])
+def test_large_pages(tq4, oracle, S, K):
+    """Pages of 3, 4 and 8 strips: a split boundary falls inside a page's
+    strip run only in whole pages, ragged tails end mid-page (NaN canaries
+    in the dead slots); K = 0 takes the auto count."""
+    rng = np.random.default_rng(0x5E40 + S + K)
+    ctx = [1, S - 1, S, S + 1, 3 * S + 7, 2100]
+    P = sum((c + S - 1) // S for c in ctx) + 4
+    kk = K or tq4.auto_splits(len(ctx), 4, (max(ctx) + S - 1) // S, S)
+    got, want, _ = run_decode(tq4, oracle, rng, ctx, 16, 4, 128, S, P, kk)
+    check_out(got, want, f"S {S} K {kk}")
+
+
 @pytest.mark.parametrize("B", [1000, 1100])
 def test_persistent_large_batch(tq4, oracle, B):
     """Up to 1024 sequences the persistent kernel ranks the last splits by
