@@ -86,6 +86,18 @@ constexpr uint32_t kPersistentMaxSeqs = 4096; // the persistent kernel stages tw
 constexpr uint32_t kLptMaxSeqs = 1024;        // and a third (the last-split order) up to this many
 constexpr int kStripSlots = TQ4_MAX_SPLIT_STRIPS + 4;  // staged window rows + padding
 
+// The thread index through an empty asm statement: address arithmetic
+// derived from it is computed where it is used rather than once per kernel
+// and held in registers across the strip loop (the kernels run at 256
+// registers per wave, and a spilled address reloaded between items would
+// wait for every load in flight).
+__device__ __forceinline__ int fresh_tid()
+{
+    int t = threadIdx.x;
+    asm volatile("" : "+v"(t));
+    return t;
+}
+
 // Eight codes of one dword as fp16 (1 + u/64), u = nibble ^ 8; halves in
 // nibble order 0,4,1,5,2,6,3,7 (every operand built against this table uses
 // that order). Each pair is one v_bitop3: kNib ? (bits ^ kCodeBase) :
@@ -379,6 +391,481 @@ __host__ __device__ constexpr size_t region_floats(uint32_t G, uint32_t D)
     return 4ull * G * D;  // q staging [G][D], then the four waves' rows [4][G][D]
 }
 
+// One wave's streaming state over the q rows of one item. Scores t = s - mo
+// with s = score * log2(e) (log2 units), mo = m_used - sh: P' = exp2(t) =
+// P * 2^sh, and the MFMA operand is the product P' * vscale in fp16. The
+// row's shift sh is set at each rescale so that the largest product of that
+// pair lands in [1, 2): every product that matters for the row's sum then
+// fits fp16 (one below 2^-24 of the largest is below 2^-24 of the sum),
+// whatever the spread of the value scales; the accumulators are FP32.
+template <int D>
+struct RowState {
+    f4_t acc[D / 16];
+    f4_t cr;       // offset column: 1.125 * sum P'vs per row
+    float m_used;  // the row maximum in use (log2 units)
+    float sh, mo, lpart, thr;
+    bool virgin;   // no rescale yet in this stream (wave-uniform)
+
+    __device__ __forceinline__ void reset(bool row_live)
+    {
+#pragma unroll
+        for (int b = 0; b < D / 16; ++b) acc[b] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        cr = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        m_used = row_live ? -INFINITY : INFINITY;  // padded rows stay silent
+        sh = 0.0f;
+        mo = m_used;
+        lpart = 0.0f;
+        thr = kTau;
+        virgin = true;
+    }
+};
+
+// This lane's B operands (q head n, channels g4*d/4 ..) in the codes8
+// channel order, the MFMA start value that removes the code offset, and the
+// score factor 64 * log2(e) * 2^q_exp.
+template <int D>
+struct QOps {
+    h8_t qop[D / 32];
+    f4_t bias4;
+    float cf;
+    bool row_live;
+};
+
+// One pair (two strips, 32 tokens) of one wave into its rows. masked: the
+// pair holds dead tokens -- those at or past live_rel tokens from the pair's
+// start, and every token of this lane's value strip when strip_ok is false;
+// a dead token is overwritten (score -inf, value scale 0), never multiplied
+// (its payload may be NaN).
+template <int D>
+__device__ __forceinline__ void process_pair(RowState<D>& st, const QOps<D>& qo,
+                                             const PairRegs<D>& r, float* sc_wave, int lane,
+                                             bool masked, uint32_t live_rel, bool strip_ok)
+{
+    constexpr int NJ = D / 32;
+    constexpr int NB = D / 16;
+    const int half = (lane >> 4) & 1, sp = lane >> 5;
+    const _Float16 off16 = (_Float16)kCodeOffset;
+    const h8_t offset_col = h8_t{off16, off16, off16, off16, off16, off16, off16, off16};
+    f4_t c1 = qo.bias4, c2 = qo.bias4;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+        c1 = mfma32(codes8(r.k1[j]), qo.qop[j], c1);
+        c2 = mfma32(codes8(r.k2[j]), qo.qop[j], c2);
+    }
+    // scales through the wave's LDS slot: key scales of this lane's 8
+    // tokens (strip sp, tokens 8*half..) at [32sp + 8half], values at +16
+    sc_wave[lane] = r.sc;
+    const f4_t ks1 = *(const f4_t*)(sc_wave + 32 * sp + 8 * half);
+    const f4_t ks2 = *(const f4_t*)(sc_wave + 32 * sp + 8 * half + 4);
+    const f4_t vs1 = *(const f4_t*)(sc_wave + 32 * sp + 16 + 8 * half);
+    const f4_t vs2 = *(const f4_t*)(sc_wave + 32 * sp + 16 + 8 * half + 4);
+    bool live[8];
+    if (masked) {
+        // token of value i from the pair's start: strip sp, 8*half + (i&3) + 4*(i>>2)
+        const uint32_t tb = 16 * sp + 8 * half;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) live[i] = strip_ok && tb + (i & 3) + 4 * (i >> 2) < live_rel;
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) live[i] = true;
+    }
+    // scores (log2 units) and value scales; a dead token is overwritten
+    float sc8[8], vs[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        sc8[i] = live[i] ? c1[i] * (qo.cf * ks1[i]) : -INFINITY;
+        sc8[4 + i] = live[4 + i] ? c2[i] * (qo.cf * ks2[i]) : -INFINITY;
+        vs[i] = live[i] ? vs1[i] : 0.0f;
+        vs[4 + i] = live[4 + i] ? vs2[i] : 0.0f;
+    }
+    // Rescale when a score passes the lazy maximum by kTau, or when a
+    // product could reach kXLimit: exp2(tmax) * vmax bounds every
+    // product (one exp per lane; the products themselves are formed
+    // after the branch, so nothing of them stays live across it).
+    float tmax = -INFINITY, vmax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        tmax = fmaxf(tmax, sc8[i] - st.mo);
+        vmax = fmaxf(vmax, vs[i]);
+    }
+    if (__builtin_expect(
+            __any(tmax > st.thr || __builtin_amdgcn_exp2f(tmax) * vmax >= kXLimit), 0)) {
+        // Move the row maximum and re-normalise the row's products.
+        float smax = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) smax = fmaxf(smax, sc8[i]);
+        smax = col_max(smax);
+        const float mn = qo.row_live ? fmaxf(st.m_used, smax) : st.m_used;
+        // the pair's largest product under the new maximum, unnormalised
+        float ymax = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) ymax = fmaxf(ymax, __builtin_amdgcn_exp2f(sc8[i] - mn) * vs[i]);
+        ymax = col_max(ymax);
+        if (st.virgin) {
+            // The stream's first rescale: nothing is accumulated yet
+            // (acc, cr and lpart are zero), so there is no mass to keep
+            // and nothing to re-scale -- only the row's maximum and shift.
+            float shn = st.sh;
+            if (qo.row_live && ymax > 0.0f)
+                shn = fminf(fmaxf(-(float)exponent_of(ymax), -kShiftLimit), kShiftLimit);
+            st.m_used = mn;
+            st.mo = mn - shn;
+            st.sh = shn;
+            st.thr = kTau + shn;
+            st.virgin = false;
+        } else {
+            // (lane indices of this rare path are taken afresh: held across
+            // the strip loop they would cost registers every pair)
+            const int ln = fresh_tid() & 63;
+            const int n = ln & 15, g4 = ln >> 4;
+            // the row's mass so far (its offset-column sum, P.V layout row n)
+            const int src = 16 * (n >> 2);
+            const float r0 = __shfl(st.cr[0], src, 64), r1 = __shfl(st.cr[1], src, 64);
+            const float r2 = __shfl(st.cr[2], src, 64), r3 = __shfl(st.cr[3], src, 64);
+            const int k3 = n & 3;
+            const float crow = k3 == 0 ? r0 : k3 == 1 ? r1 : k3 == 2 ? r2 : r3;
+            float shn = st.sh;
+            if (qo.row_live && ymax > 0.0f) {
+                shn = fminf(fmaxf(-(float)exponent_of(ymax), -kShiftLimit), kShiftLimit);
+                // keep the old mass, moved to the new units, inside FP32
+                if (st.m_used != -INFINITY && crow > 0.0f) {
+                    const float lm = (float)exponent_of(crow) + (shn - st.sh) + (st.m_used - mn);
+                    if (lm > (float)kMassLimit) shn -= ceilf(lm - (float)kMassLimit);
+                }
+            }
+            const float mon = mn - shn;
+            float f = 1.0f;
+            if (qo.row_live) f = st.mo == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(st.mo - mon);
+            st.lpart *= f;
+            float fr[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) fr[i] = __shfl(f, 4 * g4 + i, 64);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+#pragma unroll
+                for (int b = 0; b < NB; ++b) st.acc[b][i] *= fr[i];
+                st.cr[i] *= fr[i];
+            }
+            st.m_used = mn;
+            st.mo = mon;
+            st.sh = shn;
+            st.thr = kTau + shn;
+        }
+    }
+    _Float16 x[8];
+    float psum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        // a dead token is 0 even while the row has no maximum yet
+        // (-inf - -inf would be NaN)
+        const float pr = sc8[i] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(sc8[i] - st.mo);
+        psum += pr;
+        x[i] = (_Float16)(pr * vs[i]);
+    }
+    st.lpart += psum;
+    // A operand in the codes8 token order: (T1[0], T2[0], T1[1], T2[1], ...)
+    const h8_t P = h8_t{x[0], x[4], x[1], x[5], x[2], x[6], x[3], x[7]};
+    // B operands: block b = 4q + 2hb + e is channel n*d/16 + b. The lane
+    // pair (half 0, half 1) swaps so each holds its own 8-token half:
+    // permlane16_swap(x, y) leaves the even row's x plus the odd row's
+    // copy of the even row's y in its first result (block hb = 0), and
+    // the odd row's x copy plus the odd row's y in its second (hb = 1).
+#pragma unroll
+    for (int q = 0; q < NB / 4; ++q) {
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const auto sw = __builtin_amdgcn_permlane16_swap(r.v[4 * q + 2 * e],
+                                                             r.v[4 * q + 2 * e + 1], false, false);
+            st.acc[4 * q + e] = mfma32(P, codes8(sw[0]), st.acc[4 * q + e]);
+            st.acc[4 * q + 2 + e] = mfma32(P, codes8(sw[1]), st.acc[4 * q + 2 + e]);
+        }
+    }
+    st.cr = mfma32(P, offset_col, st.cr);
+}
+
+// Rotate this wave's q rows (g = wave, wave + 4, ...; lane owns channels
+// lane*CPL ..), fold inv_sqrt_len and the softmax scale, normalise each row
+// by a power of two and stage it in q_st [G][D] (exponent in q_exp[g]).
+template <int D>
+__device__ __forceinline__ void stage_q_rows(const DecodeParams& p,
+                                             const uint16_t (&qraw)[4][D / 64],
+                                             const float (&sg)[D / 64], bool rotate, float* q_st,
+                                             int* q_exp, int wave, int lane)
+{
+    constexpr int CPL = D / 64;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t g = wave + kWaves * i;
+        if (g >= p.G) continue;
+        float v[CPL];
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) v[j] = bf16_to_f32(qraw[i][j]);
+        if (rotate) {
+            rotate_ingress<D, CPL>(v, sg, lane);
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) v[j] = (v[j] * p.inv_sqrt_len) * p.scale;
+        } else {
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) v[j] = v[j] * p.scale;
+        }
+        float a = 0.0f;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) a = fmaxf(a, fabsf(v[j]));
+        a = wave_max(a);
+        const int kq = a > 0.0f ? exponent_of(a) : 0;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) q_st[g * D + lane * CPL + j] = ldexpf(v[j], -kq);
+        if (lane == 0) q_exp[g] = kq;
+    }
+}
+
+// This lane's operands from the staged rows (after a barrier).
+template <int D>
+__device__ __forceinline__ void build_qops(QOps<D>& qo, const float* q_st, const int* q_exp,
+                                           uint32_t G, int lane)
+{
+    constexpr int NJ = D / 32;
+    const int n = lane & 15, g4 = lane >> 4;
+    qo.row_live = (uint32_t)n < G;
+    float bias = 0.0f;
+    qo.cf = 0.0f;
+    if (qo.row_live) {
+        const float* qrow = q_st + n * D + g4 * (D / 4);
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+            const float4 lo = *(const float4*)(qrow + 8 * j);
+            const float4 hi = *(const float4*)(qrow + 8 * j + 4);
+            const h8_t h = h8_t{(_Float16)lo.x, (_Float16)hi.x, (_Float16)lo.y, (_Float16)hi.y,
+                                (_Float16)lo.z, (_Float16)hi.z, (_Float16)lo.w, (_Float16)hi.w};
+            qo.qop[j] = h;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) bias += (float)h[e];
+        }
+        qo.cf = ldexpf(kCodeUnit * kLog2e, q_exp[n]);
+    } else {
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) qo.qop[j] = h8_t{0, 0, 0, 0, 0, 0, 0, 0};
+    }
+    bias = col_sum(bias) * -kCodeOffset;
+    qo.bias4 = f4_t{bias, bias, bias, bias};
+}
+
+// Park one wave's rows for the merge: (m, l, 2^-sh) per row at [row][wave]
+// (one 16-byte read gives a row's four waves) and the raw rows (offset
+// column removed) at part [wave][G][D].
+template <int D>
+__device__ __forceinline__ void park_rows(const RowState<D>& st, bool row_live, float* m_x,
+                                          float* l_x, float* u_x, float* part, uint32_t G,
+                                          int wave, int lane)
+{
+    constexpr int NB = D / 16;
+    const int n = lane & 15, g4 = lane >> 4;
+    const float lsum = col_sum(st.lpart);
+    if (g4 == 0) {
+        m_x[n * kWaves + wave] = row_live ? st.m_used : -INFINITY;
+        l_x[n * kWaves + wave] = lsum;
+        u_x[n * kWaves + wave] = ldexpf(1.0f, -(int)st.sh);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t r = 4 * g4 + i;
+        if (r < G) {
+            float* dst = part + ((size_t)wave * G + r) * D + n * NB;  // channel n*d/16 + b
+#pragma unroll
+            for (int b = 0; b < NB; ++b) dst[b] = st.acc[b][i] - st.cr[i];
+        }
+    }
+}
+
+// The end of one work item: merge the four waves' rows, then MODE 0 exports
+// the partial record; MODE 1 takes the split's place in the fused combine
+// (export, or finalise from LDS when it is the only live split, or combine as
+// the last ticket). region: the item's q staging / merge region.
+template <int D, int MODE, bool OWN>
+__device__ __forceinline__ void finish_item(const DecodeParams& p, uint32_t seq, uint32_t kvh,
+                                            uint32_t split, uint32_t k_live, uint32_t ticket,
+                                            const RowState<D>& st, bool row_live, float* region)
+{
+    constexpr int RS = D + 4;  // record stride in floats
+    extern __shared__ float smem[];
+    const uint32_t G = p.G;
+    float* m_x = smem;               // [16][4] (row, wave)
+    float* l_x = smem + 64;          // [16][4]
+    int* flag = (int*)(smem + 144);  // the combiner / withheld-record flags
+    float* u_x = smem + 416;         // [16][4] (row, wave) 2^-sh
+    const int tid = fresh_tid(), lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    // ---- merge the four waves. Each parks its raw rows (offset column
+    // removed) and (m, l, 2^-sh) in LDS; then every output float4 combines
+    // the four copies with the row's common maximum.
+    float* part = region;  // [kWaves][G][D]
+    park_rows<D>(st, row_live, m_x, l_x, u_x, part, G, wave, lane);
+    if constexpr (MODE == 1) {
+        if (p.K > 1 && tid == 0) {
+            // The last ticket combines; every live split of this (seq, kv
+            // head) took its ticket before it, so all of them are running.
+            // Bit 1: the test hook's withheld record (the first ticket's,
+            // never the combiner's when more than one split is live).
+            const int last = ticket == k_live - 1;
+            if (last)
+                __hip_atomic_store(p.counters + ((size_t)seq * p.Hkv + kvh) * kTicketStride, 0u,
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            *flag = last | (p.withhold && ticket == 0 && !last ? 2 : 0);
+        }
+    }
+    lds_barrier();
+    // Per-wave weights of row r (exp2(m_w - M) * 2^-sh_w), the row's M and L;
+    // branch-free: a wave with no live token gets exp2(-inf) = 0.
+    auto row_weights = [&](uint32_t r, float (&f)[kWaves], float& M, float& L) {
+        const float4 m4 = *(const float4*)(m_x + r * kWaves);
+        const float4 l4 = *(const float4*)(l_x + r * kWaves);
+        const float4 u4 = *(const float4*)(u_x + r * kWaves);
+        const float mw[kWaves] = {m4.x, m4.y, m4.z, m4.w};
+        const float lw[kWaves] = {l4.x, l4.y, l4.z, l4.w};
+        const float uw[kWaves] = {u4.x, u4.y, u4.z, u4.w};
+        M = fmaxf(fmaxf(mw[0], mw[1]), fmaxf(mw[2], mw[3]));
+        L = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+            const float d = (mw[w] == -INFINITY) ? -INFINITY : mw[w] - M;
+            f[w] = __builtin_amdgcn_exp2f(d) * uw[w];
+            L += lw[w] * f[w];
+        }
+    };
+    const uint32_t outs4 = G * D / 4;  // float4 outputs
+    auto combined4 = [&](uint32_t e4, const float (&f)[kWaves]) {
+        float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+            const float4 x = *(const float4*)(part + (size_t)w * G * D + 4 * e4);
+            const float fw = f[w] * kCodeUnit;
+            v.x += x.x * fw;
+            v.y += x.y * fw;
+            v.z += x.z * fw;
+            v.w += x.w * fw;
+        }
+        return v;
+    };
+
+    constexpr int CC = D / 32;
+    if constexpr (MODE == 0) {
+        // ---- export one record per q head: [m (natural log), l, 0, 0, acc].
+        const __amdgpu_buffer_rsrc_t rsrc = records_rsrc(
+            p.records + (((size_t)seq * p.Hq + (size_t)kvh * G) * p.K + split) * RS);
+        const uint32_t row_bytes = p.K * RS * 4u;
+        for (uint32_t e4 = tid; e4 < outs4; e4 += kThreads) {
+            const uint32_t r = 4 * e4 / D, ch = 4 * e4 % D;
+            float f[kWaves], M, L;
+            row_weights(r, f, M, L);
+            const float4 v = combined4(e4, f);
+            const float vv[4] = {v.x, v.y, v.z, v.w};
+            rec_store<4, false>(rsrc, r * row_bytes + (4 + ch) * 4u, vv);
+            if (ch == 0) {
+                const float h[4] = {M == -INFINITY ? kMasked : M * kLn2, L, 0.0f, 0.0f};
+                rec_store<4, false>(rsrc, r * row_bytes, h);
+            }
+        }
+        return;
+    } else {
+        // One live split (K == 1, or a sequence shorter than one split's
+        // window) finalises from LDS; otherwise every split exports and the
+        // last ticket combines.
+        const bool local = p.K == 1 || k_live == 1;
+        const int fl = *flag;
+        const bool combiner = local || (fl & 1);
+        float es[CC];
+        if (!local && (fl & 2)) return;  // test hook: this record is never written
+        if (!local && (!combiner || !OWN)) {
+            // ---- export this split's encoded record.
+            const __amdgpu_buffer_rsrc_t rsrc = records_rsrc(
+                p.records + (((size_t)seq * p.Hq + (size_t)kvh * G) * p.K + split) * RS);
+            const uint32_t row_bytes = p.K * RS * 4u;
+            for (uint32_t e4 = tid; e4 < outs4; e4 += kThreads) {
+                const uint32_t r = 4 * e4 / D, ch = 4 * e4 % D;
+                float f[kWaves], M, L;
+                row_weights(r, f, M, L);
+                const float4 v = combined4(e4, f);
+                const float vv[4] = {v.x, v.y, v.z, v.w};
+                rec_store<4, true>(rsrc, r * row_bytes + (4 + ch) * 4u, vv);
+                if (ch == 0) {
+                    const float h[4] = {M == -INFINITY ? kMasked : M * kLn2, L, 0.0f, 0.0f};
+                    rec_store<4, true>(rsrc, r * row_bytes, h);
+                }
+            }
+            if (!combiner) return;
+        }
+        if (!local) {
+            // ---- the combiner: poll the records of its rows and combine
+            // them. With OWN its own record is never stored: its words are
+            // made from LDS (the export's arithmetic, in the combine layout)
+            // while the first poll is in flight. The sign and gate loads
+            // ride with that poll.
+            if (p.output_stage >= 1) load_lane_floats<D>(p.pi_signs, lane, es);
+            for (uint32_t g = wave; g < G; g += kWaves) {
+                const size_t qh = (size_t)seq * p.Hq + kvh * G + g;
+                float gt[CC];
+                if (p.output_stage == 2) load_lane_floats<D>(p.gate + qh * D, lane, gt);
+                auto own = [&](uint32_t (&h)[2], uint32_t (&a)[CC]) {
+                    float f[kWaves], M, L;
+                    row_weights(g, f, M, L);
+                    h[0] = __float_as_uint(M == -INFINITY ? kMasked : M * kLn2) ^ kRecMagic;
+                    h[1] = __float_as_uint(L) ^ kRecMagic;
+                    if constexpr (CC >= 4) {
+#pragma unroll
+                        for (int j = 0; j < CC; j += 4) {
+                            const float4 v = combined4((g * D + (lane & 31) * CC + j) / 4, f);
+                            a[j] = __float_as_uint(v.x) ^ kRecMagic;
+                            a[j + 1] = __float_as_uint(v.y) ^ kRecMagic;
+                            a[j + 2] = __float_as_uint(v.z) ^ kRecMagic;
+                            a[j + 3] = __float_as_uint(v.w) ^ kRecMagic;
+                        }
+                    } else {  // d = 64: the lane's two channels of a float4
+                        const uint32_t ch = (lane & 31) * CC;
+                        const float4 v = combined4((g * D + ch) / 4, f);
+                        const bool hi = (ch & 2) != 0;
+                        a[0] = __float_as_uint(hi ? v.z : v.x) ^ kRecMagic;
+                        a[1] = __float_as_uint(hi ? v.w : v.y) ^ kRecMagic;
+                    }
+                };
+                auto none = [](uint32_t(&)[2], uint32_t(&)[CC]) {};
+                float v[CC];
+                // 16 splits per chunk: wider chunks (32 per round trip)
+                // measured slower at every split count from 17 to 64
+                if constexpr (OWN)
+                    combine_records<D, true, 8>(p.records + qh * p.K * RS, k_live, lane, v,
+                                                split, own, p.poll_limit, p.timeouts);
+                else
+                    combine_records<D, true, 8>(p.records + qh * p.K * RS, k_live, lane, v, ~0u,
+                                                none, p.poll_limit, p.timeouts);
+                egress_row<D>(v, es, gt, p.out + qh * D, p.inv_sqrt_len, p.output_stage, lane);
+            }
+            return;
+        }
+        if (p.output_stage >= 1) load_lane_floats<D>(p.pi_signs, lane, es);
+        // ---- one live split: normalise into the wave-0 slice (each thread
+        // reads and writes only its own float4), then the egress.
+        for (uint32_t e4 = tid; e4 < outs4; e4 += kThreads) {
+            float f[kWaves], M, L;
+            row_weights(4 * e4 / D, f, M, L);
+            float4 v = combined4(e4, f);
+            const float inv = L == 0.0f ? 0.0f : 1.0f / L;
+            v = L == 0.0f ? make_float4(0.0f, 0.0f, 0.0f, 0.0f)
+                          : make_float4(v.x * inv, v.y * inv, v.z * inv, v.w * inv);
+            *(float4*)(part + 4 * e4) = v;
+        }
+        lds_barrier();
+        for (uint32_t g = wave; g < G; g += kWaves) {
+            const size_t qh = (size_t)seq * p.Hq + kvh * G + g;
+            float gt[CC];
+            if (p.output_stage == 2) load_lane_floats<D>(p.gate + qh * D, lane, gt);
+            float v[CC];
+#pragma unroll
+            for (int j = 0; j < CC; ++j) v[j] = part[g * D + (lane & 31) * CC + j];
+            egress_row<D>(v, es, gt, p.out + qh * D, p.inv_sqrt_len, p.output_stage, lane);
+        }
+    }
+}
+
 // One (seq, kv head, split) work item: MODE 0 exports the partial record,
 // MODE 1 is the fused path (ticket, export or local finish, combine).
 // OWN (MODE 1): the combining split keeps its own record in registers instead
@@ -394,18 +881,12 @@ __device__ __forceinline__ void decode_item(const DecodeParams& p, const uint32_
                                             Hook&& after_issue = Hook())
 {
     constexpr int CPL = D / 64;   // channels per lane in the row layout
-    constexpr int NJ = D / 32;    // score MFMAs per token set (one per key dword)
     constexpr int NB = D / 16;    // P.V MFMAs (16-channel blocks)
-    constexpr int RS = D + 4;     // record stride in floats
     constexpr int NBUF = D >= 256 ? 2 : 3;
     extern __shared__ float smem[];
 
     const uint32_t G = p.G, S = p.S;
-    float* m_x = smem;                       // [16][4] (row, wave)
-    float* l_x = smem + 64;                  // [16][4]
     int* q_exp = (int*)(smem + 128);         // [16]
-    int* flag = (int*)(smem + 144);
-    float* u_x = smem + 416;                 // [16][4] (row, wave) 2^-sh
     int* bad_w = (int*)(smem + 152);         // [4] per-wave invalid-page flags
     float* sc_wave = smem + 160 + 64 * (threadIdx.x >> 6);  // [4][64] per-wave scale slot
     uint32_t* strip_lds = (uint32_t*)(smem + kHdrFloats);  // [TQ4 max split strips + padding]
@@ -584,220 +1065,22 @@ __device__ __forceinline__ void decode_item(const DecodeParams& p, const uint32_
     after_issue();
 
     // ---- phase 1: rotate q (Pi = M * inv_sqrt_len), fold the softmax scale,
-    // normalise each row by a power of two, stage in LDS.
+    // normalise each row by a power of two, stage in LDS; then every lane
+    // builds its operands.
     float* q_st = region;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const uint32_t g = wave + kWaves * i;
-        if (g >= G) continue;
-        float v[CPL];
-#pragma unroll
-        for (int j = 0; j < CPL; ++j) v[j] = bf16_to_f32(qraw[i][j]);
-        if (rotate) {
-            rotate_ingress<D, CPL>(v, sg, lane);
-#pragma unroll
-            for (int j = 0; j < CPL; ++j) v[j] = (v[j] * p.inv_sqrt_len) * p.scale;
-        } else {
-#pragma unroll
-            for (int j = 0; j < CPL; ++j) v[j] = v[j] * p.scale;
-        }
-        float a = 0.0f;
-#pragma unroll
-        for (int j = 0; j < CPL; ++j) a = fmaxf(a, fabsf(v[j]));
-        a = wave_max(a);
-        const int kq = a > 0.0f ? exponent_of(a) : 0;
-#pragma unroll
-        for (int j = 0; j < CPL; ++j) q_st[g * D + lane * CPL + j] = ldexpf(v[j], -kq);
-        if (lane == 0) q_exp[g] = kq;
-    }
+    stage_q_rows<D>(p, qraw, sg, rotate, q_st, q_exp, wave, lane);
     lds_barrier();
-
-    // ---- this lane's B operands (q head n, channels g4*d/4 ..) in the
-    // codes8 channel order, and the per-row constants.
-    const bool row_live = (uint32_t)n < G;
-    h8_t qop[NJ];
-    float bias = 0.0f, cf = 0.0f;
-    if (row_live) {
-        const float* qrow = q_st + n * D + g4 * (D / 4);
-#pragma unroll
-        for (int j = 0; j < NJ; ++j) {
-            const float4 lo = *(const float4*)(qrow + 8 * j);
-            const float4 hi = *(const float4*)(qrow + 8 * j + 4);
-            const h8_t h = h8_t{(_Float16)lo.x, (_Float16)hi.x, (_Float16)lo.y, (_Float16)hi.y,
-                                (_Float16)lo.z, (_Float16)hi.z, (_Float16)lo.w, (_Float16)hi.w};
-            qop[j] = h;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) bias += (float)h[e];
-        }
-        cf = ldexpf(kCodeUnit * kLog2e, q_exp[n]);
-    } else {
-#pragma unroll
-        for (int j = 0; j < NJ; ++j) qop[j] = h8_t{0, 0, 0, 0, 0, 0, 0, 0};
-    }
-    bias = col_sum(bias) * -kCodeOffset;
-    const f4_t bias4 = f4_t{bias, bias, bias, bias};
-    const _Float16 off16 = (_Float16)kCodeOffset;
-    const h8_t offset_col = h8_t{off16, off16, off16, off16, off16, off16, off16, off16};
+    QOps<D> qo;
+    build_qops<D>(qo, q_st, q_exp, G, lane);
     // q_st is next overwritten after the first merge barrier, which every
     // wave reaches only after building its operands.
-
-    // ---- streaming state, per q row. Scores t = s - mo with s = score *
-    // log2(e) (log2 units), mo = m_used - sh: P' = exp2(t) = P * 2^sh, and
-    // the MFMA operand is the product P' * vscale in fp16. The row's shift
-    // sh is set at each rescale so that the largest product of that pair
-    // lands in [1, 2): every product that matters for the row's sum then
-    // fits fp16 (one below 2^-24 of the largest is below 2^-24 of the sum),
-    // whatever the spread of the value scales; the accumulators are FP32.
-    f4_t acc[NB];
-#pragma unroll
-    for (int b = 0; b < NB; ++b) acc[b] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
-    f4_t cr = f4_t{0.0f, 0.0f, 0.0f, 0.0f};  // offset column: 1.125 * sum P'vs per row
-    float m_used = row_live ? -INFINITY : INFINITY;  // padded rows stay silent
-    float sh = 0.0f;
-    float mo = m_used;
-    float lpart = 0.0f;
-    float thr = kTau + sh;
-    // No rescale has happened yet in this stream (wave-uniform): the first
-    // one moves the maximum from -inf and has nothing accumulated to scale.
-    bool virgin = true;
+    RowState<D> st;
+    st.reset(qo.row_live);
 
     auto process = [&](const PairRegs<D>& r, uint32_t gp, bool masked) {
-        f4_t c1 = bias4, c2 = bias4;
-#pragma unroll
-        for (int j = 0; j < NJ; ++j) {
-            c1 = mfma32(codes8(r.k1[j]), qop[j], c1);
-            c2 = mfma32(codes8(r.k2[j]), qop[j], c2);
-        }
-        // scales through the wave's LDS slot: key scales of this lane's 8
-        // tokens (strip sp, tokens 8*half..) at [32sp + 8half], values at +16
-        sc_wave[lane] = r.sc;
-        const f4_t ks1 = *(const f4_t*)(sc_wave + 32 * sp + 8 * half);
-        const f4_t ks2 = *(const f4_t*)(sc_wave + 32 * sp + 8 * half + 4);
-        const f4_t vs1 = *(const f4_t*)(sc_wave + 32 * sp + 16 + 8 * half);
-        const f4_t vs2 = *(const f4_t*)(sc_wave + 32 * sp + 16 + 8 * half + 4);
-        bool live[8];
-        if (masked) {
-            // window token of value i: pair base + strip sp + 8*half + (i&3) + 4*(i>>2)
-            const uint32_t tb = 32 * gp + 16 * sp + 8 * half;
-            const uint32_t sv = min(2 * gp + sp, nws - 1);
-            const bool page_ok = strip_lds[sv] != kBadStrip;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) live[i] = page_ok && tb + (i & 3) + 4 * (i >> 2) < ltok;
-        } else {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) live[i] = true;
-        }
-        // scores (log2 units) and value scales; a dead token is overwritten
-        // -- score -inf, value scale 0 -- never multiplied (its payload may
-        // be NaN)
-        float sc8[8], vs[8];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            sc8[i] = live[i] ? c1[i] * (cf * ks1[i]) : -INFINITY;
-            sc8[4 + i] = live[4 + i] ? c2[i] * (cf * ks2[i]) : -INFINITY;
-            vs[i] = live[i] ? vs1[i] : 0.0f;
-            vs[4 + i] = live[4 + i] ? vs2[i] : 0.0f;
-        }
-        // Rescale when a score passes the lazy maximum by kTau, or when a
-        // product could reach kXLimit: exp2(tmax) * vmax bounds every
-        // product (one exp per lane; the products themselves are formed
-        // after the branch, so nothing of them stays live across it).
-        float tmax = -INFINITY, vmax = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            tmax = fmaxf(tmax, sc8[i] - mo);
-            vmax = fmaxf(vmax, vs[i]);
-        }
-        if (__builtin_expect(
-                __any(tmax > thr || __builtin_amdgcn_exp2f(tmax) * vmax >= kXLimit), 0)) {
-            // Move the row maximum and re-normalise the row's products.
-            float smax = -INFINITY;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) smax = fmaxf(smax, sc8[i]);
-            smax = col_max(smax);
-            const float mn = row_live ? fmaxf(m_used, smax) : m_used;
-            // the pair's largest product under the new maximum, unnormalised
-            float ymax = 0.0f;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) ymax = fmaxf(ymax, __builtin_amdgcn_exp2f(sc8[i] - mn) * vs[i]);
-            ymax = col_max(ymax);
-            if (virgin) {
-                // The stream's first rescale: nothing is accumulated yet
-                // (acc, cr and lpart are zero), so there is no mass to keep
-                // and nothing to re-scale -- only the row's maximum and shift.
-                float shn = sh;
-                if (row_live && ymax > 0.0f)
-                    shn = fminf(fmaxf(-(float)exponent_of(ymax), -kShiftLimit), kShiftLimit);
-                m_used = mn;
-                mo = mn - shn;
-                sh = shn;
-                thr = kTau + shn;
-                virgin = false;
-            } else {
-            // the row's mass so far (its offset-column sum, P.V layout row n)
-            const int src = 16 * (n >> 2);
-            const float r0 = __shfl(cr[0], src, 64), r1 = __shfl(cr[1], src, 64);
-            const float r2 = __shfl(cr[2], src, 64), r3 = __shfl(cr[3], src, 64);
-            const int k3 = n & 3;
-            const float crow = k3 == 0 ? r0 : k3 == 1 ? r1 : k3 == 2 ? r2 : r3;
-            float shn = sh;
-            if (row_live && ymax > 0.0f) {
-                shn = fminf(fmaxf(-(float)exponent_of(ymax), -kShiftLimit), kShiftLimit);
-                // keep the old mass, moved to the new units, inside FP32
-                if (m_used != -INFINITY && crow > 0.0f) {
-                    const float lm = (float)exponent_of(crow) + (shn - sh) + (m_used - mn);
-                    if (lm > (float)kMassLimit) shn -= ceilf(lm - (float)kMassLimit);
-                }
-            }
-            const float mon = mn - shn;
-            float f = 1.0f;
-            if (row_live) f = mo == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mo - mon);
-            lpart *= f;
-            float fr[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) fr[i] = __shfl(f, 4 * g4 + i, 64);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-#pragma unroll
-                for (int b = 0; b < NB; ++b) acc[b][i] *= fr[i];
-                cr[i] *= fr[i];
-            }
-            m_used = mn;
-            mo = mon;
-            sh = shn;
-            thr = kTau + shn;
-            }
-        }
-        _Float16 x[8];
-        float psum = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            // a dead token is 0 even while the row has no maximum yet
-            // (-inf - -inf would be NaN)
-            const float pr = sc8[i] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(sc8[i] - mo);
-            psum += pr;
-            x[i] = (_Float16)(pr * vs[i]);
-        }
-        lpart += psum;
-        // A operand in the codes8 token order: (T1[0], T2[0], T1[1], T2[1], ...)
-        const h8_t P = h8_t{x[0], x[4], x[1], x[5], x[2], x[6], x[3], x[7]};
-        // B operands: block b = 4q + 2hb + e is channel n*d/16 + b. The lane
-        // pair (half 0, half 1) swaps so each holds its own 8-token half:
-        // permlane16_swap(x, y) leaves the even row's x plus the odd row's
-        // copy of the even row's y in its first result (block hb = 0), and
-        // the odd row's x copy plus the odd row's y in its second (hb = 1).
-#pragma unroll
-        for (int q = 0; q < NB / 4; ++q) {
-#pragma unroll
-            for (int e = 0; e < 2; ++e) {
-                const auto sw = __builtin_amdgcn_permlane16_swap(r.v[4 * q + 2 * e],
-                                                                 r.v[4 * q + 2 * e + 1], false,
-                                                                 false);
-                acc[4 * q + e] = mfma32(P, codes8(sw[0]), acc[4 * q + e]);
-                acc[4 * q + 2 + e] = mfma32(P, codes8(sw[1]), acc[4 * q + 2 + e]);
-            }
-        }
-        cr = mfma32(P, offset_col, cr);
+        bool ok = true;
+        if (masked) ok = strip_lds[min(2 * gp + sp, nws - 1)] != kBadStrip;
+        process_pair<D>(st, qo, r, sc_wave, lane, masked, ltok - 32 * gp, ok);
     };
 
     // ---- the three-deep (two-deep at d = 256) register ring: full pairs,
@@ -855,189 +1138,7 @@ __device__ __forceinline__ void decode_item(const DecodeParams& p, const uint32_
         }
     }
 
-    // ---- merge the four waves. Each parks its raw rows (offset column
-    // removed) and (m, l, 2^-sh) in LDS; then every output float4 combines
-    // the four copies with the row's common maximum.
-    const float lsum = col_sum(lpart);
-    if (g4 == 0) {  // [row][wave]: one 16-byte read gives a row's four waves
-        m_x[n * kWaves + wave] = row_live ? m_used : -INFINITY;
-        l_x[n * kWaves + wave] = lsum;
-    }
-    if (g4 == 0) u_x[n * kWaves + wave] = ldexpf(1.0f, -(int)sh);
-    if constexpr (MODE == 1) {
-        if (p.K > 1 && tid == 0) {
-            // The last ticket combines; every live split of this (seq, kv
-            // head) took its ticket before it, so all of them are running.
-            // Bit 1: the test hook's withheld record (the first ticket's,
-            // never the combiner's when more than one split is live).
-            const int last = ticket == k_live - 1;
-            if (last)
-                __hip_atomic_store(p.counters + ((size_t)seq * p.Hkv + kvh) * kTicketStride, 0u,
-                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            *flag = last | (p.withhold && ticket == 0 && !last ? 2 : 0);
-        }
-    }
-    float* part = region;  // [kWaves][G][D]
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const uint32_t r = 4 * g4 + i;
-        if (r < G) {
-            float* dst = part + ((size_t)wave * G + r) * D + n * NB;  // channel n*d/16 + b
-#pragma unroll
-            for (int b = 0; b < NB; ++b) dst[b] = acc[b][i] - cr[i];
-        }
-    }
-    lds_barrier();
-    // Per-wave weights of row r (exp2(m_w - M) * 2^-sh_w), the row's M and L;
-    // branch-free: a wave with no live token gets exp2(-inf) = 0.
-    auto row_weights = [&](uint32_t r, float (&f)[kWaves], float& M, float& L) {
-        const float4 m4 = *(const float4*)(m_x + r * kWaves);
-        const float4 l4 = *(const float4*)(l_x + r * kWaves);
-        const float4 u4 = *(const float4*)(u_x + r * kWaves);
-        const float mw[kWaves] = {m4.x, m4.y, m4.z, m4.w};
-        const float lw[kWaves] = {l4.x, l4.y, l4.z, l4.w};
-        const float uw[kWaves] = {u4.x, u4.y, u4.z, u4.w};
-        M = fmaxf(fmaxf(mw[0], mw[1]), fmaxf(mw[2], mw[3]));
-        L = 0.0f;
-#pragma unroll
-        for (int w = 0; w < kWaves; ++w) {
-            const float d = (mw[w] == -INFINITY) ? -INFINITY : mw[w] - M;
-            f[w] = __builtin_amdgcn_exp2f(d) * uw[w];
-            L += lw[w] * f[w];
-        }
-    };
-    const uint32_t outs4 = G * D / 4;  // float4 outputs
-    auto combined4 = [&](uint32_t e4, const float (&f)[kWaves]) {
-        float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-#pragma unroll
-        for (int w = 0; w < kWaves; ++w) {
-            const float4 x = *(const float4*)(part + (size_t)w * G * D + 4 * e4);
-            const float fw = f[w] * kCodeUnit;
-            v.x += x.x * fw;
-            v.y += x.y * fw;
-            v.z += x.z * fw;
-            v.w += x.w * fw;
-        }
-        return v;
-    };
-
-    constexpr int CC = D / 32;
-    if constexpr (MODE == 0) {
-        // ---- export one record per q head: [m (natural log), l, 0, 0, acc].
-        const __amdgpu_buffer_rsrc_t rsrc = records_rsrc(
-            p.records + (((size_t)seq * p.Hq + (size_t)kvh * G) * p.K + split) * RS);
-        const uint32_t row_bytes = p.K * RS * 4u;
-        for (uint32_t e4 = tid; e4 < outs4; e4 += kThreads) {
-            const uint32_t r = 4 * e4 / D, ch = 4 * e4 % D;
-            float f[kWaves], M, L;
-            row_weights(r, f, M, L);
-            const float4 v = combined4(e4, f);
-            const float vv[4] = {v.x, v.y, v.z, v.w};
-            rec_store<4, false>(rsrc, r * row_bytes + (4 + ch) * 4u, vv);
-            if (ch == 0) {
-                const float h[4] = {M == -INFINITY ? kMasked : M * kLn2, L, 0.0f, 0.0f};
-                rec_store<4, false>(rsrc, r * row_bytes, h);
-            }
-        }
-        return;
-    } else {
-        // One live split (K == 1, or a sequence shorter than one split's
-        // window) finalises from LDS; otherwise every split exports and the
-        // last ticket combines.
-        const bool local = p.K == 1 || k_live == 1;
-        const int fl = *flag;
-        const bool combiner = local || (fl & 1);
-        float es[CC];
-        if (!local && (fl & 2)) return;  // test hook: this record is never written
-        if (!local && (!combiner || !OWN)) {
-            // ---- export this split's encoded record.
-            const __amdgpu_buffer_rsrc_t rsrc = records_rsrc(
-                p.records + (((size_t)seq * p.Hq + (size_t)kvh * G) * p.K + split) * RS);
-            const uint32_t row_bytes = p.K * RS * 4u;
-            for (uint32_t e4 = tid; e4 < outs4; e4 += kThreads) {
-                const uint32_t r = 4 * e4 / D, ch = 4 * e4 % D;
-                float f[kWaves], M, L;
-                row_weights(r, f, M, L);
-                const float4 v = combined4(e4, f);
-                const float vv[4] = {v.x, v.y, v.z, v.w};
-                rec_store<4, true>(rsrc, r * row_bytes + (4 + ch) * 4u, vv);
-                if (ch == 0) {
-                    const float h[4] = {M == -INFINITY ? kMasked : M * kLn2, L, 0.0f, 0.0f};
-                    rec_store<4, true>(rsrc, r * row_bytes, h);
-                }
-            }
-            if (!combiner) return;
-        }
-        if (!local) {
-            // ---- the combiner: poll the records of its rows and combine
-            // them. With OWN its own record is never stored: its words are
-            // made from LDS (the export's arithmetic, in the combine layout)
-            // while the first poll is in flight. The sign and gate loads
-            // ride with that poll.
-            if (p.output_stage >= 1) load_lane_floats<D>(p.pi_signs, lane, es);
-            for (uint32_t g = wave; g < G; g += kWaves) {
-                const size_t qh = (size_t)seq * p.Hq + kvh * G + g;
-                float gt[CC];
-                if (p.output_stage == 2) load_lane_floats<D>(p.gate + qh * D, lane, gt);
-                auto own = [&](uint32_t (&h)[2], uint32_t (&a)[CC]) {
-                    float f[kWaves], M, L;
-                    row_weights(g, f, M, L);
-                    h[0] = __float_as_uint(M == -INFINITY ? kMasked : M * kLn2) ^ kRecMagic;
-                    h[1] = __float_as_uint(L) ^ kRecMagic;
-                    if constexpr (CC >= 4) {
-#pragma unroll
-                        for (int j = 0; j < CC; j += 4) {
-                            const float4 v = combined4((g * D + (lane & 31) * CC + j) / 4, f);
-                            a[j] = __float_as_uint(v.x) ^ kRecMagic;
-                            a[j + 1] = __float_as_uint(v.y) ^ kRecMagic;
-                            a[j + 2] = __float_as_uint(v.z) ^ kRecMagic;
-                            a[j + 3] = __float_as_uint(v.w) ^ kRecMagic;
-                        }
-                    } else {  // d = 64: the lane's two channels of a float4
-                        const uint32_t ch = (lane & 31) * CC;
-                        const float4 v = combined4((g * D + ch) / 4, f);
-                        const bool hi = (ch & 2) != 0;
-                        a[0] = __float_as_uint(hi ? v.z : v.x) ^ kRecMagic;
-                        a[1] = __float_as_uint(hi ? v.w : v.y) ^ kRecMagic;
-                    }
-                };
-                auto none = [](uint32_t(&)[2], uint32_t(&)[CC]) {};
-                float v[CC];
-                // 16 splits per chunk: wider chunks (32 per round trip)
-                // measured slower at every split count from 17 to 64
-                if constexpr (OWN)
-                    combine_records<D, true, 8>(p.records + qh * p.K * RS, k_live, lane, v,
-                                                split, own, p.poll_limit, p.timeouts);
-                else
-                    combine_records<D, true, 8>(p.records + qh * p.K * RS, k_live, lane, v, ~0u,
-                                                none, p.poll_limit, p.timeouts);
-                egress_row<D>(v, es, gt, p.out + qh * D, p.inv_sqrt_len, p.output_stage, lane);
-            }
-            return;
-        }
-        if (p.output_stage >= 1) load_lane_floats<D>(p.pi_signs, lane, es);
-        // ---- one live split: normalise into the wave-0 slice (each thread
-        // reads and writes only its own float4), then the egress.
-        for (uint32_t e4 = tid; e4 < outs4; e4 += kThreads) {
-            float f[kWaves], M, L;
-            row_weights(4 * e4 / D, f, M, L);
-            float4 v = combined4(e4, f);
-            const float inv = L == 0.0f ? 0.0f : 1.0f / L;
-            v = L == 0.0f ? make_float4(0.0f, 0.0f, 0.0f, 0.0f)
-                          : make_float4(v.x * inv, v.y * inv, v.z * inv, v.w * inv);
-            *(float4*)(part + 4 * e4) = v;
-        }
-        lds_barrier();
-        for (uint32_t g = wave; g < G; g += kWaves) {
-            const size_t qh = (size_t)seq * p.Hq + kvh * G + g;
-            float gt[CC];
-            if (p.output_stage == 2) load_lane_floats<D>(p.gate + qh * D, lane, gt);
-            float v[CC];
-#pragma unroll
-            for (int j = 0; j < CC; ++j) v[j] = part[g * D + (lane & 31) * CC + j];
-            egress_row<D>(v, es, gt, p.out + qh * D, p.inv_sqrt_len, p.output_stage, lane);
-        }
-    }
+    finish_item<D, MODE, OWN>(p, seq, kvh, split, k_live, ticket, st, qo.row_live, region);
 }
 
 // Waves per SIMD the register ring allows without spilling: two at d = 64
@@ -1075,18 +1176,16 @@ __global__ TQ4_DECODE_ATTRS void decode_kernel(DecodeParams p)
 // workgroup that has not started: the combiner of a (seq, kv head) waits only
 // for splits that took their ticket before it, each in the hands of a running
 // workgroup that only streams and exports before it fetches again.
-template <int D>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D == 256 ? 1 : 2, 2)))
-void decode_persistent_kernel(DecodeParams p)
+// The persistent kernels' plan, the same in every workgroup: per sequence
+// its live splits (at least 1) and the inclusive prefix of its full items
+// (p.Hkv * (splits - 1)), the context length (when ctx_l is not null), and,
+// for up to kLptMaxSeqs sequences (lpt), the order of the last splits,
+// longest first (ties in sequence order) -- a stable descending rank,
+// counted from keys staged in LDS. scratch: 256 free LDS words. Returns the
+// number of full items.
+__device__ uint32_t plan_items(const DecodeParams& p, uint32_t* full, uint32_t* splits,
+                               uint32_t* order, uint32_t* ctx_l, bool lpt, uint32_t* scratch)
 {
-    extern __shared__ float smem[];
-    uint32_t* full = (uint32_t*)(smem + kHdrFloats + kStripSlots + region_floats(p.G, D));
-    uint32_t* splits = full + p.B;  // max(1, live splits) per sequence
-    // Up to kLptMaxSeqs sequences: the order of the last splits, longest
-    // first (ties in sequence order), so the short ones pack the tail.
-    uint32_t* order = splits + p.B;
-    const bool lpt = p.B <= kLptMaxSeqs;
-    uint32_t* next_lds = (uint32_t*)(smem + 145);
     const int tid = threadIdx.x, lane = tid & 63;
     const uint32_t width = (p.max_blocks + p.K - 1) / p.K;
     const uint64_t capacity = (uint64_t)p.max_blocks * p.S;
@@ -1100,18 +1199,15 @@ void decode_persistent_kernel(DecodeParams p)
         kl = kl > 0 ? kl : 1u;
         splits[s] = kl;
         full[s] = p.Hkv * (kl - 1);
+        if (ctx_l != nullptr) ctx_l[s] = ctx;
         if (lpt) order[s] = pages - (kl - 1) * width;  // the last split's pages (the sort key)
     }
     __syncthreads();
-    // Rank of each sequence's last split: longer ones, then equal ones of
-    // lower index, come before it (a stable descending sort; every
-    // workgroup derives the same order). Kept in registers until all keys
-    // are read.
-    // Up to 64 sequences, the four waves each count over a quarter of the
-    // keys (partial ranks in the free q staging region, summed at placing).
+    // Ranks are kept in registers until all keys are read. Up to 64
+    // sequences, the four waves each count over a quarter of the keys
+    // (partial ranks in scratch [4][64], summed at placing).
     constexpr int kRanks = kLptMaxSeqs / kThreads;
     uint32_t rank[kRanks];
-    uint32_t* part_rank = (uint32_t*)(smem + kHdrFloats + kStripSlots);  // [4][64]
     if (lpt && p.B <= 64) {
         const uint32_t s = tid & 63, part = tid >> 6;
         uint32_t r = 0;
@@ -1124,7 +1220,7 @@ void decode_persistent_kernel(DecodeParams p)
                 r += (kt > key || (kt == key && t < s)) ? 1u : 0u;
             }
         }
-        part_rank[part * 64 + s] = r;
+        scratch[part * 64 + s] = r;
     } else if (lpt) {
 #pragma unroll
         for (int i = 0; i < kRanks; ++i) {
@@ -1159,8 +1255,7 @@ void decode_persistent_kernel(DecodeParams p)
     __syncthreads();  // every key is read: the ranks can be placed
     if (lpt && p.B <= 64) {
         if ((uint32_t)tid < p.B)
-            order[part_rank[tid] + part_rank[64 + tid] + part_rank[128 + tid] +
-                  part_rank[192 + tid]] = tid;
+            order[scratch[tid] + scratch[64 + tid] + scratch[128 + tid] + scratch[192 + tid]] = tid;
         __syncthreads();
     } else if (lpt) {
 #pragma unroll
@@ -1170,7 +1265,56 @@ void decode_persistent_kernel(DecodeParams p)
         }
         __syncthreads();
     }
-    const uint32_t n_full = full[p.B - 1];
+    return full[p.B - 1];
+}
+
+// (seq, kv head, split) of queue item `item` under the plan: the full splits
+// first, in (seq, kv head, split) order, then the last splits.
+__device__ __forceinline__ void item_coords(const DecodeParams& p, uint32_t item, uint32_t n_full,
+                                            const uint32_t* full, const uint32_t* splits,
+                                            const uint32_t* order, bool lpt, uint32_t& seq,
+                                            uint32_t& kvh, uint32_t& split)
+{
+    const int lane = threadIdx.x & 63;
+    if (item < n_full) {
+        // a full split: its sequence is the first s with full[s] > item
+        uint32_t sq = 0;
+        for (uint32_t b = 0; b < p.B; b += 64) {
+            const uint32_t i = b + lane;
+            const uint64_t m = __ballot(i < p.B && full[i] > item);
+            if (m != 0) {
+                sq = b + (uint32_t)__builtin_ctzll(m);
+                break;
+            }
+        }
+        seq = __builtin_amdgcn_readfirstlane(sq);
+        const uint32_t r = item - (seq > 0 ? full[seq - 1] : 0u);
+        const uint32_t per = splits[seq] - 1;
+        kvh = r / per;
+        split = r % per;
+    } else {
+        // a last split
+        const uint32_t r = item - n_full;
+        seq = lpt ? order[r / p.Hkv] : r / p.Hkv;
+        kvh = r % p.Hkv;
+        split = splits[seq] - 1;
+    }
+}
+
+template <int D>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D == 256 ? 1 : 2, 2)))
+void decode_persistent_kernel(DecodeParams p)
+{
+    extern __shared__ float smem[];
+    uint32_t* full = (uint32_t*)(smem + kHdrFloats + kStripSlots + region_floats(p.G, D));
+    uint32_t* splits = full + p.B;  // max(1, live splits) per sequence
+    uint32_t* order = splits + p.B;
+    const bool lpt = p.B <= kLptMaxSeqs;
+    uint32_t* next_lds = (uint32_t*)(smem + 145);
+    const int tid = threadIdx.x;
+    const uint32_t n_full =
+        plan_items(p, full, splits, order, nullptr, lpt,
+                   (uint32_t*)(smem + kHdrFloats + kStripSlots));  // the free q staging region
     const uint32_t n_items = n_full + p.B * p.Hkv;
     // kSubQueues interleaved queues (one counter line each): sub-queue x
     // holds items x, x + nq, x + 2nq, ... and serves workgroups x, x + nq,
@@ -1184,29 +1328,7 @@ void decode_persistent_kernel(DecodeParams p)
     while (item < n_items) {
         uint32_t fetched = 0;
         uint32_t seq, kvh, split;
-        if (item < n_full) {
-            // a full split: its sequence is the first s with full[s] > item
-            uint32_t sq = 0;
-            for (uint32_t b = 0; b < p.B; b += 64) {
-                const uint32_t i = b + lane;
-                const uint64_t m = __ballot(i < p.B && full[i] > item);
-                if (m != 0) {
-                    sq = b + (uint32_t)__builtin_ctzll(m);
-                    break;
-                }
-            }
-            seq = __builtin_amdgcn_readfirstlane(sq);
-            const uint32_t r = item - (seq > 0 ? full[seq - 1] : 0u);
-            const uint32_t per = splits[seq] - 1;
-            kvh = r / per;
-            split = r % per;
-        } else {
-            // a last split
-            const uint32_t r = item - n_full;
-            seq = lpt ? order[r / p.Hkv] : r / p.Hkv;
-            kvh = r % p.Hkv;
-            split = splits[seq] - 1;
-        }
+        item_coords(p, item, n_full, full, splits, order, lpt, seq, kvh, split);
         // the next item's queue fetch goes out after this item's first strip
         // loads (decode_item's hook); its value is read after the item
         decode_item<D, 1, false>(p, seq, kvh, split, [&]() {
@@ -1256,17 +1378,16 @@ __global__ void fill_zero_kernel(uint32_t* ptr, size_t words)
         ptr[i] = 0u;
 }
 
-// Workgroup slots of the persistent kernel on the current device (CUs x
+// Workgroup slots of a persistent kernel on the current device (CUs x
 // resident workgroups per CU at this LDS size), 0 if it cannot run.
-template <int D>
-uint32_t persistent_slots(size_t lds)
+template <class Kernel>
+uint32_t persistent_slots(Kernel kernel, size_t lds)
 {
     int dev = 0, cus = 0, per_cu = 0;
     if (hipGetDevice(&dev) != hipSuccess) return 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
         return 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_persistent_kernel<D>,
-                                                     kThreads, lds) != hipSuccess)
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kThreads, lds) != hipSuccess)
         return 0;
     return cus > 0 && per_cu > 0 ? (uint32_t)cus * (uint32_t)per_cu : 0u;
 }
@@ -1284,7 +1405,7 @@ hipError_t launch_decode_t(hipStream_t stream, const DecodeParams& p, int mode)
     // Fused: persistent when the split grid outnumbers the resident slots.
     if (p.queue != nullptr && p.K > 1 && p.B <= kPersistentMaxSeqs) {
         const size_t lds_p = lds + (p.B <= kLptMaxSeqs ? 3 : 2) * (size_t)p.B * sizeof(uint32_t);
-        const uint32_t slots = persistent_slots<D>(lds_p);
+        const uint32_t slots = persistent_slots(decode_persistent_kernel<D>, lds_p);
         if (slots > 0 && blocks > slots) {
             hipLaunchKernelGGL((decode_persistent_kernel<D>), dim3(slots), dim3(kThreads), lds_p,
                                stream, p);
