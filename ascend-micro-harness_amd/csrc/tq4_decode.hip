@@ -74,6 +74,9 @@ constexpr float kLn2 = 0.6931471805599453f;
 constexpr uint32_t kNib = 0x00F000F0u;   // a code at fp16 mantissa bits [7:4], both halves
 constexpr uint32_t kCodeBase = 0x3C803C80u;  // fp16 1.0 outside kNib; the nibble sign bit inside
 constexpr float kCodeOffset = 1.125f;    // fp16 code value is 1 + u/64 = 1.125 + n/64
+constexpr uint32_t kNibLo = 0x000F000Fu;     // a key code at fp16 mantissa bits [3:0], both halves
+constexpr uint32_t kCodeBaseLo = 0x4C084C08u;  // fp16 16.0 outside kNibLo; the nibble sign bit inside
+constexpr float kCodeOffsetLo = 16.125f;     // fp16 key code value is 16 + u/64 = 16.125 + n/64
 constexpr float kCodeUnit = 64.0f;
 constexpr float kTau = 8.0f;             // lazy-maximum headroom, log2 units
 constexpr float kShiftLimit = 100.0f;    // bound of a row's product normalisation shift
@@ -109,6 +112,21 @@ __device__ __forceinline__ h8_t codes8(uint32_t w)
     const uint32_t p15 = __builtin_amdgcn_bitop3_b32(w, kNib, kCodeBase, 0x6A);
     const uint32_t p26 = __builtin_amdgcn_bitop3_b32(w >> 4, kNib, kCodeBase, 0x6A);
     const uint32_t p37 = __builtin_amdgcn_bitop3_b32(w >> 8, kNib, kCodeBase, 0x6A);
+    return __builtin_bit_cast(h8_t, u4_t{p04, p15, p26, p37});
+}
+
+// The key side of codes8 with one shift instead of three: the halves of
+// nibbles 0,4 and 2,6 sit at mantissa bits [3:0] under an fp16 16.0, so
+// their value is 16 + u/64 (the same step as 1 + u/64 at bits [7:4]). The
+// score's start value removes both offsets; they cancel inside each pair's
+// score, so the larger one costs nothing that accumulates across the split.
+__device__ __forceinline__ h8_t key_codes8(uint32_t w)
+{
+    const uint32_t w8 = w >> 8;
+    const uint32_t p04 = __builtin_amdgcn_bitop3_b32(w, kNibLo, kCodeBaseLo, 0x6A);
+    const uint32_t p15 = __builtin_amdgcn_bitop3_b32(w, kNib, kCodeBase, 0x6A);
+    const uint32_t p26 = __builtin_amdgcn_bitop3_b32(w8, kNibLo, kCodeBaseLo, 0x6A);
+    const uint32_t p37 = __builtin_amdgcn_bitop3_b32(w8, kNib, kCodeBase, 0x6A);
     return __builtin_bit_cast(h8_t, u4_t{p04, p15, p26, p37});
 }
 
@@ -449,8 +467,8 @@ __device__ __forceinline__ void process_pair(RowState<D>& st, const QOps<D>& qo,
     f4_t c1 = qo.bias4, c2 = qo.bias4;
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
-        c1 = mfma32(codes8(r.k1[j]), qo.qop[j], c1);
-        c2 = mfma32(codes8(r.k2[j]), qo.qop[j], c2);
+        c1 = mfma32(key_codes8(r.k1[j]), qo.qop[j], c1);
+        c2 = mfma32(key_codes8(r.k2[j]), qo.qop[j], c2);
     }
     // scales through the wave's LDS slot: key scales of this lane's 8
     // tokens (strip sp, tokens 8*half..) at [32sp + 8half], values at +16
@@ -627,7 +645,7 @@ __device__ __forceinline__ void build_qops(QOps<D>& qo, const float* q_st, const
     constexpr int NJ = D / 32;
     const int n = lane & 15, g4 = lane >> 4;
     qo.row_live = (uint32_t)n < G;
-    float bias = 0.0f;
+    float bias = 0.0f;  // -sum of q times each key_codes8 half's offset
     qo.cf = 0.0f;
     if (qo.row_live) {
         const float* qrow = q_st + n * D + g4 * (D / 4);
@@ -639,14 +657,15 @@ __device__ __forceinline__ void build_qops(QOps<D>& qo, const float* q_st, const
                                 (_Float16)lo.z, (_Float16)hi.z, (_Float16)lo.w, (_Float16)hi.w};
             qo.qop[j] = h;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) bias += (float)h[e];
+            for (int e = 0; e < 8; ++e)
+                bias += (float)h[e] * ((e & 2) == 0 ? kCodeOffsetLo : kCodeOffset);
         }
         qo.cf = ldexpf(kCodeUnit * kLog2e, q_exp[n]);
     } else {
 #pragma unroll
         for (int j = 0; j < NJ; ++j) qo.qop[j] = h8_t{0, 0, 0, 0, 0, 0, 0, 0};
     }
-    bias = col_sum(bias) * -kCodeOffset;
+    bias = -col_sum(bias);
     qo.bias4 = f4_t{bias, bias, bias, bias};
 }
 
