@@ -574,9 +574,13 @@ __device__ __forceinline__ void process_pair(RowState<D>& st, const QOps<D>& qo,
     float psum = 0.0f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        // a dead token is 0 even while the row has no maximum yet
-        // (-inf - -inf would be NaN)
-        const float pr = sc8[i] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(sc8[i] - st.mo);
+        // A dead token is 0 even while the row has no maximum yet (-inf -
+        // -inf would be NaN). Only a masked pair holds dead tokens, and it is
+        // a wave's last: after an unmasked pair a live row's mo is finite
+        // (its first pair rescaled to a finite maximum) and a padded row's
+        // is +inf, so exp2 alone gives every product there.
+        const float pr = masked && sc8[i] == -INFINITY ? 0.0f
+                                                       : __builtin_amdgcn_exp2f(sc8[i] - st.mo);
         psum += pr;
         x[i] = (_Float16)(pr * vs[i]);
     }
