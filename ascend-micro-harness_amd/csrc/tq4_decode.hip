@@ -410,7 +410,8 @@ __host__ __device__ constexpr size_t region_floats(uint32_t G, uint32_t D)
 }
 
 // One wave's streaming state over the q rows of one item. Scores t = s - mo
-// with s = score * log2(e) (log2 units), mo = m_used - sh: P' = exp2(t) =
+// with s = score * log2(e) (log2 units), mo = m_used - sh (before a live
+// row's first rescale mo = 0, so that t = s): P' = exp2(t) =
 // P * 2^sh, and the MFMA operand is the product P' * vscale in fp16. The
 // row's shift sh is set at each rescale so that the largest product of that
 // pair lands in [1, 2): every product that matters for the row's sum then
@@ -429,11 +430,14 @@ struct RowState {
 #pragma unroll
         for (int b = 0; b < D / 16; ++b) acc[b] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
         cr = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
-        m_used = row_live ? -INFINITY : INFINITY;  // padded rows stay silent
+        // A padded row stays silent (mo = +inf: every t is -inf). A live
+        // row starts with a finite mo (t = s exactly) and thr = -inf, so its
+        // first pair holding a live token always rescales.
+        m_used = row_live ? -INFINITY : INFINITY;
         sh = 0.0f;
-        mo = m_used;
+        mo = row_live ? 0.0f : INFINITY;
         lpart = 0.0f;
-        thr = kTau;
+        thr = row_live ? -INFINITY : kTau;
         virgin = true;
     }
 };
@@ -503,9 +507,10 @@ __device__ __forceinline__ void process_pair(RowState<D>& st, const QOps<D>& qo,
     float tmax = -INFINITY, vmax = 0.0f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        tmax = fmaxf(tmax, sc8[i] - st.mo);
+        tmax = fmaxf(tmax, sc8[i]);
         vmax = fmaxf(vmax, vs[i]);
     }
+    tmax -= st.mo;  // a live row's mo is finite; a padded row's is +inf
     if (__builtin_expect(
             __any(tmax > st.thr || __builtin_amdgcn_exp2f(tmax) * vmax >= kXLimit), 0)) {
         // Move the row maximum and re-normalise the row's products.
@@ -553,7 +558,7 @@ __device__ __forceinline__ void process_pair(RowState<D>& st, const QOps<D>& qo,
             }
             const float mon = mn - shn;
             float f = 1.0f;
-            if (qo.row_live) f = st.mo == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(st.mo - mon);
+            if (qo.row_live) f = __builtin_amdgcn_exp2f(st.mo - mon);
             st.lpart *= f;
             float fr[4];
 #pragma unroll
@@ -570,21 +575,16 @@ __device__ __forceinline__ void process_pair(RowState<D>& st, const QOps<D>& qo,
             st.thr = kTau + shn;
         }
     }
+    // A dead token's t = s - mo is -inf, and so is every t of a padded row
+    // (mo = +inf); a live row's mo is always finite, so no t is NaN.
     _Float16 x[8];
-    float psum = 0.0f;
+    float pr[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        // A dead token is 0 even while the row has no maximum yet (-inf -
-        // -inf would be NaN). Only a masked pair holds dead tokens, and it is
-        // a wave's last: after an unmasked pair a live row's mo is finite
-        // (its first pair rescaled to a finite maximum) and a padded row's
-        // is +inf, so exp2 alone gives every product there.
-        const float pr = masked && sc8[i] == -INFINITY ? 0.0f
-                                                       : __builtin_amdgcn_exp2f(sc8[i] - st.mo);
-        psum += pr;
-        x[i] = (_Float16)(pr * vs[i]);
+        pr[i] = __builtin_amdgcn_exp2f(sc8[i] - st.mo);
+        x[i] = (_Float16)(pr[i] * vs[i]);
     }
-    st.lpart += psum;
+    st.lpart += ((pr[0] + pr[1]) + (pr[2] + pr[3])) + ((pr[4] + pr[5]) + (pr[6] + pr[7]));
     // A operand in the codes8 token order: (T1[0], T2[0], T1[1], T2[1], ...)
     const h8_t P = h8_t{x[0], x[4], x[1], x[5], x[2], x[6], x[3], x[7]};
     // B operands: block b = 4q + 2hb + e is channel n*d/16 + b. The lane
