@@ -158,16 +158,20 @@ size_t tq4_decode_workspace_bytes(uint32_t num_seqs, uint32_t num_heads, uint32_
 uint32_t tq4_decode_auto_splits(uint32_t num_seqs, uint32_t num_kv_heads,
                                 uint32_t max_blocks_per_seq, uint32_t block_size)
 {
-    // Workgroups for half the CUs (256), and for all their two slots when
-    // the splits would still be long (> 64 strips); splits of at most ~512
-    // strips; never fewer than 16 strips per split, and at most 32 splits.
+    // Workgroups for half the CUs (256); for one per CU while each split
+    // still holds 16 strips (20 when that takes the fused combine past one
+    // 16-split record chunk); for all their two slots when the splits would
+    // still be long (> 64 strips); splits of at most ~512 strips; never
+    // fewer than 16 strips per split, and at most 32 splits.
     // - Each extra item costs a table and a first-strip round trip, a merge
     //   and a record, and the persistent kernel orders the last splits
     //   longest first, so a batch that already fills the slots runs best
     //   with few, long items: 64 sequences x 8 KV heads, K = 1 beat K = 2 by
     //   20 % at ctx 4096; a spread of 1..32768 tokens wanted K = 4..8.
-    // - One sequence (8 KV heads): K = 16 was best from ctx 2048 to 16384,
-    //   K = 32 at 32768 and 65536.
+    // - One sequence (8 KV heads): K = 16 was best up to ctx 8192, K = 32
+    //   from 12288 (16384: 10.7 against 11.6 us). Two sequences at ctx 4096
+    //   and 8192, four at ctx 4096: one workgroup per CU, 11-16 % faster
+    //   than half the CUs.
     // - More than 32 splits combine in two record chunks and measured 5-7 us
     //   slower than 32 at d = 128.
     const uint64_t strips = (uint64_t)max_blocks_per_seq * (block_size / kStrip);
@@ -175,6 +179,8 @@ uint32_t tq4_decode_auto_splits(uint32_t num_seqs, uint32_t num_kv_heads,
                                ? (uint64_t)num_seqs * num_kv_heads
                                : 1;
     uint64_t k = (128 + items - 1) / items;
+    const uint64_t per_cu = 256 / items;
+    if (per_cu > k && strips >= (per_cu > 16 ? 20 : 16) * per_cu) k = per_cu;
     if (strips > 64 * k) {
         uint64_t more = (512 + items - 1) / items;
         const uint64_t by_work = (strips + 63) / 64;
