@@ -84,6 +84,25 @@ def test_decode_refusals_and_sizes(lib):
     assert comb(None, d, d, None, d, 1, 32, 128, 4, 0.1, 2) == -7
 
 
+def test_auto_splits_operating_points(lib):
+    """The split counts the rule was measured at (32q:8kv, d 128, page 16):
+    one sequence K = 16 up to ctx 8192 and 32 from 12288 (one workgroup per
+    CU once each split keeps 20 strips past one 16-split record chunk); two
+    and four sequences one workgroup per CU (16 strips per split suffice
+    within one chunk); a 64-sequence batch one split per (seq, kv head)."""
+    f = lib.tq4_decode_auto_splits
+    pages = lambda ctx: (ctx + 15) // 16
+    want = {(1, 2048): 8, (1, 4096): 16, (1, 4103): 16, (1, 8192): 16, (1, 12288): 32,
+            (1, 16384): 32, (1, 32768): 32, (1, 65536): 32, (2, 4096): 16, (2, 8192): 16,
+            (4, 4096): 8, (4, 8192): 8, (64, 8192): 1}
+    got = {k: f(k[0], 8, pages(k[1]), 16) for k in want}
+    assert got == want
+    # the grid of one launch stays within one workgroup per CU at these points
+    for (b, ctx), k in want.items():
+        if b <= 4:
+            assert b * 8 * k <= 256
+
+
 def test_scatter_refusals(lib):
     d = C.c_void_p(16)
     f = lib.tq4_reshape_scatter
