@@ -649,7 +649,7 @@ __device__ __forceinline__ void build_qops(QOps<D>& qo, const float* q_st, const
     constexpr int NJ = D / 32;
     const int n = lane & 15, g4 = lane >> 4;
     qo.row_live = (uint32_t)n < G;
-    float bias = 0.0f;  // -sum of q times each key_codes8 half's offset
+    float bias = 0.0f;  // sum of q times each key_codes8 half's offset (negated below)
     qo.cf = 0.0f;
     if (qo.row_live) {
         const float* qrow = q_st + n * D + g4 * (D / 4);
