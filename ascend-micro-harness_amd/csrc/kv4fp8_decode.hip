@@ -61,7 +61,13 @@ constexpr float kNegInf = -3.4028235e38f;    // kVectorNegInf
 constexpr float kGateFloor = -80.0f;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr uint32_t kRecFloats = 260;         // acc[256], m, l, pad, pad
-constexpr int kMergeFloats = kWaves * 16 * kD;
+// LDS rows of 256 floats (q rows, merge rows) are kRow apart: the pad of one
+// float4 puts eight consecutive rows' same columns on eight different bank
+// quads, so the row-strided float4 accesses below are conflict-free (at kD
+// apart they all hit one quad: the q prologue and the merge took 2.4 and
+// 2.8 us at the reference shape, 1.9 and 1.4 us padded).
+constexpr int kRow = kD + 4;
+constexpr int kMergeFloats = kWaves * 16 * kRow;
 constexpr int kScaleFloats = kWaves * 3 * kTile;
 constexpr int kQopFloats = 8 * 64 * 4;  // 8 k-steps x 64 lanes x 8 f16
 
@@ -265,21 +271,22 @@ __device__ __forceinline__ void combine_polled(const Kv4Params& p, uint32_t row,
         uint32_t aw[kPollBatch][4], hw[kPollBatch][2];
         for (uint32_t it = 0;; ++it) {
             asm volatile("" ::: "memory");  // every poll reloads
+            // Every slot loads (past `live` the last record again, the own
+            // slot its never-written words), so the loads carry no branches;
+            // the check skips those slots.
 #pragma unroll
             for (int j = 0; j < kPollBatch; ++j) {
-                const uint32_t k = k0 + j;
-                if (k < live && k != own) {
-                    rec_load<4, true>(rs, k * kRecBytes + 16u * lane, aw[j]);
-                    rec_load<2, true>(rs, k * kRecBytes + 4u * kD, hw[j]);
-                }
+                const uint32_t k = min(k0 + j, live - 1);
+                rec_load<4, true>(rs, k * kRecBytes + 16u * lane, aw[j]);
+                rec_load<2, true>(rs, k * kRecBytes + 4u * kD, hw[j]);
             }
             uint32_t mn = 0xffffffffu;
 #pragma unroll
             for (int j = 0; j < kPollBatch; ++j) {
                 const uint32_t k = k0 + j;
-                if (k < live && k != own)
-                    mn = min(min(mn, min(hw[j][0], hw[j][1])),
-                             min(min(aw[j][0], aw[j][1]), min(aw[j][2], aw[j][3])));
+                const uint32_t w = min(min(hw[j][0], hw[j][1]),
+                                       min(min(aw[j][0], aw[j][1]), min(aw[j][2], aw[j][3])));
+                mn = k < live && k != own ? min(mn, w) : mn;
             }
             if (!__any(mn == 0u)) break;
             if (it + 1 >= p.poll_limit) {  // gave up: merged from what arrived
@@ -290,26 +297,51 @@ __device__ __forceinline__ void combine_polled(const Kv4Params& p, uint32_t row,
         // the last batch is zeroed at once, earlier ones after the loop (a
         // later batch's poll would wait for their write acknowledgements)
         if (k0 + kPollBatch >= live) zero_batch(k0);
+        // merge_record over the batch in part order, four slots at a time
+        // and branch-free inside: the running maxima first, then each
+        // record's weights and sums (the same operations on the same values
+        // as record by record; slots past the live records select the running
+        // values through), so the compiler interleaves the records'
+        // independent work
+        const uint32_t nb = min((uint32_t)kPollBatch, live - k0);
+        float nm[kPollBatch];
+        float prev = run_max;
 #pragma unroll
         for (int j = 0; j < kPollBatch; ++j) {
-            const uint32_t k = k0 + j;
-            if (k >= live) break;
-            float m, l, a[4];
-            if (k == own) {
-                m = om.x;
-                l = om.y;
-                a[0] = oa.x;
-                a[1] = oa.y;
-                a[2] = oa.z;
-                a[3] = oa.w;
-            } else {
-                m = __uint_as_float(hw[j][0] ^ kRecMagic);
-                l = __uint_as_float(hw[j][1] ^ kRecMagic);
-#pragma unroll
-                for (int i = 0; i < 4; ++i) a[i] = __uint_as_float(aw[j][i] ^ kRecMagic);
-            }
-            merge_record(run_max, run_sum, x, m, l, a);
+            const float m = k0 + j == own ? om.x : __uint_as_float(hw[j][0] ^ kRecMagic);
+            nm[j] = (uint32_t)j < nb ? fmaxf(prev, m) : prev;
+            prev = nm[j];
         }
+        float pm = run_max;
+#pragma unroll
+        for (int j4 = 0; j4 < kPollBatch; j4 += 4) {
+            if ((uint32_t)j4 >= nb) break;
+#pragma unroll
+            for (int j = j4; j < j4 + 4; ++j) {
+                const bool mine = k0 + j == own;
+                const float m = mine ? om.x : __uint_as_float(hw[j][0] ^ kRecMagic);
+                const float l = mine ? om.y : __uint_as_float(hw[j][1] ^ kRecMagic);
+                float a[4];
+                a[0] = mine ? oa.x : __uint_as_float(aw[j][0] ^ kRecMagic);
+                a[1] = mine ? oa.y : __uint_as_float(aw[j][1] ^ kRecMagic);
+                a[2] = mine ? oa.z : __uint_as_float(aw[j][2] ^ kRecMagic);
+                a[3] = mine ? oa.w : __uint_as_float(aw[j][3] ^ kRecMagic);
+                const float alpha = fexp(pm - nm[j]), beta = fexp(m - nm[j]);
+                float rs = run_sum * alpha;
+                const float ps = l * beta;
+                rs = rs + ps;
+                const bool in = (uint32_t)j < nb;
+                run_sum = in ? rs : run_sum;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float u = x[i] * alpha;
+                    const float v = a[i] * beta;
+                    x[i] = in ? u + v : x[i];
+                }
+                pm = nm[j];
+            }
+        }
+        run_max = prev;
     }
     for (uint32_t k0 = 0; k0 + kPollBatch < live; k0 += kPollBatch) zero_batch(k0);
 }
@@ -320,8 +352,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
 void kv4_decode_kernel(Kv4Params p)
 {
     extern __shared__ __align__(16) float lds[];
-    float* merge = lds;                                  // [4][16][256] (q rows first)
-    float* q_lds = lds;                                  // [16][256]
+    float* merge = lds;                                  // [4][16][kRow] (q rows first)
+    float* q_lds = lds;                                  // [16][kRow]
     float* ml = lds + kMergeFloats;                      // [4][16][2]
     int* role_lds = (int*)(ml + kWaves * 32);            // [4] this part's combine role
     float* mlo = ml + kWaves * 32 + 4;                   // [16][2] merged (m, l) per head
@@ -381,7 +413,7 @@ void kv4_decode_kernel(Kv4Params p)
                 x[3] = v.w;
             }
         }
-        *(float4*)(q_lds + h * kD + 4 * lane) = make_float4(x[0], x[1], x[2], x[3]);
+        *(float4*)(q_lds + h * kRow + 4 * lane) = make_float4(x[0], x[1], x[2], x[3]);
     }
     __syncthreads();
     const size_t row0 = (size_t)token * p.Hq + p.G * kvh + head0;  // the chunk's first row
@@ -447,7 +479,7 @@ void kv4_decode_kernel(Kv4Params p)
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) {
         const int c0 = 4 * (8 * g + ks);
-        const float* qr = q_lds + n16 * kD;
+        const float* qr = q_lds + n16 * kRow;
         const float4 lo = *(const float4*)(qr + c0);
         const float4 hi = *(const float4*)(qr + 128 + c0);
         qv[ks][0] = lo.x; qv[ks][1] = lo.z; qv[ks][2] = hi.x; qv[ks][3] = hi.z;
@@ -607,7 +639,7 @@ void kv4_decode_kernel(Kv4Params p)
     // ---- this wave's (m, l, acc): acc = (64 acc' - 71.5 B) / prob_scale_last
     const float off = bsum * (kLevelUnit * kLevelOffset);
     __syncthreads();  // every wave is past its q_lds reads
-    float* mw = merge + wave * 16 * kD + n16 * kD;
+    float* mw = merge + wave * 16 * kRow + n16 * kRow;
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -646,10 +678,11 @@ void kv4_decode_kernel(Kv4Params p)
     }
     __syncthreads();
 
-    // ---- merge the four waves: thread -> head tid / 16, channels 16 (tid % 16) ..
-    // The merged row replaces the wave-0 slice (each thread reads and writes
-    // only its own channels of it); (M, L) go to mlo.
-    const uint32_t h = tid >> 4, c0 = (tid & 15) * 16;
+    // ---- merge the four waves: thread -> head tid / 16, channels 4 (tid % 16)
+    // + 64 q4 (consecutive lanes on consecutive float4s). The merged row
+    // replaces the wave-0 slice (each thread reads and writes only its own
+    // channels of it); (M, L) go to mlo.
+    const uint32_t h = tid >> 4, c0 = (tid & 15) * 4;
     if (h < gc) {
         float mwv[kWaves], M = kNegInf;
 #pragma unroll
@@ -668,13 +701,13 @@ void kv4_decode_kernel(Kv4Params p)
             float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
             for (int w = 0; w < kWaves; ++w) {
-                const float4 x = *(const float4*)(merge + (w * 16 + h) * kD + c0 + 4 * q4);
+                const float4 x = *(const float4*)(merge + (w * 16 + h) * kRow + c0 + 64 * q4);
                 o.x += x.x * f[w];
                 o.y += x.y * f[w];
                 o.z += x.z * f[w];
                 o.w += x.w * f[w];
             }
-            *(float4*)(merge + h * kD + c0 + 4 * q4) = o;
+            *(float4*)(merge + h * kRow + c0 + 64 * q4) = o;
         }
         if ((tid & 15) == 0) *(float2*)(mlo + 2 * h) = make_float2(M, L);
     }
@@ -684,7 +717,7 @@ void kv4_decode_kernel(Kv4Params p)
     // ---- one live part: its rows finish from LDS (the merge of one record)
     if (live_parts == 1) {
         for (uint32_t hh = wave; hh < gc; hh += kWaves) {
-            const float4 a4 = *(const float4*)(merge + hh * kD + 4 * lane);
+            const float4 a4 = *(const float4*)(merge + hh * kRow + 4 * lane);
             const float2 m2 = *(const float2*)(mlo + 2 * hh);
             const float a[4] = {a4.x, a4.y, a4.z, a4.w};
             float x[4] = {0.0f, 0.0f, 0.0f, 0.0f}, run_max = kNegInf, run_sum = 0.0f;
@@ -701,7 +734,7 @@ void kv4_decode_kernel(Kv4Params p)
         if (role >= 0 && hh % R == (uint32_t)role) continue;
         const __amdgpu_buffer_rsrc_t rs =
             records_rsrc(p.records + (row0 + hh) * p.parts * kRecFloats);
-        rec_store<4, true>(rs, part * kRecBytes + 16u * lane, merge + hh * kD + 4 * lane);
+        rec_store<4, true>(rs, part * kRecBytes + 16u * lane, merge + hh * kRow + 4 * lane);
         if (lane == 0) rec_store<2, true>(rs, part * kRecBytes + 4u * kD, mlo + 2 * hh);
     }
     if (role < 0) return;
@@ -710,7 +743,7 @@ void kv4_decode_kernel(Kv4Params p)
     for (uint32_t i = wave; role + R * i < gc; i += kWaves) {
         const uint32_t hh = role + R * i;
         float x[4], run_sum;
-        combine_polled(p, row0 + hh, live_parts, part, merge + hh * kD, mlo + 2 * hh, lane, x,
+        combine_polled(p, row0 + hh, live_parts, part, merge + hh * kRow, mlo + 2 * hh, lane, x,
                        run_sum);
         finish_row(p, row0 + hh, x, run_sum, lane);
     }
