@@ -605,9 +605,16 @@ __device__ __forceinline__ void process_pair(RowState<D>& st, const QOps<D>& qo,
     st.cr = mfma32(P, offset_col, st.cr);
 }
 
+// Staged q rows are kQRow floats apart: the pad of one float4 puts the
+// same column of eight consecutive rows on eight different bank quads, so
+// build_qops' row-strided float4 reads are conflict-free (D apart, they all
+// fall on one quad).
+template <int D>
+constexpr int kQRow = D + 4;
+
 // Rotate this wave's q rows (g = wave, wave + 4, ...; lane owns channels
 // lane*CPL ..), fold inv_sqrt_len and the softmax scale, normalise each row
-// by a power of two and stage it in q_st [G][D] (exponent in q_exp[g]).
+// by a power of two and stage it in q_st [G][kQRow<D>] (exponent in q_exp[g]).
 template <int D>
 __device__ __forceinline__ void stage_q_rows(const DecodeParams& p,
                                              const uint16_t (&qraw)[4][D / 64],
@@ -636,7 +643,7 @@ __device__ __forceinline__ void stage_q_rows(const DecodeParams& p,
         a = wave_max(a);
         const int kq = a > 0.0f ? exponent_of(a) : 0;
 #pragma unroll
-        for (int j = 0; j < CPL; ++j) q_st[g * D + lane * CPL + j] = ldexpf(v[j], -kq);
+        for (int j = 0; j < CPL; ++j) q_st[g * kQRow<D> + lane * CPL + j] = ldexpf(v[j], -kq);
         if (lane == 0) q_exp[g] = kq;
     }
 }
@@ -652,7 +659,7 @@ __device__ __forceinline__ void build_qops(QOps<D>& qo, const float* q_st, const
     float bias = 0.0f;  // sum of q times each key_codes8 half's offset (negated below)
     qo.cf = 0.0f;
     if (qo.row_live) {
-        const float* qrow = q_st + n * D + g4 * (D / 4);
+        const float* qrow = q_st + n * kQRow<D> + g4 * (D / 4);
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
             const float4 lo = *(const float4*)(qrow + 8 * j);
