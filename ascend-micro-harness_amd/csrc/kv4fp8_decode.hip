@@ -113,10 +113,25 @@ __device__ __forceinline__ float fexp(float x) { return __builtin_amdgcn_exp2f(x
 // nearest even, subnormals kept), back to FP32 (v_cvt_pk_f32_fp8) and packed
 // as f16 (exact: every e4m3 value is an f16 value, so the truncating pack
 // does not round).
+// Only the low word of the conversion is read, so its other word may come
+// from any register: a's bits, rather than a zero to materialise.
 __device__ __forceinline__ h2_t fp8_pair(float a, float b)
 {
-    const uint32_t w = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+    const uint32_t w =
+        (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a, b, __float_as_int(a), false);
     const auto f = __builtin_amdgcn_cvt_pk_f32_fp8(w, false);
+    return __builtin_bit_cast(h2_t, __builtin_amdgcn_cvt_pkrtz(f[0], f[1]));
+}
+
+// The same, also handing back the two values in FP32 (equal to the f16
+// halves).
+__device__ __forceinline__ h2_t fp8_pair_f(float a, float b, float& fa, float& fb)
+{
+    const uint32_t w =
+        (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a, b, __float_as_int(a), false);
+    const auto f = __builtin_amdgcn_cvt_pk_f32_fp8(w, false);
+    fa = f[0];
+    fb = f[1];
     return __builtin_bit_cast(h2_t, __builtin_amdgcn_cvt_pkrtz(f[0], f[1]));
 }
 
@@ -497,10 +512,11 @@ void kv4_decode_kernel(Kv4Params p)
     for (int ks = 0; ks < 8; ++ks) {
 #pragma unroll
         for (int j = 0; j < 8; j += 2) {
-            const h2_t h = fp8_pair(qv[ks][j] * q_scale, qv[ks][j + 1] * q_scale);
+            float f0, f1;
+            const h2_t h = fp8_pair_f(qv[ks][j] * q_scale, qv[ks][j + 1] * q_scale, f0, f1);
             qop[ks][j] = h[0];
             qop[ks][j + 1] = h[1];
-            q1 += (float)h[0] + (float)h[1];
+            q1 += f0 + f1;  // (float)h[i] == f_i: every e4m3 value is an f16 value
         }
     }
     q1 = col_sum(q1);
