@@ -406,7 +406,10 @@ __device__ __forceinline__ void load_lane_floats(const float* src, int lane, flo
 
 __host__ __device__ constexpr size_t region_floats(uint32_t G, uint32_t D)
 {
-    return 4ull * G * D;  // q staging [G][D], then the four waves' rows [4][G][D]
+    // q staging [G][D + 4], then the four waves' rows [4][G][D], disjoint: a
+    // wave without pairs parks its rows while the others may still be
+    // reading q for their operands
+    return (size_t)G * (D + 4) + 4ull * G * D;
 }
 
 // One wave's streaming state over the q rows of one item. Scores t = s - mo
@@ -728,7 +731,7 @@ __device__ __forceinline__ void finish_item(const DecodeParams& p, uint32_t seq,
     // ---- merge the four waves. Each parks its raw rows (offset column
     // removed) and (m, l, 2^-sh) in LDS; then every output float4 combines
     // the four copies with the row's common maximum.
-    float* part = region;  // [kWaves][G][D]
+    float* part = region + G * kQRow<D>;  // [kWaves][G][D], past the q staging rows
     park_rows<D>(st, row_live, m_x, l_x, u_x, part, G, wave, lane);
     if constexpr (MODE == 1) {
         if (p.K > 1 && tid == 0) {
@@ -1102,8 +1105,9 @@ __device__ __forceinline__ void decode_item(const DecodeParams& p, const uint32_
     lds_barrier();
     QOps<D> qo;
     build_qops<D>(qo, q_st, q_exp, G, lane);
-    // q_st is next overwritten after the first merge barrier, which every
-    // wave reaches only after building its operands.
+    // The merge rows lie past q_st, so a wave without pairs may park its
+    // rows while the others still read q here; q_st is next written by the
+    // next item's prologue, behind the item's closing barriers.
     RowState<D> st;
     st.reset(qo.row_live);
 

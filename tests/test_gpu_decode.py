@@ -335,6 +335,42 @@ def test_persistent_large_batch(tq4, oracle, B):
     check_out(got, want, f"persistent B={B}")
 
 
+@pytest.mark.parametrize("B", [1000, 64])
+def test_short_splits_repeatable(tq4, oracle, B):
+    """Splits of one to three 32-token pairs leave waves without pairs; those
+    park their merge rows while the other waves may still be reading the
+    staged q rows, so the two LDS areas must not overlap. Six calls on one
+    workspace (the persistent kernel at B = 1000, the one-launch kernel at
+    B = 64) must each match the oracle and be bit-identical to the first."""
+    import torch
+    rng = np.random.default_rng(0x5E30 + B)
+    # page 16, 10 pages per table, K = 2: the last split (pages 5..) holds
+    # 1..80 tokens, mostly one to three pairs
+    ctx = [int(x) for x in rng.integers(81, 160, B)]
+    P = sum((c + 15) // 16 for c in ctx) + 8
+    Hq, H, d, S, K = 4, 1, 128, 16, 2
+    kc, vc, sc, tables, signs, isl = build_cache(oracle, rng, ctx, H, d, S, P)
+    ctx_a = np.array(ctx, np.int32)
+    q = f32_to_bf16(rng.standard_normal((B, Hq, d)).astype(np.float32))
+    scale = np.float32(1.0 / math.sqrt(d))
+    _, want = oracle.paged_decode(q, kc, vc, sc, tables, ctx_a, signs, None, Hq, H, d, S, P, K,
+                                  scale, isl, 1, threads=8)
+    ws = tq4.decode_workspace(B, Hq, H, d, K)
+    args = [dev(q), dev(kc), dev(vc), dev(sc), dev(tables), dev(ctx_a), dev(signs)]
+    first = None
+    for call in range(6):
+        out = tq4.paged_decode(*args, H, S, P, workspace=ws, num_splits=K, scale=float(scale),
+                               inv_sqrt_len=float(isl))
+        torch.cuda.synchronize()
+        got = host(out)
+        check_out(got, want, f"short splits B={B} call {call}")
+        if first is None:
+            first = got
+        else:
+            assert np.array_equal(got, first), f"call {call} differs from call 0"
+    assert tq4.decode_poll_timeouts(ws, B, H) == 0
+
+
 def test_persistent_fewer_live_items_than_slots(tq4, oracle):
     """A large split grid whose live items are fewer than the resident
     workgroups: the surplus workgroups leave at once, nobody fetches."""
