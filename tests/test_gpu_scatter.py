@@ -167,4 +167,11 @@ def test_config5_batched_decode_step(tq4, oracle):
             record_margin(f"configs[4] K={K or 'auto'} seq {b}", mx, mr, 2e-2, 1e-3)
             assert mx <= 2e-2 and mr <= 1e-3, (K, b, mx, mr)
         if K:
+            # the work queue deals items to workgroups in a different order
+            # on every call; the output must not depend on it
+            for call in range(3):
+                again = tq4.paged_decode(dev(q), kc, vc, sc, dev(tables), dev(ctx1), dev(signs),
+                                         H, S, P, workspace=ws, num_splits=K,
+                                         scale=float(scale), inv_sqrt_len=isl)
+                assert np.array_equal(host(again), got), f"K={K} call {call + 1} differs"
             assert tq4.decode_poll_timeouts(ws, B, H) == 0
