@@ -371,6 +371,44 @@ def test_short_splits_repeatable(tq4, oracle, B):
     assert tq4.decode_poll_timeouts(ws, B, H) == 0
 
 
+@pytest.mark.parametrize("case", [
+    # (ctx lengths, Hq, H, d, page, K): configs[2]; ragged with 40 splits
+    # (three record chunks); GQA 16 at d = 256; short splits at d = 64
+    ([4096], 32, 8, 128, 16, 16),
+    ([4103], 32, 8, 128, 16, 40),
+    ([700, 1500], 32, 2, 256, 32, 6),
+    ([90, 33, 160, 7], 8, 4, 64, 16, 8),
+])
+def test_one_launch_repeat_bit_identical(tq4, oracle, case):
+    """The one-launch fused decode, four calls on one workspace: every call
+    matches the oracle and has the first call's bits (the output may not
+    depend on which split takes the last ticket or on wave timing)."""
+    import torch
+    ctx, Hq, H, d, S, K = case
+    rng = np.random.default_rng(0x5E40 + d + K)
+    P = sum((c + S - 1) // S for c in ctx) + 8
+    kc, vc, sc, tables, signs, isl = build_cache(oracle, rng, ctx, H, d, S, P)
+    ctx_a = np.array(ctx, np.int32)
+    q = f32_to_bf16(rng.standard_normal((len(ctx), Hq, d)).astype(np.float32))
+    scale = np.float32(1.0 / math.sqrt(d))
+    _, want = oracle.paged_decode(q, kc, vc, sc, tables, ctx_a, signs, None, Hq, H, d, S, P, K,
+                                  scale, isl, 1, threads=8)
+    ws = tq4.decode_workspace(len(ctx), Hq, H, d, K)
+    args = [dev(q), dev(kc), dev(vc), dev(sc), dev(tables), dev(ctx_a), dev(signs)]
+    first = None
+    for call in range(4):
+        out = tq4.paged_decode(*args, H, S, P, workspace=ws, num_splits=K, scale=float(scale),
+                               inv_sqrt_len=float(isl))
+        torch.cuda.synchronize()
+        got = host(out)
+        check_out(got, want, f"repeat {ctx} K {K} call {call}")
+        if first is None:
+            first = got
+        else:
+            assert np.array_equal(got, first), f"call {call} differs from call 0"
+    assert tq4.decode_poll_timeouts(ws, len(ctx), H) == 0
+
+
 def test_persistent_fewer_live_items_than_slots(tq4, oracle):
     """A large split grid whose live items are fewer than the resident
     workgroups: the surplus workgroups leave at once, nobody fetches."""
