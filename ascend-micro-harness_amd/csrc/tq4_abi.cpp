@@ -26,8 +26,8 @@ int launched(hipError_t e) { return e == hipSuccess ? TQ4_OK : TQ4_ERR_LAUNCH; }
 // served one after another, so counters that many workgroups hit at once
 // must not share one.
 constexpr size_t kQueueBytes = 1024;
-constexpr uint32_t kFlagsKnown = TQ4_DECODE_QUERY_ROTATED | TQ4_DECODE_TEST_POLL_BOUND |
-                                 TQ4_DECODE_TEST_WITHHOLD;
+constexpr uint32_t kFlagsKnown = TQ4_DECODE_QUERY_ROTATED | TQ4_DECODE_PRECISE |
+                                 TQ4_DECODE_TEST_POLL_BOUND | TQ4_DECODE_TEST_WITHHOLD;
 size_t ticket_bytes(uint32_t num_seqs, uint32_t num_kv_heads)
 {
     return ((size_t)num_seqs * num_kv_heads * tq4::kTicketStride * sizeof(uint32_t) + 255) &
@@ -299,6 +299,7 @@ int tq4_paged_decode(void* stream, const uint16_t* q, const int8_t* key_cache,
                            pi_signs, num_seqs, num_heads, num_kv_heads, head_size, block_size,
                            num_blocks, max_blocks_per_seq, flags);
     if (rc != TQ4_OK) return rc;
+    if (flags & TQ4_DECODE_PRECISE) return TQ4_ERR_FLAGS;  // the partials entry's mode only
     if (!out) return TQ4_ERR_NULL_POINTER;
     if (output_stage > 2 || (output_stage == 2 && !gate)) return TQ4_ERR_OUTPUT_STAGE;
     if (output_stage >= 1 && !pi_signs) return TQ4_ERR_ROTATION;
@@ -385,13 +386,17 @@ int tq4_paged_decode_partials(void* stream, const uint16_t* q, const int8_t* key
                            pi_signs, num_seqs, num_heads, num_kv_heads, head_size, block_size,
                            num_blocks, max_blocks_per_seq, flags);
     if (rc != TQ4_OK) return rc;
-    if (flags & ~TQ4_DECODE_QUERY_ROTATED) return TQ4_ERR_FLAGS;  // no poll, no test hook
+    // no poll, no test hook
+    if (flags & ~(TQ4_DECODE_QUERY_ROTATED | TQ4_DECODE_PRECISE)) return TQ4_ERR_FLAGS;
     if (num_splits == 0 || num_splits > TQ4_MAX_SPLITS ||
         !split_pages_ok(max_blocks_per_seq, block_size, num_splits))
         return TQ4_ERR_SPLITS;
     if ((uint64_t)num_seqs * num_kv_heads * num_splits > 0x7fffffffull) return TQ4_ERR_RANGE;
-    if (!workspace || ((uintptr_t)workspace & 15u) ||
-        workspace_bytes < tq4::decode_records_bytes(num_seqs, num_heads, head_size, num_splits))
+    // exactly the records [num_seqs][num_heads][num_splits][head_size + 4]
+    // (the fused entry's size adds padding, tickets and counters)
+    const size_t records =
+        (size_t)num_seqs * num_heads * num_splits * (head_size + 4) * sizeof(float);
+    if (!workspace || ((uintptr_t)workspace & 15u) || workspace_bytes < records)
         return TQ4_ERR_WORKSPACE;
     tq4::DecodeParams p = make_params(q, key_cache, value_cache, scale_cache, block_tables,
                                       context_lens, pi_signs, nullptr, num_seqs, num_heads,
@@ -399,6 +404,8 @@ int tq4_paged_decode_partials(void* stream, const uint16_t* q, const int8_t* key
                                       max_blocks_per_seq, num_splits, scale, inv_sqrt_len, 0,
                                       flags);
     p.records = workspace;
+    if (flags & TQ4_DECODE_PRECISE)
+        return launched(tq4::launch_decode_precise((hipStream_t)stream, p));
     return launched(tq4::launch_decode((hipStream_t)stream, p, 0));
 }
 

@@ -46,6 +46,8 @@ struct DecodeParams {
 // mode 0: partials only; mode 1: fused (partials + last-workgroup combine).
 hipError_t launch_decode(hipStream_t stream, const DecodeParams& p, int mode);
 hipError_t launch_combine(hipStream_t stream, const DecodeParams& p);
+// Partial records in the reference's FP32 operation order (tq4_precise.hip).
+hipError_t launch_decode_precise(hipStream_t stream, const DecodeParams& p);
 hipError_t launch_fill_zero(hipStream_t stream, void* ptr, size_t bytes);
 
 // Codebook leaves (count = elements, a multiple of 8).

@@ -141,6 +141,14 @@ int tq4_reshape_scatter(void* stream, uint32_t block_dim, const uint16_t* key,
  * flags: TQ4_DECODE_QUERY_ROTATED = q already holds Pi q (no rotation).
  */
 #define TQ4_DECODE_QUERY_ROTATED 1u
+/* tq4_paged_decode_partials only: FP32 scores and recurrence in the
+ * reference's operation order, on the vector ALU, with the rotated query
+ * rounded to BF16 first (the reference device's score operand,
+ * tests/common/paged_decode_oracle.hpp:506-514; a pre-rotated q is BF16
+ * already). Its records meet the reference rig's budgets
+ * (tests/npu/turboquant_splitk_rigs.hpp:144-158); slower than the default
+ * MFMA path, whose fp16 operands agree with them to about 2^-11. */
+#define TQ4_DECODE_PRECISE 2u
 /* Test hooks of the fused entry's bounded wait (never set in production):
  * TQ4_DECODE_TEST_POLL_BOUND cuts a combiner's record poll to 16 attempts
  * (from 2^20); TQ4_DECODE_TEST_WITHHOLD (accepted only together with the
@@ -244,8 +252,10 @@ int tq4_paged_decode_noalloc(void* stream, const uint16_t* q, const int8_t* key_
  * per-sequence context lengths instead of one seq_len and a page window, a
  * [num_seqs][max_blocks_per_seq] table, pi_signs instead of a 256 x 256
  * pi_table, one [m, l, 0, 0, acc] record per (seq, q head, split) instead of
- * [m(8) | l(8) | acc] per packed row, and an FP16 q operand (finer than the
- * reference device's BF16 q_rot). */
+ * [m(8) | l(8) | acc] per packed row. The default path feeds the MFMA an FP16
+ * q operand and FP16 P * value-scale operands; with TQ4_DECODE_PRECISE the
+ * records follow the reference's FP32 recurrence on a BF16 q_rot. workspace
+ * holds at least num_seqs * num_heads * num_splits * (head_size + 4) floats. */
 int tq4_paged_decode_partials(void* stream, const uint16_t* q, const int8_t* key_cache,
                               const int8_t* value_cache, const float* scale_cache,
                               const int32_t* block_tables, const int32_t* context_lens,

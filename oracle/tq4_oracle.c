@@ -490,6 +490,20 @@ void tq4o_combine_step(float* m, float* l, float* acc, float m_t, float l_t, con
 }
 
 #define TQ4O_FLAG_QUERY_ROTATED 1u
+#define TQ4O_FLAG_QROT_BF16 2u
+
+/* q_eff = bf16(Pi q) * scale: the rotated query rounded to BF16 before the
+ * score, as the reference device's Fixpipe leaves it
+ * (paged_decode_oracle.hpp:506-514, GoldenQRotBf16). */
+static void rotate_query_bf16(const uint16_t* q, const float* signs, uint32_t d,
+                              float inv_sqrt_len, float scale, float* q_eff)
+{
+    float x[512], y[512];
+    for (uint32_t c = 0; c < d; ++c) x[c] = tq4o_bf16_to_f32(q[c]);
+    tq4o_rotate_ingress(x, signs, d, y);
+    for (uint32_t c = 0; c < d; ++c)
+        q_eff[c] = tq4o_bf16_to_f32(tq4o_f32_to_bf16(y[c] * inv_sqrt_len)) * scale;
+}
 
 typedef struct {
     const uint16_t* q;
@@ -535,6 +549,8 @@ static void decode_item(const DecodeJob* j, uint32_t item)
         const uint16_t* qrow = j->q + ((uint64_t)seq * j->Hq + qh) * d;
         if (j->flags & TQ4O_FLAG_QUERY_ROTATED) {
             for (uint32_t c = 0; c < d; ++c) q_eff[c] = tq4o_bf16_to_f32(qrow[c]) * j->scale;
+        } else if (j->flags & TQ4O_FLAG_QROT_BF16) {
+            rotate_query_bf16(qrow, j->signs, d, j->inv_sqrt_len, j->scale, q_eff);
         } else {
             tq4o_rotate_query(qrow, j->signs, d, j->inv_sqrt_len, j->scale, q_eff);
         }

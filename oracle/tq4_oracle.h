@@ -92,6 +92,9 @@ void tq4o_rotate_query(const uint16_t* q, const float* signs, uint32_t d, float 
                        float scale, float* q_eff);
 void tq4o_combine_step(float* m, float* l, float* acc, float m_t, float l_t, const float* acc_t,
                        uint32_t d);
+/* decode flags: 1 = q already holds Pi q (BF16); 2 = round Pi q to BF16
+ * before the score, the reference device's operand
+ * (paged_decode_oracle.hpp:506-514); neither = FP32 q_rot. */
 int tq4o_decode_partials(const uint16_t* q, const int8_t* key_cache, const int8_t* value_cache,
                          const float* scale_cache, const int32_t* block_tables,
                          const int32_t* context_lens, const float* pi_signs, float* workspace,

@@ -31,6 +31,8 @@ IN_BF16 = 1
 POLICY_PREFILL = 0
 POLICY_EXACT = 1
 FLAG_QUERY_ROTATED = 1
+FLAG_QROT_BF16 = 2  # oracle: round Pi q to BF16 before the score (the reference device operand)
+FLAG_PRECISE = 2  # device partials: TQ4_DECODE_PRECISE
 
 
 def ptr(a):

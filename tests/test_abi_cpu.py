@@ -200,6 +200,7 @@ def test_flag_and_timeout_refusals(lib):
                    C.c_float(0.1), C.c_float(0.1), 1, flags)
     assert call(1 << 5) == -12
     assert call(1 << 31) == -12                      # withhold without the bound
+    assert call(2) == -12                            # TQ4_DECODE_PRECISE: partials only
     part = lib.tq4_paged_decode_partials
     assert part(None, d, d, d, d, d, d, d, d, ws, 1, 8, 2, 128, 16, 64, 4, 2, C.c_float(0.1),
                 C.c_float(0.1), 1 << 30) == -12       # partials: no poll, no hook
@@ -222,5 +223,6 @@ def test_noalloc_refusals_before_any_hip_call(lib):
                   C.c_float(0.1), C.c_float(0.1), 1, flags)
     assert call(64, 16) == -13                       # 17.3 MB of workspace > 16 MiB
     assert call(1, 4, 1 << 30) == -12                # no test hooks
+    assert call(1, 4, 2) == -12                      # nor the partials' precise mode
     assert call(1, 300) == -5                        # splits
     assert lib.tq4_status_string(-13) != b"unknown status"

@@ -7,10 +7,10 @@ are checked against the oracle's FP32 records with budgets 1e-3*max(1,|m|)
 for m, 2e-3*max(1,l) for l and 2e-3*max|acc| + 1e-5*l + 1e-6 for acc, and
 the empty-split neutral element exactly. The reference rig's budgets
 (tests/npu/turboquant_splitk_rigs.hpp:144-158: m 2e-6, l 1e-4, acc 2e-4)
-assume its exact BF16 score panel; this kernel feeds the MFMA the rotated
-query in fp16 (11-bit significand, finer than the reference device's BF16
-q_rot, 8 bits), so a score carries a relative error up to ~2^-11 and m
-moves by that much.
+assume its exact BF16 score panel; the MFMA kernel feeds the rotated query
+in fp16 and P * value scale in fp16, so a score carries a relative error up
+to ~2^-11 and m moves by that much. TQ4_DECODE_PRECISE (FP32 recurrence,
+BF16 q_rot) is held to the rig's budgets.
 """
 import math
 
@@ -18,7 +18,8 @@ import numpy as np
 import pytest
 
 from gpu_helpers import bf16_out_error, canary_bytes, canary_floats, dev, host, record_margin
-from oracle_bindings import FLAG_QUERY_ROTATED, IN_BF16, bf16_to_f32, f32_to_bf16
+from oracle_bindings import (FLAG_PRECISE, FLAG_QROT_BF16, FLAG_QUERY_ROTATED, IN_BF16, bf16_to_f32,
+                             f32_to_bf16)
 
 pytestmark = pytest.mark.gpu
 
@@ -156,6 +157,33 @@ def test_config4_ctx32768(tq4, oracle, long_context, K):
     check_out(host(out), want, f"ctx 32768 K {kk}{' (auto)' if K == 0 else ''}")
 
 
+@pytest.fixture(scope="module")
+def longest_context(oracle):
+    """One ctx-65536 sequence (the split sweep's longest row), cache built once."""
+    rng = np.random.default_rng(0x71340014)
+    P = 4096 + 8
+    kc, vc, sc, tables, signs, isl = build_cache(oracle, rng, [65536], 8, 128, 16, P)
+    q = f32_to_bf16(rng.standard_normal((1, 32, 128)).astype(np.float32))
+    return P, q, kc, vc, sc, tables, signs, isl
+
+
+@pytest.mark.parametrize("K", [8, 16, 32, 0])
+def test_sweep_ctx65536(tq4, oracle, longest_context, K):
+    """The split sweep's ctx 65536 rows (K 8, 16, 32 and the auto count the
+    bench times): the longest single sequence timed, where the combine's
+    mean-relative error grows most with context."""
+    P, q, kc, vc, sc, tables, signs, isl = longest_context
+    ctx = np.array([65536], np.int32)
+    kk = K or tq4.auto_splits(1, 8, tables.shape[1], 16)
+    scale = np.float32(1.0 / math.sqrt(128))
+    _, want = oracle.paged_decode(q, kc, vc, sc, tables, ctx, signs, None, 32, 8, 128, 16, P,
+                                  kk, scale, isl, 1, threads=16)
+    print(f"ctx 65536 K {kk}", flush=True)
+    out = tq4.paged_decode(dev(q), dev(kc), dev(vc), dev(sc), dev(tables), dev(ctx), dev(signs),
+                           8, 16, P, num_splits=K, scale=float(scale), inv_sqrt_len=float(isl))
+    check_out(host(out), want, f"ctx 65536 K {kk}{' (auto)' if K == 0 else ''}")
+
+
 @pytest.mark.parametrize("G", [1, 4, 6, 16])
 @pytest.mark.parametrize("d", [64, 128, 256])
 def test_gqa_and_head_size(tq4, oracle, G, d):
@@ -253,6 +281,44 @@ def test_partials_match_oracle(tq4, oracle):
     out = tq4.splitk_combine(ws, dev(signs), 2, Hq, d, K, inv_sqrt_len=float(isl))
     _, want_out = oracle.combine(want, signs, None, Hq, d, K, isl, 1)
     check_out(host(out), want_out, "combine")
+
+
+@pytest.mark.parametrize("d,G", [(128, 4), (64, 16), (256, 6)])
+def test_precise_partials_rig_budgets(tq4, oracle, d, G):
+    """TQ4_DECODE_PRECISE on an unrotated query: the kernel rotates q in FP32
+    and rounds Pi q to BF16 (the reference device's score operand), the
+    oracle does the same (FLAG_QROT_BF16); the records meet the reference
+    rig's budgets (m 2e-6, l 1e-4, acc 2e-4: turboquant_splitk_rigs.hpp:144-158)
+    for several split counts, a ragged tail whose dead slots hold NaN
+    canaries, a short sequence with empty splits, and G up to 16 rows."""
+    from test_gpu_golden import RIG, check_records
+    rng = np.random.default_rng(0x7E5 + d + G)
+    H, S = 2, 16
+    Hq = H * G
+    ctx_lens = [1000 + 7, 37]
+    P = sum((c + S - 1) // S for c in ctx_lens) + 8
+    kc, vc, sc, tables, signs, isl = build_cache(oracle, rng, ctx_lens, H, d, S, P)
+    ctx = np.array(ctx_lens, np.int32)
+    q = f32_to_bf16(rng.standard_normal((2, Hq, d)).astype(np.float32))
+    scale = np.float32(1.0 / math.sqrt(d))
+    worst = [0.0, 0.0, 0.0]
+    for K in (1, 3, 8):
+        want = oracle.decode_partials(q, kc, vc, sc, tables, ctx, signs, Hq, H, d, S, P, K, scale,
+                                      isl, flags=FLAG_QROT_BF16)
+        ws = tq4.paged_decode_partials(dev(q), dev(kc), dev(vc), dev(sc), dev(tables), dev(ctx),
+                                       dev(signs), H, S, P, K, scale=float(scale),
+                                       inv_sqrt_len=float(isl), flags=FLAG_PRECISE)
+        got = host(ws).astype(np.float64)
+        for b in range(2):
+            for h in range(Hq):
+                for k in range(K):
+                    rec = got[b, h, k][None]
+                    w = want[b, h, k].astype(np.float64)
+                    fr = check_records(rec, w[None, 0], w[None, 1], w[None, 4:], RIG,
+                                       f"d {d} G {G} K {K} b {b} h {h} split {k}")
+                    worst = [max(x, y) for x, y in zip(worst, fr)]
+    print(f"precise partials d {d} G {G}: worst m/l/acc fraction of the rig budget "
+          f"{worst[0]:.3f} / {worst[1]:.3f} / {worst[2]:.3f}")
 
 
 def test_combine_uniform_closed_form(tq4, oracle):

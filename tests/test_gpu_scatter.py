@@ -147,10 +147,9 @@ def test_config5_batched_decode_step(tq4, oracle):
     after = [host(kc), host(vc), host(sc)]
     assert_same(after, o)
     # split-K decode over ctx + 1, against the oracle on the same cache image:
-    # the auto split count (one launch, local finish) and K = 3, the count
-    # bench.py times for this batch, which runs the persistent work-queue
-    # kernel (64 x 8 x 3 items > the resident workgroup slots) on a fresh
-    # workspace
+    # the auto split count (one launch, local finish), which bench.py times
+    # for this batch, and K = 3, which runs the persistent work-queue kernel
+    # (64 x 8 x 3 items > the resident workgroup slots) on a fresh workspace
     q = f32_to_bf16(rng.standard_normal((B, Hq, d)).astype(np.float32))
     ctx1 = (ctx + 1).astype(np.int32)
     scale = np.float32(1 / math.sqrt(d))
