@@ -78,8 +78,9 @@ int geometry(const tq4_kv4fp8_launch* L)
 
 uint64_t round256(uint64_t b) { return (b + 255) & ~(uint64_t)255; }
 
-// Workspace: the part tickets of every (token, kv head, chunk), then the
-// partial records of every (token, q head, part); both all-zero between calls.
+// Workspace: the part ticket counter of every (token, kv head, chunk), then
+// the partial records of every (token, q head, part); both all-zero between
+// calls.
 uint64_t counters_bytes(const tq4_kv4fp8_launch* L, const Plan& p)
 {
     return round256((uint64_t)L->tokens * L->kv_heads * p.chunks * sizeof(uint32_t));
@@ -109,6 +110,9 @@ int common_checks(const tq4_kv4fp8_launch* L, const tq4_kv4fp8_buffers* b, const
         return TQ4_ERR_GEOMETRY;
     if (!aligned16(b->workspace) || L->workspace_bytes < workspace_need(L, plan))
         return TQ4_ERR_WORKSPACE;
+    // a group's tickets count in 16 bits of its counter word (at most
+    // max_blocks / 8192 + 1024 parts arise; checked all the same)
+    if (plan.parts > 0xFFFFu) return TQ4_ERR_GEOMETRY;
     if (L->test_flags & ~(uint32_t)(TQ4_KV4FP8_TEST_POLL_BOUND | TQ4_KV4FP8_TEST_WITHHOLD))
         return TQ4_ERR_FLAGS;
     if ((L->test_flags & TQ4_KV4FP8_TEST_WITHHOLD) && !(L->test_flags & TQ4_KV4FP8_TEST_POLL_BOUND))

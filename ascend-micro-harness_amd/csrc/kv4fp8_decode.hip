@@ -15,7 +15,11 @@
 // in LDS. The parts holding the last four tickets of their (token, kv head,
 // chunk) then merge the group's partial records (m, l, acc), a quarter of
 // the rows each, in the same launch, and run the egress; the other parts
-// only export records. Tiles are the reference's tiles (64 aligned rows of
+// only export records. A combiner waits only for parts that hold a ticket:
+// an early combiner (not the last ticket) merges only if every ticket had
+// been taken when it registered (every part has then started), else it hands
+// its rows to the last ticket holder -- so no part ever waits on one that
+// has not started, whatever the number of workgroups in flight. Tiles are the reference's tiles (64 aligned rows of
 // the sequence), so the per-tile FP8 operands are the same; only the
 // summation order of the merges differs.
 //
@@ -247,6 +251,8 @@ __device__ __forceinline__ void finish_row(const Kv4Params& p, uint32_t row, flo
 
 constexpr uint32_t kRecBytes = kRecFloats * 4;
 constexpr int kPollBatch = 16;  // records polled together (one round trip)
+constexpr uint32_t kTicketMask = 0xFFFFu;  // counter word: tickets taken
+constexpr uint32_t kRegShift = 16;         // counter word: early combiners registered
 
 // The combiner's merge of one row: the records of parts 0 .. live-1 in part
 // order, its own part's (`own`) from LDS and the others' polled from the
@@ -482,10 +488,16 @@ void kv4_decode_kernel(Kv4Params p)
     // This part's ticket of its (token, kv head, chunk): the last R ticket
     // holders combine. Its round trip overlaps the tile loads; the value is
     // first needed at the merge.
+    // The group's counter word: tickets count in its low 16 bits; an early
+    // combiner (role r < R - 1) registers by adding 1 << (16 + r). The word
+    // ends each call at `full`, and the atomic that makes it so resets it.
     uint32_t* counter = p.counters + ((size_t)token * p.H + kvh) * p.chunks + chunk;
-    uint32_t ticket = 0;
+    const uint32_t R = live_parts > 1 ? min(p.combiners, live_parts) : 1u;
+    const uint32_t full = live_parts | (((1u << (R - 1)) - 1u) << kRegShift);
+    uint32_t ticket_word = 0;
     if (live_parts > 1 && tid == 0)
-        ticket = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        ticket_word =
+            __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
     // ---- the query operand of head n16 for k group g: k-step ks covers the
     // dword d = 8g + ks of a key row, channels 4d + {0, 2, 128, 130, 1, 3, 129, 131}.
@@ -652,9 +664,22 @@ void kv4_decode_kernel(Kv4Params p)
         }
     }
 
+    // An early combiner (tickets live - R .. live - 2) registers now; the
+    // reply, read at the end of the merge, says whether every ticket had
+    // been taken, i.e. every part of the group had started. The merge's
+    // barriers are LDS-only, so the atomic stays in flight under it.
+    const uint32_t ticket = ticket_word & kTicketMask;
+    uint32_t reg_old = 0;
+    if (R > 1 && tid == 0 && ticket >= live_parts - R && ticket < live_parts - 1) {
+        const uint32_t reg = 1u << (kRegShift + ticket - (live_parts - R));
+        reg_old = __hip_atomic_fetch_add(counter, reg, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (reg_old + reg == full)
+            __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+
     // ---- this wave's (m, l, acc): acc = (64 acc' - 71.5 B) / prob_scale_last
     const float off = bsum * (kLevelUnit * kLevelOffset);
-    __syncthreads();  // every wave is past its q_lds reads
+    lds_barrier();  // every wave is past its q_lds reads
     float* mw = merge + wave * 16 * kRow + n16 * kRow;
 #pragma unroll
     for (int i = 0; i < 4; ++i)
@@ -673,26 +698,27 @@ void kv4_decode_kernel(Kv4Params p)
         ml[(wave * 16 + n16) * 2] = run_max;
         ml[(wave * 16 + n16) * 2 + 1] = run_sum;
     }
-    // R = min(p.combiners, live parts) combiners: the parts holding the last
-    // R tickets, role 0 .. R-1, combine the rows h = role (mod R). Every
-    // other live part of the group took its ticket earlier or takes one
-    // later: the host allows R > 1 only when the whole grid is resident,
-    // so a combiner waits only on running workgroups. The last ticket resets
-    // the counter for the next call.
-    const uint32_t R = live_parts > 1 ? min(p.combiners, live_parts) : 1u;
+    // Roles: the parts holding the last R tickets are combiners 0 .. R-1,
+    // combiner r owning the rows h = r (mod R). The last ticket (role R-1)
+    // also takes the rows of every early combiner whose registration came
+    // before it (the registrations its own ticket's reply holds).
     if (tid == 0) {
         int role = live_parts > 1 ? -1 : 0;
+        uint32_t mine = live_parts > 1 ? 0u : 1u;  // role classes this part combines
         if (live_parts > 1) {
             if (ticket >= live_parts - R) role = (int)(ticket - (live_parts - R));
-            if (ticket == live_parts - 1)
+            if (ticket_word + 1u == full)  // this ticket completes the word
                 __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (ticket == live_parts - 1)
+                mine = (1u << (R - 1)) | ((ticket_word >> kRegShift) & ((1u << (R - 1)) - 1u));
         }
         role_lds[0] = role;
+        role_lds[2] = (int)mine;
         // test hook: the first ticket's part withholds the records the other
         // combiners wait for
         role_lds[1] = p.withhold && live_parts > 1 && ticket == 0;
     }
-    __syncthreads();
+    lds_barrier();
 
     // ---- merge the four waves: thread -> head tid / 16, channels 4 (tid % 16)
     // + 64 q4 (consecutive lanes on consecutive float4s). The merged row
@@ -727,7 +753,7 @@ void kv4_decode_kernel(Kv4Params p)
         }
         if ((tid & 15) == 0) *(float2*)(mlo + 2 * h) = make_float2(M, L);
     }
-    __syncthreads();
+    lds_barrier();
     const int role = *role_lds;
 
     // ---- one live part: its rows finish from LDS (the merge of one record)
@@ -743,21 +769,45 @@ void kv4_decode_kernel(Kv4Params p)
         return;
     }
 
+    // An early combiner merges its rows only if every ticket had been taken
+    // when it registered; else it exports them too and leaves them to the
+    // last ticket holder. Decided before the exports: the registration's
+    // reply then waits behind no store.
+    uint32_t mine = (uint32_t)role_lds[2];
+    if (role >= 0 && role < (int)R - 1) {
+        if (tid == 0) role_lds[3] = (reg_old & kTicketMask) == live_parts ? (int)(1u << role) : 0;
+        lds_barrier();
+        mine = (uint32_t)role_lds[3];
+    }
+
     // ---- export the records of the rows other parts combine: encoded
-    // (bits ^ kRecMagic, never 0) with device-coherent stores
+    // (bits ^ kRecMagic, never 0) with device-coherent stores. Not exported:
+    // the rows this part combines (a record it stored for a row it combines
+    // would never be consumed and cleared).
     const bool withheld = role_lds[1] != 0;
     for (uint32_t hh = wave; hh < gc && !withheld; hh += kWaves) {
-        if (role >= 0 && hh % R == (uint32_t)role) continue;
+        if ((mine >> (hh % R)) & 1u) continue;
         const __amdgpu_buffer_rsrc_t rs =
             records_rsrc(p.records + (row0 + hh) * p.parts * kRecFloats);
         rec_store<4, true>(rs, part * kRecBytes + 16u * lane, merge + hh * kRow + 4 * lane);
         if (lane == 0) rec_store<2, true>(rs, part * kRecBytes + 4u * kD, mlo + 2 * hh);
     }
-    if (role < 0) return;
+    if (mine == 0) return;
 
-    // ---- combiner `role`: rows role, role + R, ..., one wave each
-    for (uint32_t i = wave; role + R * i < gc; i += kWaves) {
-        const uint32_t hh = role + R * i;
+    // ---- the rows of the role classes in `mine` (class c: rows c, c + R,
+    // ...), listed class by class; wave w takes rows w, w + 4, ... of the list
+    for (uint32_t k = wave;; k += kWaves) {
+        uint32_t hh = gc, rem = k;
+        for (uint32_t c = 0; c < R; ++c) {
+            if (!((mine >> c) & 1u)) continue;
+            const uint32_t cnt = c < gc ? (gc - c + R - 1) / R : 0u;
+            if (rem < cnt) {
+                hh = c + R * rem;
+                break;
+            }
+            rem -= cnt;
+        }
+        if (hh >= gc) break;
         float x[4], run_sum;
         combine_polled(p, row0 + hh, live_parts, part, merge + hh * kRow, mlo + 2 * hh, lane, x,
                        run_sum);
@@ -788,18 +838,10 @@ hipError_t launch_kv4_decode(hipStream_t stream, const Kv4Params& p)
     const uint32_t npages = ((kWaves * p.nt * kTile - 1) >> p.block_shift) + 2;
     const dim3 grid(p.parts, p.H * p.chunks, p.T);
     const size_t lds = kv4_lds_bytes(npages);
-    // Four combiners per group when every workgroup of the grid is resident
-    // at once (so a combiner never waits on one that has not started), else
-    // the last ticket alone.
+    // Four combiners per group on any grid: a combiner waits only for parts
+    // that hold a ticket (see the kernel's roles).
     Kv4Params q = p;
-    q.combiners = 1;
-    int dev = 0, cus = 0, per_cu = 0;
-    if (hipGetDevice(&dev) == hipSuccess &&
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kv4_decode_kernel, kThreads, lds) ==
-            hipSuccess &&
-        (uint64_t)grid.x * grid.y * grid.z <= (uint64_t)(cus > 0 ? cus : 0) * (per_cu > 0 ? per_cu : 0))
-        q.combiners = 4;
+    q.combiners = 4;
     hipLaunchKernelGGL(kv4_decode_kernel, grid, dim3(kThreads), lds, stream, q);
     return hipGetLastError();
 }

@@ -35,8 +35,8 @@ TQ4_DECODE_QUERY_ROTATED = 1
 TQ4_DECODE_PRECISE = 2  # partials only: FP32 recurrence, BF16 q_rot (reference rig budgets)
 TQ4_DECODE_TEST_POLL_BOUND = 1 << 30  # test hooks of the bounded wait (include/tq4.h)
 TQ4_DECODE_TEST_WITHHOLD = 1 << 31
-TQ4_KV4FP8_TEST_POLL_BOUND = 1
-TQ4_KV4FP8_TEST_WITHHOLD = 2
+TQ4_KV4FP8_TEST_POLL_BOUND = 1 << 30
+TQ4_KV4FP8_TEST_WITHHOLD = 1 << 31
 TQ4_MAX_SPLITS = 256
 
 _P = C.c_void_p

@@ -864,9 +864,9 @@ def extra_workloads(tq4, torch, dev, w, pmc, cpu=True):
     # more than the Infinity Cache, so each step reads its batch cold)
     bats = [Batch(tq4, torch, dev, 0x71340050 + k, w.signs) for k in range(2)]
     res = time_launches(torch, [b.step for b in bats], 32, 4, samples=16, chunk=8)
-    t_step = sum(tq4.decode_poll_timeouts(b.ws, 64, HKV) for b in bats)
+    t_step = sum(tq4.decode_poll_timeouts(b.ws, 64, HKV) for b in bats if b.ws is not None)
     resd = time_launches(torch, [b.decode for b in bats], 32, 4, samples=16, chunk=8)
-    t_step += sum(tq4.decode_poll_timeouts(b.ws, 64, HKV) for b in bats)
+    t_step += sum(tq4.decode_poll_timeouts(b.ws, 64, HKV) for b in bats if b.ws is not None)
     sbytes, dbytes = bats[0].step_bytes(), bats[0].decode_bytes()
     bsz = len(bats[0].ctxs)
     row = {"workload": "configs[4] 64 seqs ctx~U[512,8192]: scatter 64 tokens + split-K decode",

@@ -77,8 +77,8 @@ typedef struct tq4_kv4fp8_launch {
     uint32_t test_flags;
 } tq4_kv4fp8_launch;
 
-#define TQ4_KV4FP8_TEST_POLL_BOUND 1u
-#define TQ4_KV4FP8_TEST_WITHHOLD 2u
+#define TQ4_KV4FP8_TEST_POLL_BOUND (1u << 30)
+#define TQ4_KV4FP8_TEST_WITHHOLD (1u << 31)
 
 /* ascend_micro::fused_decode_opt::Buffers. query: FP32 [tokens][heads][256]
  * in the rotated basis; block_table int32 [tokens][max_blocks];

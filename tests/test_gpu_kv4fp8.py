@@ -214,13 +214,19 @@ def test_raw_query_zero_context_and_gate(tq4, oracle, element):
     assert mx <= 2e-2 and mr <= 1e-3, (mx, mr)
 
 
-def test_grid_beyond_resident_workgroups(tq4, oracle):
-    """75 tokens x 4 KV heads x 2 parts = 600 workgroups, more than two per
-    CU: one combiner per group (the last ticket), which waits only on parts
-    that are already running. Two calls on one workspace agree bit for bit."""
-    rng = np.random.default_rng(31)
-    T, H, G, S = 75, 4, 16, 64
-    ctx = [int(c) for c in rng.integers(300, 1500, T)]
+@pytest.mark.parametrize("case", ["two_parts", "many_parts"])
+def test_grid_beyond_resident_workgroups(tq4, oracle, case):
+    """Grids beyond the resident workgroups: 75 tokens x 4 KV heads x 2 parts
+    (600 workgroups), and 96 tokens x 4 KV heads with up to 8 live parts
+    (about 2000 workgroups), so groups have four combiners and an early
+    combiner can finish before its group's last ticket holder has started:
+    it then hands its rows to the last ticket, and no combiner waits on a
+    part that has not started. Two calls on one workspace agree bit for bit
+    and leave the whole workspace zero."""
+    rng = np.random.default_rng(31 if case == "two_parts" else 32)
+    T, H, G, S = (75, 4, 16, 64) if case == "two_parts" else (96, 4, 16, 64)
+    lo, hi = (300, 1500) if case == "two_parts" else (2000, 8192)
+    ctx = [int(c) for c in rng.integers(lo, hi, T)]
     P = sum((c + S - 1) // S for c in ctx) + 4
     q, key, val, sc, tb, ln = random_case(rng, T, H, G, S, P, ctx, key_scale=(0.5, 2.0))
     kw = dict(heads=H * G, kv_heads=H, block_size=S, max_blocks=tb.shape[1], num_blocks=P)
