@@ -360,7 +360,7 @@ int tq4_paged_decode_noalloc(void* stream, const uint16_t* q, const int8_t* key_
         if (tq4_decode_workspace_bytes(num_seqs, num_heads, num_kv_heads, head_size,
                                        num_splits) > tq4::kNoAllocScratchBytes)
             return TQ4_ERR_SCRATCH;
-        if (tq4::noalloc_scratch((hipStream_t)stream, &ws) != hipSuccess) return TQ4_ERR_LAUNCH;
+        if (tq4::noalloc_scratch(&ws) != hipSuccess) return TQ4_ERR_LAUNCH;
     }
     // The whole scratch is the workspace: its tail (queue, timeout word,
     // tickets) sits at the end whatever the geometry, and between calls
@@ -371,6 +371,26 @@ int tq4_paged_decode_noalloc(void* stream, const uint16_t* q, const int8_t* key_
                             out, num_seqs, num_heads, num_kv_heads, head_size, block_size,
                             num_blocks, max_blocks_per_seq, num_splits, scale, inv_sqrt_len,
                             output_stage, flags);
+}
+
+int tq4_paged_decode_noalloc_poll_timeouts(void* stream, uint32_t num_seqs,
+                                           uint32_t num_kv_heads, uint32_t* count)
+{
+    if (!count) return TQ4_ERR_NULL_POINTER;
+    if (num_seqs == 0 || num_kv_heads == 0) return TQ4_ERR_GEOMETRY;
+    if (ticket_bytes(num_seqs, num_kv_heads) + kQueueBytes > tq4::kNoAllocScratchBytes)
+        return TQ4_ERR_SCRATCH;
+    void* ws = nullptr;
+    if (tq4::noalloc_scratch(&ws) != hipSuccess) return TQ4_ERR_LAUNCH;
+    return tq4_decode_poll_timeouts(stream, ws, tq4::kNoAllocScratchBytes, num_seqs, num_kv_heads,
+                                    count);
+}
+
+int tq4_paged_decode_noalloc_reset(void* stream)
+{
+    void* ws = nullptr;
+    if (tq4::noalloc_scratch(&ws) != hipSuccess) return TQ4_ERR_LAUNCH;
+    return launched(tq4::launch_fill_zero((hipStream_t)stream, ws, tq4::kNoAllocScratchBytes));
 }
 
 int tq4_paged_decode_partials(void* stream, const uint16_t* q, const int8_t* key_cache,

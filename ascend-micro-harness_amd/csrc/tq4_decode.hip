@@ -1489,10 +1489,12 @@ hipError_t launch_combine(hipStream_t stream, const DecodeParams& p)
 }
 
 // The no-allocation decode's workspace: a static device array, one copy per
-// GPU the library runs on, held until the process ends. In host code its
-// name is only a stand-in; its device address comes from
-// hipGetSymbolAddress, once per device, and only that address is handed to
-// kernels and fills.
+// GPU the library runs on, held until the process ends. It is zero when the
+// code object is loaded (a zero-filled segment) and every decode leaves the
+// words it used zero again; after a poll give-up the caller re-zeroes it
+// with tq4_paged_decode_noalloc_reset. In host code its name is only a
+// stand-in; its device address comes from hipGetSymbolAddress, once per
+// device, and only that address is handed to kernels and fills.
 static __device__ __align__(256) uint32_t scratch[kNoAllocScratchBytes / sizeof(uint32_t)];
 
 namespace {
@@ -1501,7 +1503,7 @@ std::mutex g_scratch_mutex;
 void* g_scratch_ptr[kMaxDevices] = {};
 }  // namespace
 
-hipError_t noalloc_scratch(hipStream_t stream, void** ptr)
+hipError_t noalloc_scratch(void** ptr)
 {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
@@ -1509,14 +1511,12 @@ hipError_t noalloc_scratch(hipStream_t stream, void** ptr)
     if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
     std::lock_guard<std::mutex> lock(g_scratch_mutex);
     if (g_scratch_ptr[dev] == nullptr) {
+        // no fill here: the array is zero at load, and a fill made at a first
+        // call under graph capture would become a node of that graph
         void* p = nullptr;
         e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
         if (e != hipSuccess) return e;
         if (p == nullptr) return hipErrorInvalidSymbol;
-        // the decode's tickets, queue and records start at zero; every call
-        // leaves them zero again (a fill kernel: it may be captured)
-        e = launch_fill_zero(stream, p, kNoAllocScratchBytes);
-        if (e != hipSuccess) return e;
         g_scratch_ptr[dev] = p;
     }
     *ptr = g_scratch_ptr[dev];

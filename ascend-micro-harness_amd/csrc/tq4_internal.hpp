@@ -104,9 +104,9 @@ constexpr uint32_t kTicketStride = 32;
 constexpr uint32_t kSubQueues = 4;
 
 // The no-allocation decode's static scratch (tq4_decode.hip): its size, and
-// its device address on the current device (set up, and zeroed on `stream`,
-// at the first call on each device).
+// its device address on the current device (looked up at the first call on
+// each device; the array is zero at load).
 constexpr size_t kNoAllocScratchBytes = (size_t)16 << 20;
-hipError_t noalloc_scratch(hipStream_t stream, void** ptr);
+hipError_t noalloc_scratch(void** ptr);
 
 }  // namespace tq4

@@ -89,6 +89,10 @@ def lib():
     L.tq4_paged_decode.argtypes = [_P] * 10 + [_SZ, _P] + [_U32] * 8 + [_F32, _F32, _U32, _U32]
     L.tq4_paged_decode_noalloc.restype = _I32
     L.tq4_paged_decode_noalloc.argtypes = [_P] * 10 + [_U32] * 8 + [_F32, _F32, _U32, _U32]
+    L.tq4_paged_decode_noalloc_poll_timeouts.restype = _I32
+    L.tq4_paged_decode_noalloc_poll_timeouts.argtypes = [_P, _U32, _U32, _P]
+    L.tq4_paged_decode_noalloc_reset.restype = _I32
+    L.tq4_paged_decode_noalloc_reset.argtypes = [_P]
     L.tq4_paged_decode_partials.restype = _I32
     L.tq4_paged_decode_partials.argtypes = [_P] * 9 + [_SZ] + [_U32] * 8 + [_F32, _F32, _U32]
     L.tq4_splitk_combine.restype = _I32
@@ -404,6 +408,22 @@ def paged_decode_noalloc(q, key_cache, value_cache, scale_cache, block_tables, c
     return out
 
 
+def paged_decode_noalloc_poll_timeouts(num_seqs, num_kv_heads, stream=None):
+    """The no-allocation decode's sticky poll-timeout count for the geometry
+    of its last call (tq4_paged_decode_noalloc_poll_timeouts). Nonzero: call
+    paged_decode_noalloc_reset before the next no-allocation call.
+    Synchronises the stream."""
+    return _read_count(lambda dst: lib().tq4_paged_decode_noalloc_poll_timeouts(
+        _stream(stream), num_seqs, num_kv_heads, dst), "paged_decode_noalloc_poll_timeouts",
+        stream)
+
+
+def paged_decode_noalloc_reset(stream=None):
+    """Zero the no-allocation decode's static scratch on this device
+    (tq4_paged_decode_noalloc_reset: one fill kernel, nothing allocated)."""
+    _check(lib().tq4_paged_decode_noalloc_reset(_stream(stream)), "paged_decode_noalloc_reset")
+
+
 def paged_decode_partials(q, key_cache, value_cache, scale_cache, block_tables, context_lens,
                           pi_signs, num_kv_heads, block_size, num_blocks, num_splits,
                           workspace=None, scale=None, inv_sqrt_len=None, flags=0, stream=None):
@@ -556,7 +576,8 @@ __all__ = [
     "TQ4Error", "lib", "status_string", "reshape_and_cache_a8", "reshape_and_cache_bf16",
     "reshape_scatter", "decode_workspace_bytes", "auto_splits", "decode_workspace",
     "paged_decode", "paged_decode_partials", "splitk_combine", "icdf_quantize",
-    "decode_workspace_init", "paged_decode_noalloc", "rms_reshape_and_cache", "rms_dequantize",
+    "decode_workspace_init", "paged_decode_noalloc", "paged_decode_noalloc_poll_timeouts",
+    "paged_decode_noalloc_reset", "rms_reshape_and_cache", "rms_dequantize",
     "rms_scale_slot_floats",
     "lloydmax_quantize", "TQ4_DECODE_QUERY_ROTATED", "TQ4_MAX_SPLITS",
     "Kv4Fp8Launch", "Kv4Fp8Buffers", "Kv4Fp8RawQueryBuffers", "fused_decode_opt_launch",

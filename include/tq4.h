@@ -223,16 +223,20 @@ int tq4_paged_decode(void* stream, const uint16_t* q, const int8_t* key_cache,
  * allocate (code under HIP graph capture, tight serving loops, harnesses
  * that forbid hipMalloc). No counterpart in the reference. Same arguments and
  * result as tq4_paged_decode; the workspace is a static 16 MiB device array
- * inside libtq4.so, one per GPU, held until the process ends (set up and
- * zeroed on `stream` at the first call on each device; no allocation ever).
+ * inside libtq4.so, one per GPU, held until the process ends (zero when the
+ * library's code object is loaded; its address is looked up at the first
+ * call on each device, which launches nothing, so that call may be made
+ * under graph capture; no allocation ever).
  * A call whose workspace (tq4_decode_workspace_bytes) exceeds 16 MiB is
  * refused with TQ4_ERR_SCRATCH (e.g. 64 sequences x 32 q heads at d = 128 fit
  * up to 15 splits). Every call on one GPU shares that array: calls that
  * overlap in time on one GPU (two streams, two threads) race and must be
- * serialised by the caller. The test hooks are refused (TQ4_ERR_FLAGS), and
- * the poll-timeout count is not reported: a combiner waits only for
- * workgroups that are already running, so a give-up (2^20 polls) would mean
- * a stalled device; callers that need that report use tq4_paged_decode. */
+ * serialised by the caller. The test hooks are refused (TQ4_ERR_FLAGS). A
+ * combiner waits only for workgroups that are already running, so a poll
+ * give-up (2^20 polls) means a stalled device; it is counted in the scratch
+ * (tq4_paged_decode_noalloc_poll_timeouts) and leaves late records and the
+ * count behind, which later calls of any geometry would read: after a
+ * nonzero count, call tq4_paged_decode_noalloc_reset before the next call. */
 int tq4_paged_decode_noalloc(void* stream, const uint16_t* q, const int8_t* key_cache,
                              const int8_t* value_cache, const float* scale_cache,
                              const int32_t* block_tables, const int32_t* context_lens,
@@ -241,6 +245,20 @@ int tq4_paged_decode_noalloc(void* stream, const uint16_t* q, const int8_t* key_
                              uint32_t head_size, uint32_t block_size, uint32_t num_blocks,
                              uint32_t max_blocks_per_seq, uint32_t num_splits, float scale,
                              float inv_sqrt_len, uint32_t output_stage, uint32_t flags);
+
+/* The no-allocation decode's sticky poll-timeout count for the geometry of
+ * its last call (num_seqs, num_kv_heads locate the count in the scratch), as
+ * tq4_decode_poll_timeouts reads it (asynchronous on `stream`; `count` is a
+ * host or device pointer). Allocates nothing. No counterpart in the
+ * reference (it reports its watchdog the same way: README.md:65-76). */
+int tq4_paged_decode_noalloc_poll_timeouts(void* stream, uint32_t num_seqs,
+                                           uint32_t num_kv_heads, uint32_t* count);
+
+/* Zero the whole no-allocation scratch of the current device (one fill
+ * kernel on `stream`; allocates nothing): after a poll give-up, before the
+ * next tq4_paged_decode_noalloc call. Calls on other streams must not
+ * overlap it. No counterpart in the reference. */
+int tq4_paged_decode_noalloc_reset(void* stream);
 
 /* Partials only: workspace record (seq, q head, split) at float offset
  * ((seq*num_heads + head)*num_splits + split)*(head_size + 4) holds

@@ -226,3 +226,8 @@ def test_noalloc_refusals_before_any_hip_call(lib):
     assert call(1, 4, 2) == -12                      # nor the partials' precise mode
     assert call(1, 300) == -5                        # splits
     assert lib.tq4_status_string(-13) != b"unknown status"
+    cnt = C.c_uint32(0)
+    to = lib.tq4_paged_decode_noalloc_poll_timeouts
+    assert to(None, 1, 8, None) == -1                   # no count pointer
+    assert to(None, 0, 8, C.byref(cnt)) == -3           # no sequences
+    assert to(None, 1 << 20, 8, C.byref(cnt)) == -13    # a tail beyond the scratch

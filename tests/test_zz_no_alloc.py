@@ -53,6 +53,39 @@ def run_both(tq4, oracle, case, K, label):
     return got
 
 
+def test_noalloc_first_call_under_graph_capture(tq4, oracle):
+    """The process's first no-allocation call is made while a HIP graph is
+    being captured: it launches nothing of its own (no set-up fill enters the
+    graph), and every replay matches the workspace entry bit for bit, with
+    eager no-allocation calls and synchronisations between the replays. The
+    scratch's timeout count stays zero; a reset, then a call, still agrees."""
+    case = make_case(oracle, 4, [2048 + 5, 700])
+    q, kc, vc, sc, tables, ctx, signs = case["d"]
+    kw = dict(num_splits=8, inv_sqrt_len=float(case["isl"]))
+    ws = tq4.decode_workspace(2, HQ, H, D, 8)
+    ref = host(tq4.paged_decode(q, kc, vc, sc, tables, ctx, signs, H, S, case["P"], workspace=ws,
+                                **kw)).copy()
+    out = torch.empty_like(q)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    print("noalloc: first call inside a graph capture", flush=True)
+    with torch.cuda.graph(g):
+        tq4.paged_decode_noalloc(q, kc, vc, sc, tables, ctx, signs, H, S, case["P"], out, **kw)
+    for i in range(3):
+        out.zero_()
+        g.replay()
+        assert np.array_equal(host(out), ref), f"replay {i}"
+        tq4.paged_decode_noalloc(q, kc, vc, sc, tables, ctx, signs, H, S, case["P"], out, **kw)
+        assert np.array_equal(host(out), ref), f"eager call {i}"
+    assert tq4.paged_decode_noalloc_poll_timeouts(2, H) == 0
+    tq4.paged_decode_noalloc_reset()
+    out.zero_()
+    tq4.paged_decode_noalloc(q, kc, vc, sc, tables, ctx, signs, H, S, case["P"], out, **kw)
+    assert np.array_equal(host(out), ref), "after a reset"
+
+
 def test_noalloc_matches_workspace_entry_on_shrinking_calls(tq4, oracle):
     rng = np.random.default_rng(0xA110C)
     big = make_case(oracle, 1, [int(x) for x in rng.integers(200, 1500, 64)])
