@@ -94,3 +94,65 @@ def test_written_rows_decode_to_their_centroids(tq4, oracle):
     want = np.stack([lv & 15, lv >> 4], axis=-1).reshape(-1, 128)
     cents = np.array([oracle.lib.tq4o_rms_centroid(q) for q in range(16)], np.float32)
     assert np.array_equal(dec, cents[want])
+
+
+@pytest.mark.parametrize("d", [64, 256])
+def test_scale_closed_form_in_any_summation_order(tq4, oracle, d):
+    """The reference sums the squares with AscendC ReduceSum, in an order this
+    writer does not restate; for general data the scale's last bits depend on
+    it, so its parity with the reference is unpinned there. Here every sum is
+    exact in any order, which pins the scale bits independently of it: rows
+    a*e_j and a*e_j + b*e_k (one- and two-hot, BF16), inv_sqrt_len = 1/8.
+    Pi x = s . H (s . x) / 8 then has entries +-a/8 (or +-(a +- b)/8), whose
+    squares and every partial sum of them are exact in FP32, and d is a
+    perfect square, so sqrt is exact too: scale = sqrt(sum y^2) / 8 + 1e-20
+    with a single rounding, for both planes, on the GPU and in the oracle."""
+    rng = np.random.default_rng(0x5C + d)
+    H, S, P = 2, 16, 4
+    T = 24
+    key = np.zeros((T, H, d), np.float32)
+    val = np.zeros((T, H, d), np.float32)
+    for t in range(T):
+        for h in range(H):
+            for x in (key, val):
+                a = float(rng.choice([1.0, 1.5, 3.0, 0.25, 96.0, 2.0 ** -10]))
+                j = rng.integers(d)
+                x[t, h, j] = a * rng.choice([-1, 1])
+                if t % 2:  # two-hot
+                    k = (j + 1 + rng.integers(d - 1)) % d
+                    x[t, h, k] = float(rng.choice([0.5, 2.0, 5.0])) * a * rng.choice([-1, 1])
+    kb, vb = f32_to_bf16(key), f32_to_bf16(val)
+    signs = np.where(rng.random(d) < 0.5, -1.0, 1.0).astype(np.float32)
+    isl = np.float32(0.125)
+    slots = rng.permutation(P * S)[:T].astype(np.int32)
+    ssf = tq4.rms_scale_slot_floats(H)
+    nb = P * S * H * d // 2
+    kc, vc, sc = canary_bytes(nb), canary_bytes(nb), canary_floats(P * S * ssf)
+    o = [kc.copy(), vc.copy(), sc.copy()]
+    oracle.rms_reshape_and_cache(1, kb, vb, o[0], o[1], o[2], slots, signs, H, d, S, P, T, isl)
+    g = [dev(kc), dev(vc), dev(sc)]
+    kt = torch.from_numpy(kb.view(np.int16)).cuda().view(torch.bfloat16)
+    vt = torch.from_numpy(vb.view(np.int16)).cuda().view(torch.bfloat16)
+    tq4.rms_reshape_and_cache(kt, vt, *g, dev(slots), dev(signs), num_blocks=P, block_size=S,
+                              inv_sqrt_len=float(isl))
+    got = [host(x) for x in g]
+    for a, b, name in zip(got, o, ("key", "value", "scale")):
+        assert np.array_equal(a.view(np.uint8), b.view(np.uint8)), name
+    hd = hadamard(d)
+    for t in range(T):
+        rec = got[2][slots[t] * ssf: slots[t] * ssf + 2 * H]
+        for plane in range(2 * H):
+            x = (kb if plane < H else vb)[t, plane % H].astype(np.uint32) << 16
+            x = x.view(np.float32).astype(np.float64)
+            y = signs * (hd @ (signs * x)) * 0.125
+            ss = float(np.sum(y * y))
+            assert ss == float(np.float32(ss)), "the sum of squares is exact in FP32"
+            want = np.float32(np.float32(np.sqrt(ss)) * np.float32(0.125)) + np.float32(1e-20)
+            assert rec[plane].view(np.uint32) == np.float32(want).view(np.uint32), (t, plane)
+
+
+def hadamard(n):
+    h = np.array([[1.0]])
+    while h.shape[0] < n:
+        h = np.block([[h, h], [h, -h]])
+    return h

@@ -65,6 +65,32 @@ def test_scale_closed_form_and_zero_row(oracle, n):
     assert np.float32(oracle.lib.tq4o_rms_scale(z.ctypes.data, n, isl)) == np.float32(1e-20)
 
 
+@pytest.mark.parametrize("n", [64, 256])
+def test_scale_exact_sums_pin_the_bits_in_any_order(oracle, n):
+    """Rows whose rotation has entries +-a/8 or +-(a +- b)/8 (one- and two-hot
+    x, inv_sqrt_len = 1/8): every square and partial sum is exact in FP32 and
+    sqrt is exact (n a perfect square), so the scale's bits are fixed whatever
+    the summation order -- the reference's ReduceSum order included."""
+    rng = np.random.default_rng(7 + n)
+    h = hadamard(n)
+    for trial in range(200):
+        x = np.zeros(n)
+        a = rng.choice([1.0, 1.5, 3.0, 0.25, 96.0, 2.0 ** -10])
+        j = rng.integers(n)
+        x[j] = a
+        if trial % 2:
+            x[(j + 1 + rng.integers(n - 1)) % n] = rng.choice([0.5, 2.0, 5.0]) * a * rng.choice([-1, 1])
+        s = np.where(rng.random(n) < 0.5, -1.0, 1.0)
+        y = (s * (h @ (s * x)) * 0.125).astype(np.float32)
+        ss = float(np.sum(y.astype(np.float64) ** 2))
+        assert ss == float(np.float32(ss))
+        got = np.float32(oracle.lib.tq4o_rms_scale(y.ctypes.data, n, np.float32(0.125)))
+        want = np.float32(np.float32(np.sqrt(ss)) * np.float32(0.125)) + np.float32(1e-20)
+        assert got == want, (trial, got, want)
+        # and a shuffled order of the same squares gives the same sum
+        assert float(np.sum(rng.permutation(y.astype(np.float64) ** 2))) == ss
+
+
 def test_tables_are_the_pinned_lloydmax_codebook(oracle):
     from test_oracle_codebook import load
     f = load("cb_lloyd_b4")  # the reference's lloyd:: fixture
