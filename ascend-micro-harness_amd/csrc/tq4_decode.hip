@@ -84,7 +84,7 @@ constexpr float kXLimit = 32768.0f;      // a normalised product at or above thi
 constexpr int kMassLimit = 100;          // log2 bound of a row's normalised mass after a rescale
 constexpr uint32_t kBadStrip = 0xFFFFFFFFu;
 constexpr uint32_t kFlagRotated = 1u;
-constexpr int kHdrFloats = 480;          // m_x, l_x [16][4], q_exp[16], flags, wave flags[4], scale slots [4][64], 2^-sh [16][4]
+constexpr int kHdrFloats = 544;          // m_x, l_x [16][4], q_exp[16], flags, wave flags[4], scale slots [4][64], 2^-sh [16][4], exact maxima [16][4]
 constexpr uint32_t kPersistentMaxSeqs = 4096; // the persistent kernel stages two words per sequence
 constexpr uint32_t kLptMaxSeqs = 1024;        // and a third (the last-split order) up to this many
 constexpr int kStripSlots = TQ4_MAX_SPLIT_STRIPS + 4;  // staged window rows + padding
@@ -425,6 +425,7 @@ struct RowState {
     f4_t acc[D / 16];
     f4_t cr;       // offset column: 1.125 * sum P'vs per row
     float m_used;  // the row maximum in use (log2 units)
+    float smax;    // partials only: this lane's exact maximum score (log2 units)
     float sh, mo, lpart, thr;
     bool virgin;   // no rescale yet in this stream (wave-uniform)
 
@@ -437,6 +438,7 @@ struct RowState {
         // row starts with a finite mo (t = s exactly) and thr = -inf, so its
         // first pair holding a live token always rescales.
         m_used = row_live ? -INFINITY : INFINITY;
+        smax = -INFINITY;
         sh = 0.0f;
         mo = row_live ? 0.0f : INFINITY;
         lpart = 0.0f;
@@ -460,8 +462,10 @@ struct QOps {
 // pair holds dead tokens -- those at or past live_rel tokens from the pair's
 // start, and every token of this lane's value strip when strip_ok is false;
 // a dead token is overwritten (score -inf, value scale 0), never multiplied
-// (its payload may be NaN).
-template <int D>
+// (its payload may be NaN). EXACT (the partials entry): also track the exact
+// maximum score, which the exported record's m must be (the lazy maximum
+// may sit up to kTau below it).
+template <int D, bool EXACT = false>
 __device__ __forceinline__ void process_pair(RowState<D>& st, const QOps<D>& qo,
                                              const PairRegs<D>& r, float* sc_wave, int lane,
                                              bool masked, uint32_t live_rel, bool strip_ok)
@@ -513,6 +517,7 @@ __device__ __forceinline__ void process_pair(RowState<D>& st, const QOps<D>& qo,
         tmax = fmaxf(tmax, sc8[i]);
         vmax = fmaxf(vmax, vs[i]);
     }
+    if constexpr (EXACT) st.smax = fmaxf(st.smax, tmax);
     tmax -= st.mo;  // a live row's mo is finite; a padded row's is +inf
     if (__builtin_expect(
             __any(tmax > st.thr || __builtin_amdgcn_exp2f(tmax) * vmax >= kXLimit), 0)) {
@@ -684,16 +689,21 @@ __device__ __forceinline__ void build_qops(QOps<D>& qo, const float* q_st, const
 }
 
 // Park one wave's rows for the merge: (m, l, 2^-sh) per row at [row][wave]
-// (one 16-byte read gives a row's four waves) and the raw rows (offset
-// column removed) at part [wave][G][D].
-template <int D>
+// (one 16-byte read gives a row's four waves), with EXACT the row's exact
+// maximum score at t_x, and the raw rows (offset column removed) at part
+// [wave][G][D].
+template <int D, bool EXACT>
 __device__ __forceinline__ void park_rows(const RowState<D>& st, bool row_live, float* m_x,
-                                          float* l_x, float* u_x, float* part, uint32_t G,
-                                          int wave, int lane)
+                                          float* l_x, float* u_x, float* t_x, float* part,
+                                          uint32_t G, int wave, int lane)
 {
     constexpr int NB = D / 16;
     const int n = lane & 15, g4 = lane >> 4;
     const float lsum = col_sum(st.lpart);
+    if constexpr (EXACT) {
+        const float tm = col_max(st.smax);
+        if (g4 == 0) t_x[n * kWaves + wave] = row_live ? tm : -INFINITY;
+    }
     if (g4 == 0) {
         m_x[n * kWaves + wave] = row_live ? st.m_used : -INFINITY;
         l_x[n * kWaves + wave] = lsum;
@@ -726,13 +736,14 @@ __device__ __forceinline__ void finish_item(const DecodeParams& p, uint32_t seq,
     float* l_x = smem + 64;          // [16][4]
     int* flag = (int*)(smem + 144);  // the combiner / withheld-record flags
     float* u_x = smem + 416;         // [16][4] (row, wave) 2^-sh
+    float* t_x = smem + 480;         // [16][4] (row, wave) exact maximum (partials)
     const int tid = fresh_tid(), lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     // ---- merge the four waves. Each parks its raw rows (offset column
     // removed) and (m, l, 2^-sh) in LDS; then every output float4 combines
     // the four copies with the row's common maximum.
     float* part = region + G * kQRow<D>;  // [kWaves][G][D], past the q staging rows
-    park_rows<D>(st, row_live, m_x, l_x, u_x, part, G, wave, lane);
+    park_rows<D, MODE == 0>(st, row_live, m_x, l_x, u_x, t_x, part, G, wave, lane);
     if constexpr (MODE == 1) {
         if (p.K > 1 && tid == 0) {
             // The last ticket combines; every live split of this (seq, kv
@@ -757,6 +768,12 @@ __device__ __forceinline__ void finish_item(const DecodeParams& p, uint32_t seq,
         const float lw[kWaves] = {l4.x, l4.y, l4.z, l4.w};
         const float uw[kWaves] = {u4.x, u4.y, u4.z, u4.w};
         M = fmaxf(fmaxf(mw[0], mw[1]), fmaxf(mw[2], mw[3]));
+        if constexpr (MODE == 0) {
+            // the record's m is the row's exact running maximum, as the
+            // contract has it: every wave's weight moves down to it
+            const float4 t4 = *(const float4*)(t_x + r * kWaves);
+            M = fmaxf(fmaxf(t4.x, t4.y), fmaxf(t4.z, t4.w));
+        }
         L = 0.0f;
 #pragma unroll
         for (int w = 0; w < kWaves; ++w) {
@@ -1114,7 +1131,7 @@ __device__ __forceinline__ void decode_item(const DecodeParams& p, const uint32_
     auto process = [&](const PairRegs<D>& r, uint32_t gp, bool masked) {
         bool ok = true;
         if (masked) ok = strip_lds[min(2 * gp + sp, nws - 1)] != kBadStrip;
-        process_pair<D>(st, qo, r, sc_wave, lane, masked, ltok - 32 * gp, ok);
+        process_pair<D, MODE == 0>(st, qo, r, sc_wave, lane, masked, ltok - 32 * gp, ok);
     };
 
     // ---- the three-deep (two-deep at d = 256) register ring: full pairs,
