@@ -61,6 +61,31 @@
 #include "tq4_internal.hpp"
 
 namespace tq4 {
+
+// Phase stamps of the measurement build (make stamps: libtq4_stamps.so,
+// bench.py --phases): thread 0 of workgroup b < kStampBlocks writes the
+// 100 MHz realtime counter to slot [b][i] at each phase boundary -- 0 start,
+// 1 phase-0 loads retired, 2 first strip pairs issued, 3 q operands built,
+// 4 wave 0's strip loop done, 5 waves merged, 6 record exported (a split
+// that does not combine), 7 first row combined (poll complete + merge), 8
+// egress done (the combiner); slots a workgroup does not reach are 0. The
+// product library is built without them.
+#ifdef TQ4_DECODE_STAMPS
+constexpr int kStampBlocks = 4096;
+constexpr int kStampSlots = 16;
+__device__ uint64_t g_decode_stamps[kStampBlocks * kStampSlots];
+#define TQ4_STAMP(i, v)                                                                \
+    do {                                                                               \
+        if (threadIdx.x == 0 && blockIdx.x < kStampBlocks)                             \
+            g_decode_stamps[blockIdx.x * kStampSlots + (i)] = (v);                     \
+    } while (0)
+#else
+#define TQ4_STAMP(i, v) \
+    do {                \
+    } while (0)
+#endif
+#define TQ4_NOW __builtin_amdgcn_s_memrealtime()
+
 namespace {
 
 typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
@@ -758,6 +783,10 @@ __device__ __forceinline__ void finish_item(const DecodeParams& p, uint32_t seq,
         }
     }
     lds_barrier();
+    TQ4_STAMP(5, TQ4_NOW);
+    TQ4_STAMP(6, 0);
+    TQ4_STAMP(7, 0);
+    TQ4_STAMP(8, 0);
     // Per-wave weights of row r (exp2(m_w - M) * 2^-sh_w), the row's M and L;
     // branch-free: a wave with no live token gets exp2(-inf) = 0.
     auto row_weights = [&](uint32_t r, float (&f)[kWaves], float& M, float& L) {
@@ -842,6 +871,7 @@ __device__ __forceinline__ void finish_item(const DecodeParams& p, uint32_t seq,
                     rec_store<4, true>(rsrc, r * row_bytes, h);
                 }
             }
+            TQ4_STAMP(6, TQ4_NOW);
             if (!combiner) return;
         }
         if (!local) {
@@ -887,8 +917,10 @@ __device__ __forceinline__ void finish_item(const DecodeParams& p, uint32_t seq,
                 else
                     combine_records<D, true, 8>(p.records + qh * p.K * RS, k_live, lane, v, ~0u,
                                                 none, p.poll_limit, p.timeouts);
+                if (g == 0) TQ4_STAMP(7, TQ4_NOW);
                 egress_row<D>(v, es, gt, p.out + qh * D, p.inv_sqrt_len, p.output_stage, lane);
             }
+            TQ4_STAMP(8, TQ4_NOW);
             return;
         }
         if (p.output_stage >= 1) load_lane_floats<D>(p.pi_signs, lane, es);
@@ -950,6 +982,7 @@ __device__ __forceinline__ void decode_item(const DecodeParams& p, const uint32_
     // ---- phase 0: every small load -- context length, q rows, rotation
     // signs, the split's block-table window -- is issued before any strip
     // load and retired together.
+    TQ4_STAMP(0, TQ4_NOW);
     const int32_t ctx_raw = p.context_lens[seq];
     const bool rotate = !(p.flags & kFlagRotated);
     uint16_t qraw[4][CPL];
@@ -1044,6 +1077,7 @@ __device__ __forceinline__ void decode_item(const DecodeParams& p, const uint32_
     // lgkmcnt left at their maxima) keeps the compiler's wait analysis from
     // later waiting on them -- and so on the strip loads queued after them.
     __builtin_amdgcn_s_waitcnt(0x0F70);
+    TQ4_STAMP(1, TQ4_NOW);
     const uint32_t np_total = (ltok + 2 * kStrip - 1) / (2 * kStrip);
     const uint32_t np_full = bad ? 0u : ltok / (2 * kStrip);
     const uint32_t nws = pc * spp;  // strips in the window
@@ -1099,6 +1133,7 @@ __device__ __forceinline__ void decode_item(const DecodeParams& p, const uint32_
         fetch(b0, gp_of(0), false);
         if constexpr (NBUF == 3) fetch(b1, gp_of(1), false);
     }
+    TQ4_STAMP(2, TQ4_NOW);
     // Fused entry: this split's ticket, and the caller's atomics (the
     // persistent kernel's queue fetch), issued only now: atomics on one
     // counter queue behind each other (about 50 ns per earlier one), and a
@@ -1122,6 +1157,7 @@ __device__ __forceinline__ void decode_item(const DecodeParams& p, const uint32_
     lds_barrier();
     QOps<D> qo;
     build_qops<D>(qo, q_st, q_exp, G, lane);
+    TQ4_STAMP(3, TQ4_NOW);
     // The merge rows lie past q_st, so a wave without pairs may park its
     // rows while the others still read q here; q_st is next written by the
     // next item's prologue, behind the item's closing barriers.
@@ -1189,6 +1225,7 @@ __device__ __forceinline__ void decode_item(const DecodeParams& p, const uint32_
         }
     }
 
+    TQ4_STAMP(4, TQ4_NOW);
     finish_item<D, MODE, OWN>(p, seq, kvh, split, k_live, ticket, st, qo.row_live, region);
 }
 
@@ -1539,6 +1576,18 @@ hipError_t noalloc_scratch(void** ptr)
     *ptr = g_scratch_ptr[dev];
     return hipSuccess;
 }
+
+#ifdef TQ4_DECODE_STAMPS
+// The measurement build's stamp readout (declared only by its users).
+extern "C" int tq4_decode_stamps(void* dst, size_t bytes)
+{
+    const size_t all = sizeof(uint64_t) * kStampBlocks * kStampSlots;
+    return hipMemcpyFromSymbol(dst, HIP_SYMBOL(g_decode_stamps), bytes < all ? bytes : all, 0,
+                               hipMemcpyDeviceToHost) == hipSuccess
+               ? 0
+               : -1;
+}
+#endif
 
 hipError_t launch_fill_zero(hipStream_t stream, void* ptr, size_t bytes)
 {

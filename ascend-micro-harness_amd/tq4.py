@@ -29,7 +29,8 @@ import os
 import torch  # noqa: F401  (loads torch's HIP runtime first; libtq4 binds to it)
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libtq4.so")
+# TQ4_LIBRARY=libtq4_stamps.so selects the measurement build (bench.py --phases)
+LIB_PATH = os.path.join(_HERE, os.environ.get("TQ4_LIBRARY", "libtq4.so"))
 
 TQ4_DECODE_QUERY_ROTATED = 1
 TQ4_DECODE_PRECISE = 2  # partials only: FP32 recurrence, BF16 q_rot (reference rig budgets)

@@ -562,6 +562,10 @@ def main():
     ap.add_argument("--pmc-run", action="store_true",
                     help="the profiled kernels' workloads plus a plain copy of known size, "
                          "for rocprofv3 --pmc")
+    ap.add_argument("--phases", action="store_true",
+                    help="configs[2] per-phase timeline from the measurement build's in-kernel "
+                         "stamps (libtq4_stamps.so), the split tail delta, and the host enqueue "
+                         "cost of one decode call")
     ap.add_argument("--summarize-pmc", metavar="DIR")
     ap.add_argument("--summarize-trace", metavar="DIR")
     ap.add_argument("--trace-limit", type=int, default=0,
@@ -582,6 +586,8 @@ def main():
     if args.steps < 1:
         raise SystemExit("--steps must be at least 1")
 
+    if args.phases:
+        os.environ["TQ4_LIBRARY"] = "libtq4_stamps.so"  # before the library is first loaded
     import torch
 
     import __graft_entry__
@@ -591,6 +597,9 @@ def main():
 
     if args.pmc_run:
         pmc_workload(tq4, torch, dev)
+        return
+    if args.phases:
+        phases(tq4, torch, dev)
         return
 
     log(f"prefilling {SLICES} config-3 sequences ({SLICES * PAGES} pages)")
@@ -666,6 +675,67 @@ def main():
         result["INVALID"] = f"{timeouts} combine rows gave up their bounded poll"
     result.update(extra)
     print(json.dumps(result), flush=True)
+
+
+PHASES = ["start", "phase-0 loads retired", "first strip pairs issued", "q operands built",
+          "wave 0 strip loop done", "waves merged", "record exported (non-combining split)",
+          "first row combined (poll + merge)", "egress done (combiner)"]
+
+
+def phases(tq4, torch, dev, samples=64):
+    """The configs[2] decode's phase timeline from the measurement build:
+    after each replay of a graph of 32 cold back-to-back launches, the stamps
+    of its last launch (128 workgroups) are read; per phase the median over
+    workgroups of (stamp - the launch's first start), then the median over
+    samples. The split tail delta is the slowest split's export minus the
+    median split's. Host enqueue: wall time of eager tq4.paged_decode calls
+    (Python + ctypes + C ABI + launch), no synchronisation inside."""
+    import ctypes as C
+    lib_path = sys.modules[tq4.__name__ + ".tq4"].LIB_PATH
+    assert lib_path.endswith("libtq4_stamps.so"), lib_path
+    w = Workload(tq4, torch, dev, SLICES)
+    torch.cuda.synchronize()
+    nblk = B * HKV * w.splits
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    gs = [_graph(torch, stream, [lambda i=i: w.decode((32 * k + i) % SLICES) for i in range(32)])
+          for k in range(4)]
+    buf = np.zeros((4096, 16), np.uint64)
+    rows = []
+    for k in range(samples):
+        with torch.cuda.stream(stream):
+            gs[k % 4].replay()
+        torch.cuda.synchronize()
+        assert tq4.lib().tq4_decode_stamps(buf.ctypes.data_as(C.c_void_p), buf.nbytes) == 0
+        st = buf[:nblk].astype(np.int64)
+        t0 = st[:, 0].min()
+        rel = np.where(st > 0, (st - t0) * 0.01, np.nan)  # 100 MHz counter -> us
+        rows.append(rel)
+    rel = np.stack(rows)  # [sample][workgroup][slot]
+    out = {}
+    for i, name in enumerate(PHASES):
+        per = np.nanmedian(rel[:, :, i], axis=1) if np.isfinite(rel[:, :, i]).any() else None
+        if per is not None:
+            out[name] = round(float(np.nanmedian(per)), 3)
+    exp = rel[:, :, 6]
+    tail = np.nanmax(exp, axis=1) - np.nanmedian(exp, axis=1)
+    out["split export spread (max - median)"] = round(float(np.nanmedian(tail)), 3)
+    out["launch end (last combiner's egress)"] = round(float(np.nanmedian(np.nanmax(rel[:, :, 8], axis=1))), 3)
+    out["workgroup start spread (max)"] = round(float(np.nanmedian(np.nanmax(rel[:, :, 0], axis=1))), 3)
+    # host enqueue cost of one call (the GPU drains afterwards)
+    torch.cuda.synchronize()
+    n = 2000
+    t = time.perf_counter()
+    for i in range(n):
+        w.decode(i % SLICES)
+    host_us = (time.perf_counter() - t) / n * 1e6
+    torch.cuda.synchronize()
+    res = {"phases_us": out, "host_enqueue_us_per_call": round(host_us, 2),
+           "workload": "configs[2] single-sequence decode, cold, graphs of 32 back-to-back "
+                       "launches; stamps of the last launch (thread 0 of each workgroup)",
+           "samples": samples, "workgroups": int(nblk), "library": "libtq4_stamps.so",
+           "clock": "s_memrealtime, 100 MHz"}
+    print(json.dumps(res), flush=True)
 
 
 def pmc_workload(tq4, torch, dev):
