@@ -62,13 +62,14 @@ SLICES = 128
 SEED = 0x71340003
 CALIB_BYTES = 64 << 20  # plain copy (x * 2) of known size for the PMC scale factors
 PMC_FILE = os.path.join(REPO, "profiles", "pmc_summary.json")
-PMC_KERNELS = {  # kernel-name fragment -> key in profiles/pmc_summary.json
-    "decode_kernel<128, 1>": "decode_kernel<128,1>",
-    "decode_persistent_kernel<128>": "decode_persistent_kernel<128>",
-    "strip_writer<128, unsigned short, 1>": "strip_writer<128,bf16,1>",
-}
 CALIB_KERNEL = "MulFunctor<float"
-DECODE_KERNEL = "decode_kernel<128,1>@128"  # PMC key: kernel@workgroups (16 splits x 8 heads)
+SWEEP = ((4096, (2, 4, 8, 16, 0)), (16384, (2, 4, 8, 16, 0)), (32768, (2, 4, 8, 16, 0)),
+         (65536, (8, 16, 0)), (4103, (0,)))
+
+
+def sweep_row(ctx, k):
+    """PMC row name of a split-sweep row (k = the split count, auto resolved)."""
+    return f"sweep_ctx{ctx}_K{k}"
 
 
 def log(*a):
@@ -210,54 +211,57 @@ def roofline(nbytes, ms, kernel, pmc=None):
 
 
 def summarize_pmc(root):
-    """Mean counter value per dispatch for the profiled kernels over every
-    pass under root (rocprofv3 --output-format csv), by kernel and grid
-    ("name@workgroups"), FETCH_SIZE / WRITE_SIZE scaled to bytes by what they
-    read for the plain copy of CALIB_BYTES (the largest-grid float multiply)."""
-    vals = {}
-    meta = {}
-    for f in sorted(glob.glob(os.path.join(root, "*", "run_counter_collection.csv"))):
-        with open(f) as fh:
-            for row in csv.DictReader(fh):
-                name = row.get("Kernel_Name", "")
-                key = next((v for k, v in PMC_KERNELS.items() if k in name), None)
-                if key is None and CALIB_KERNEL in name:
-                    key = "copy"
-                if key is None:
-                    continue
-                grid, wg = int(row["Grid_Size"]), int(row["Workgroup_Size"])
-                kg = (key, grid)
-                vals.setdefault(kg, {}).setdefault(row["Counter_Name"], []).append(
-                    float(row["Counter_Value"]))
-                meta.setdefault(kg, {"workgroups": grid // max(1, wg), "workgroup_size": wg,
-                                     "vgprs": int(row["VGPR_Count"]),
-                                     "agprs": int(row["Accum_VGPR_Count"]),
-                                     "sgprs": int(row["SGPR_Count"]),
-                                     "lds_bytes": int(row["LDS_Block_Size"]),
-                                     "scratch_bytes": int(row["Scratch_Size"])})
-    copies = [kg for kg in vals if kg[0] == "copy"]
-    if not copies:
-        raise SystemExit(f"no calibration copy among the profiled kernels under {root}")
-    cal_kg = max(copies, key=lambda kg: kg[1])
-    cal = {c: float(np.mean(v)) for c, v in vals[cal_kg].items()}
-    f_scale = CALIB_BYTES / (cal["FETCH_SIZE"] * 1024.0)
-    w_scale = CALIB_BYTES / (cal["WRITE_SIZE"] * 1024.0)
-    out = {"calibration": {"kernel": "torch.mul(x, 2.0) over CALIB_BYTES of float32",
-                           "bytes_read_and_written": CALIB_BYTES,
-                           "dispatches": len(vals[cal_kg]["FETCH_SIZE"]),
-                           "fetch_kib_raw": cal["FETCH_SIZE"], "write_kib_raw": cal["WRITE_SIZE"],
-                           "fetch_scale": f_scale, "write_scale": w_scale}}
-    for (key, grid), cv in sorted(vals.items()):
-        if key == "copy":
+    """Mean counter value per dispatch of each profiled row: root/<row>/<pass>/
+    run_counter_collection.csv (rocprofv3 --output-format csv) over the passes
+    of `bench.py --pmc-run <row>`; the row's dispatches are those of its
+    kernel and grid (pmc_kernel_of), FETCH_SIZE / WRITE_SIZE scaled to bytes
+    by what they read for the row run's own plain copy of CALIB_BYTES."""
+    out = {}
+    for rdir in sorted(glob.glob(os.path.join(root, "*"))):
+        row = os.path.basename(rdir)
+        if not os.path.isdir(rdir) or row not in pmc_row_names():
             continue
-        e = {"kernel": key, **meta[(key, grid)],
-             "dispatches": max(len(v) for v in cv.values()),
-             "counters": {c: float(np.mean(v)) for c, v in cv.items()}}
-        if "FETCH_SIZE" in cv and "WRITE_SIZE" in cv:
-            e["fetch_bytes"] = e["counters"]["FETCH_SIZE"] * 1024.0 * f_scale
-            e["write_bytes"] = e["counters"]["WRITE_SIZE"] * 1024.0 * w_scale
+        frag, grid_wg = pmc_kernel_of(row)
+        vals, cals, meta = {}, {}, None
+        for f in sorted(glob.glob(os.path.join(rdir, "*", "run_counter_collection.csv"))):
+            with open(f) as fh:
+                for r in csv.DictReader(fh):
+                    name = r.get("Kernel_Name", "")
+                    grid, wg = int(r["Grid_Size"]), int(r["Workgroup_Size"])
+                    nwg = grid // max(1, wg)
+                    if CALIB_KERNEL in name:  # the copy is the largest such multiply
+                        cals.setdefault(grid, {}).setdefault(r["Counter_Name"], []).append(
+                            float(r["Counter_Value"]))
+                        continue
+                    if frag not in name or (grid_wg is not None and nwg != grid_wg):
+                        continue
+                    vals.setdefault(r["Counter_Name"], []).append(float(r["Counter_Value"]))
+                    short = name.replace("(anonymous namespace)::", "").replace("void ", "")
+                    meta = meta or {"kernel": short.split("(")[0].replace("tq4::", ""),
+                                    "workgroups": nwg, "workgroup_size": wg,
+                                    "vgprs": int(r["VGPR_Count"]),
+                                    "agprs": int(r["Accum_VGPR_Count"]),
+                                    "sgprs": int(r["SGPR_Count"]),
+                                    "lds_bytes": int(r["LDS_Block_Size"]),
+                                    "scratch_bytes": int(r["Scratch_Size"])}
+        if not vals:
+            continue
+        cal = cals[max(cals)] if cals else {}
+        e = {**meta, "dispatches": max(len(v) for v in vals.values()),
+             "counters": {c: float(np.mean(v)) for c, v in vals.items()}}
+        if "FETCH_SIZE" in vals and "WRITE_SIZE" in vals and "FETCH_SIZE" in cal \
+                and "WRITE_SIZE" in cal:
+            fs = CALIB_BYTES / (float(np.mean(cal["FETCH_SIZE"])) * 1024.0)
+            ws = CALIB_BYTES / (float(np.mean(cal["WRITE_SIZE"])) * 1024.0)
+            e["fetch_bytes"] = e["counters"]["FETCH_SIZE"] * 1024.0 * fs
+            e["write_bytes"] = e["counters"]["WRITE_SIZE"] * 1024.0 * ws
             e["traffic_bytes"] = e["fetch_bytes"] + e["write_bytes"]
-        out[f"{key}@{e['workgroups']}"] = e
+            e["calibration"] = {"fetch_kib_raw": float(np.mean(cal["FETCH_SIZE"])),
+                                "write_kib_raw": float(np.mean(cal["WRITE_SIZE"])),
+                                "fetch_scale": fs, "write_scale": ws}
+        out[row] = e
+    if not out:
+        raise SystemExit(f"no profiled rows under {root}")
     os.makedirs(os.path.dirname(PMC_FILE), exist_ok=True)
     with open(PMC_FILE, "w") as f:
         json.dump(out, f, indent=1)
@@ -265,17 +269,21 @@ def summarize_pmc(root):
 
 
 def print_pmc_table(out):
-    """Markdown view of the PMC summary."""
-    cal = out["calibration"]
-    print(f"Calibration copy: FETCH_SIZE {cal['fetch_kib_raw']:.0f} KiB and WRITE_SIZE "
-          f"{cal['write_kib_raw']:.0f} KiB for {CALIB_BYTES >> 10} KiB read and written "
-          f"(scales {cal['fetch_scale']:.3f}, {cal['write_scale']:.3f}).\n")
-    keys = [k for k in out if k != "calibration"]
+    """Markdown view of the PMC summary, one column per row."""
+    keys = list(out)
+    cals = [out[k]["calibration"] for k in keys if "calibration" in out[k]]
+    if cals:
+        fs = [c["fetch_scale"] for c in cals]
+        ws = [c["write_scale"] for c in cals]
+        print(f"Calibration (each row's run has its own plain copy of {CALIB_BYTES >> 20} MiB "
+              f"read and written): FETCH_SIZE scale {min(fs):.3f} .. {max(fs):.3f}, WRITE_SIZE "
+              f"scale {min(ws):.3f} .. {max(ws):.3f}.\n")
 
     def c(e, n):
         return e["counters"].get(n, float("nan"))
 
     lines = [
+        ("kernel", lambda e: f"`{e['kernel']}`"),
         ("dispatches", lambda e: f"{e['dispatches']}"),
         ("workgroups x size", lambda e: f"{e['workgroups']} x {e['workgroup_size']}"),
         ("arch VGPRs / AGPRs / SGPRs", lambda e: f"{e['vgprs']} / {e['agprs']} / {e['sgprs']}"),
@@ -302,7 +310,7 @@ def print_pmc_table(out):
         ("TA_ADDR_STALLED_BY_TC_CYCLES_sum / TA_BUSY_avr",
          lambda e: f"{c(e, 'TA_ADDR_STALLED_BY_TC_CYCLES_sum'):.0f} / {c(e, 'TA_BUSY_avr'):.0f}"),
     ]
-    print("| per dispatch | " + " | ".join(f"`{k}`" for k in keys) + " |")
+    print("| per dispatch | " + " | ".join(f"{k}" for k in keys) + " |")
     print("|---|" + "---|" * len(keys))
     for label, fn in lines:
         print(f"| {label} | " + " | ".join(fn(out[k]) for k in keys) + " |")
@@ -408,7 +416,7 @@ def oracle():
 class Workload:
     """SLICES config-3 sequences in one page pool, prefilled on the GPU."""
 
-    def __init__(self, tq4, torch, dev, slices):
+    def __init__(self, tq4, torch, dev, slices, touch=True):
         self.tq4, self.torch = tq4, torch
         rng = np.random.default_rng(SEED)
         gen = torch.Generator(device=dev)
@@ -446,7 +454,7 @@ class Workload:
         # stays cold for the timed steps: at least 96 other slices (> 400 MB,
         # more than the 256 MiB Infinity Cache) are read between this pass
         # and any slice's next use.
-        for i in range(slices):
+        for i in range(slices if touch else 0):
             self.decode(i)
 
     def decode(self, i, out=None):
@@ -517,14 +525,6 @@ class Batch:
         self.K = tq4.auto_splits(bsz, HKV, tab.shape[1], S_)
         self.ws = tq4.decode_workspace(bsz, HQ, HKV, D, self.K) if self.K > 1 else None
 
-    def kernel(self):
-        """The decode kernel's name and grid as the PMC summary keys it."""
-        bsz = len(self.ctxs)
-        if self.K == 1:
-            return f"decode_kernel<128,1>@{bsz * HKV}"
-        return f"decode_persistent_kernel<128>@512" if bsz * HKV * self.K > 512 else \
-            f"decode_kernel<128,1>@{bsz * HKV * self.K}"
-
     def scatter(self):
         self.tq4.reshape_scatter(self.kn, self.vn, self.kc, self.vc, self.sc, self.slots,
                                  self.signs, num_blocks=self.pool, block_size=S,
@@ -559,9 +559,10 @@ def main():
                     help="CPU-leg budget of the headline row (other rows use less)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="headline decode only")
-    ap.add_argument("--pmc-run", action="store_true",
-                    help="the profiled kernels' workloads plus a plain copy of known size, "
-                         "for rocprofv3 --pmc")
+    ap.add_argument("--pmc-run", metavar="ROW",
+                    help="one bench row's workload (8 or more launches of its kernel) plus a "
+                         "plain copy of known size, for rocprofv3 --pmc; --pmc-rows lists them")
+    ap.add_argument("--pmc-rows", action="store_true", help="the rows --pmc-run knows")
     ap.add_argument("--phases", action="store_true",
                     help="configs[2] per-phase timeline from the measurement build's in-kernel "
                          "stamps (libtq4_stamps.so), the split tail delta, and the host enqueue "
@@ -577,6 +578,9 @@ def main():
         return
     if args.summarize_trace:
         summarize_trace(args.summarize_trace, args.trace_limit)
+        return
+    if args.pmc_rows:
+        print(" ".join(pmc_row_names()))
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}): the TQ4 path is "
@@ -596,7 +600,7 @@ def main():
     torch.cuda.set_device(dev)
 
     if args.pmc_run:
-        pmc_workload(tq4, torch, dev)
+        pmc_workload(tq4, torch, dev, args.pmc_run)
         return
     if args.phases:
         phases(tq4, torch, dev)
@@ -664,7 +668,7 @@ def main():
         "decode_us": {"cold": round(cold_ms * 1e3, 3), "cold_spread": res["spread"],
                       "warm": round(warm["ms"] * 1e3, 3), "warm_spread": warm["spread"]},
         "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
-        "roofline": roofline(dec_bytes, cold_ms, DECODE_KERNEL, pmc),
+        "roofline": roofline(dec_bytes, cold_ms, "configs2_decode", pmc),
         "launch_floor_note": "a back-to-back graph launch of an empty kernel of 128 workgroups "
                              "costs about 1.7 us; one launch moving 4.47 MB therefore tops "
                              "out near 33 % of peak",
@@ -738,23 +742,112 @@ def phases(tq4, torch, dev, samples=64):
     print(json.dumps(res), flush=True)
 
 
-def pmc_workload(tq4, torch, dev):
-    """A few launches of each profiled kernel on the bench's own inputs
-    (cold where the bench is cold), then a plain copy of CALIB_BYTES."""
-    w = Workload(tq4, torch, dev, 32)
-    torch.cuda.synchronize()
-    for i in range(32):
-        w.decode(i)
-    torch.cuda.synchronize()
-    bats = [Batch(tq4, torch, dev, 0x71340050 + k, w.signs) for k in range(2)]
-    for _ in range(2):
-        for b in bats:
-            b.decode()
-    torch.cuda.synchronize()
-    del bats
-    wr = WriterInputs(tq4, torch, dev, w, 4)
-    for i in range(4):
-        wr.write(i)
+def pmc_row_names():
+    names = ["configs2_decode", "configs4_decode", "configs4_step_scatter", "configs1_writer",
+             "configs1_scatter", "rms_writer", "configs0_a8", "kv4_ref_shape", "kv4_batched",
+             "codebook_lloyd", "codebook_icdf"]
+    for ctx, ks in SWEEP:
+        names += [sweep_row(ctx, k) for k in ks if k]
+        names.append(sweep_row(ctx, "auto"))
+    return names
+
+
+def pmc_kernel_of(row):
+    """(kernel-name fragment, workgroups or None) of a PMC row's dispatches."""
+    fixed = {"configs2_decode": ("decode_kernel<128, 1>", B * HKV * 16),
+             "configs4_step_scatter": ("scatter_token_writer<128>", None),
+             "configs1_writer": ("strip_writer<128, unsigned short, 1>", 512),
+             "configs1_scatter": ("scatter_token_writer<128>", None),
+             "rms_writer": ("rms_writer<128, 1>", None),
+             "configs0_a8": ("strip_writer<128, signed char, 1>", None),
+             "kv4_ref_shape": ("kv4_decode_kernel", None), "kv4_batched": ("kv4_decode_kernel", None),
+             "codebook_lloyd": ("quantize_kernel", None), "codebook_icdf": ("icdf_kernel", None)}
+    if row in fixed:
+        return fixed[row]
+    if row == "configs4_decode":
+        return ("decode_", None)  # the kernel the auto split count selects
+    if row.startswith("sweep_"):
+        return ("decode_kernel<128, 1>", None)
+    raise SystemExit(f"unknown PMC row {row}")
+
+
+def pmc_workload(tq4, torch, dev, row):
+    """One bench row's workload on the bench's own input shapes (at least 8
+    launches of its kernel, cold where the bench is cold), then a plain copy
+    of CALIB_BYTES (the row run's calibration)."""
+    if row not in pmc_row_names():
+        raise SystemExit(f"unknown PMC row {row}; known: {' '.join(pmc_row_names())}")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0x71340007)
+    if row == "configs2_decode" or row.startswith("sweep_"):
+        # no set-up pass: a sweep row's kernel may share the headline's grid
+        w = Workload(tq4, torch, dev, 32, touch=row == "configs2_decode")
+        if row == "configs2_decode":
+            for i in range(32):
+                w.decode(i)
+        else:
+            ctx = int(row.split("_")[1][3:])
+            kk = row.split("_")[2][1:]
+            pages = (ctx + S - 1) // S
+            k = tq4.auto_splits(1, HKV, pages, S) if kk == "auto" else int(kk)
+            rng = np.random.default_rng(0x71340004)
+            ws = tq4.decode_workspace(1, HQ, HKV, D, k)
+            ctx_t = torch.tensor([ctx], dtype=torch.int32, device=dev)
+            out = torch.empty((1, HQ, D), dtype=torch.bfloat16, device=dev)
+            for _ in range(8):
+                tab = torch.from_numpy(rng.permutation(w.pool)[:pages].astype(np.int32)[None, :]).to(dev)
+                q = torch.randn((1, HQ, D), generator=gen, device=dev).to(torch.bfloat16)
+                tq4.paged_decode(q, w.kc, w.vc, w.sc, tab, ctx_t, w.signs, HKV, S, w.pool,
+                                 out=out, workspace=ws, num_splits=k, scale=w.scale,
+                                 inv_sqrt_len=w.isl)
+    elif row in ("configs4_decode", "configs4_step_scatter"):
+        signs = torch.ones(D, device=dev)
+        bats = [Batch(tq4, torch, dev, 0x71340050 + k, signs) for k in range(2)]
+        for _ in range(4):
+            for b in bats:
+                b.decode() if row == "configs4_decode" else b.scatter()
+    elif row in ("configs1_writer", "configs1_scatter", "rms_writer", "configs0_a8"):
+        w = Workload(tq4, torch, dev, 1, touch=False)
+        wr = WriterInputs(tq4, torch, dev, w, 8)
+        if row == "configs1_writer":
+            for i in range(8):
+                wr.write(i)
+        elif row == "configs1_scatter":
+            rng = np.random.default_rng(0x71340008)
+            for i in range(8):
+                k, v, _ = wr.ins[i]
+                strips = rng.permutation(wr.pool * S // 16)[:1024]
+                sl = torch.from_numpy((strips * 16 + rng.integers(0, 16, 1024)).astype(np.int32)).to(dev)
+                tq4.reshape_scatter(k, v, wr.kc, wr.vc, wr.sc, sl, w.signs, num_blocks=wr.pool,
+                                    block_size=S, inv_sqrt_len=w.isl)
+        elif row == "rms_writer":
+            rpool = wr.pool * S
+            rkc = torch.zeros(rpool * HKV * D // 2, dtype=torch.int8, device=dev)
+            rvc = torch.zeros_like(rkc)
+            rsc = torch.zeros(rpool * tq4.rms_scale_slot_floats(HKV), device=dev)
+            for i in range(8):
+                k, v, slots = wr.ins[i]
+                tq4.rms_reshape_and_cache(k, v, rkc, rvc, rsc, slots, w.signs, num_blocks=wr.pool,
+                                          block_size=S, inv_sqrt_len=w.isl)
+        else:
+            ident = torch.arange(S, dtype=torch.int32, device=dev)
+            for _ in range(8):
+                k = torch.randint(-127, 128, (S, HKV, D), dtype=torch.int8, device=dev, generator=gen)
+                v = torch.randint(-127, 128, (S, HKV, D), dtype=torch.int8, device=dev, generator=gen)
+                tq4.reshape_and_cache_a8(k, v, wr.kc, wr.vc, wr.sc, ident, pi_signs=w.signs,
+                                         num_blocks=wr.pool, block_size=S, inv_sqrt_len=w.isl)
+    elif row.startswith("kv4_"):
+        kv4fp8_workloads(tq4, torch, dev, None, only=row, launches=8)
+    elif row == "codebook_lloyd":
+        x = torch.randn(1 << 25, generator=gen, device=dev)
+        r_, c_ = torch.empty_like(x), torch.empty((1 << 24), dtype=torch.uint8, device=dev)
+        for _ in range(8):
+            tq4.lloydmax_quantize(x, 4, 0, dst=r_, codes=c_)
+    elif row == "codebook_icdf":
+        x = torch.randn(1 << 26, generator=gen, device=dev).to(torch.float16)
+        c_ = torch.empty((1 << 25), dtype=torch.uint8, device=dev)
+        for _ in range(8):
+            tq4.icdf_quantize(x, out=c_)
     torch.cuda.synchronize()
     src = torch.ones(CALIB_BYTES // 4, dtype=torch.float32, device=dev)
     dst = torch.empty_like(src)
@@ -762,7 +855,7 @@ def pmc_workload(tq4, torch, dev):
     for _ in range(4):
         torch.mul(src, 2.0, out=dst)  # the calibration copy: reads and writes CALIB_BYTES
     torch.cuda.synchronize()
-    log("pmc workload done")
+    log(f"pmc workload {row} done")
 
 
 class WriterInputs:
@@ -808,7 +901,7 @@ def extra_workloads(tq4, torch, dev, w, pmc, cpu=True):
     row = {"workload": "configs[1] BF16 1024 tokens -> 4096-page pool", **row_times(res),
            "tokens_per_s": round(wt / (res["ms"] * 1e-3), 1),
            "GBps": round(wbytes / (res["ms"] * 1e-3) / 1e9, 2), "algorithmic_bytes": wbytes,
-           "roofline": roofline(wbytes, res["ms"], "strip_writer<128,bf16,1>@512", pmc)}
+           "roofline": roofline(wbytes, res["ms"], "configs1_writer", pmc)}
     if cpu:
         from oracle_bindings import IN_BF16
         k, v, slots = (t.cpu() for t in wr.ins[0])
@@ -849,7 +942,8 @@ def extra_workloads(tq4, torch, dev, w, pmc, cpu=True):
     row = {"workload": "configs[1] secondary: 1024 BF16 tokens, one per strip at random "
                        "positions (value-strip RMW)", **row_times(res),
            "tokens_per_s": round(wt / (res["ms"] * 1e-3), 1),
-           "GBps": round(sbytes / (res["ms"] * 1e-3) / 1e9, 2), "algorithmic_bytes": sbytes}
+           "GBps": round(sbytes / (res["ms"] * 1e-3) / 1e9, 2), "algorithmic_bytes": sbytes,
+           "roofline": roofline(sbytes, res["ms"], "configs1_scatter", pmc)}
     if cpu:
         k, v, sl = (t.cpu() for t in sins[0])
         hk = k.view(torch.int16).numpy().view(np.uint16)
@@ -881,7 +975,8 @@ def extra_workloads(tq4, torch, dev, w, pmc, cpu=True):
     row = {"workload": "N2 RMS + threshold codec writer, 1024 BF16 tokens (the reference "
                        "bench's baseline writer)", **row_times(res),
            "tokens_per_s": round(wt / (res["ms"] * 1e-3), 1),
-           "GBps": round(rbytes / (res["ms"] * 1e-3) / 1e9, 2), "algorithmic_bytes": rbytes}
+           "GBps": round(rbytes / (res["ms"] * 1e-3) / 1e9, 2), "algorithmic_bytes": rbytes,
+           "roofline": roofline(rbytes, res["ms"], "rms_writer", pmc)}
     if cpu:
         k, v, slots = (t.cpu() for t in wr.ins[0])
         hk = k.view(torch.int16).numpy().view(np.uint16)
@@ -914,7 +1009,8 @@ def extra_workloads(tq4, torch, dev, w, pmc, cpu=True):
                         chunk=64)
     abytes = writer_algorithmic_bytes(S, HKV, D, 1)
     row = {"workload": "configs[0] A8, one 16-token strip", **row_times(res),
-           "tokens_per_s": round(S / (res["ms"] * 1e-3), 1), "algorithmic_bytes": abytes}
+           "tokens_per_s": round(S / (res["ms"] * 1e-3), 1), "algorithmic_bytes": abytes,
+           "roofline": roofline(abytes, res["ms"], "configs0_a8", pmc)}
     if cpu:
         from oracle_bindings import IN_INT8
         hk, hv = a8[0][0].cpu().numpy(), a8[0][1].cpu().numpy()
@@ -928,7 +1024,7 @@ def extra_workloads(tq4, torch, dev, w, pmc, cpu=True):
     log(f"reshape_and_cache A8 strip: {res['ms'] * 1e3:.2f} us")
 
     # --- split sweep over the headline pool
-    out["split_sweep"] = split_sweep(tq4, torch, dev, w, orc)
+    out["split_sweep"] = split_sweep(tq4, torch, dev, w, orc, pmc)
 
     # --- the batched step, two batches rotated (each 0.3 GB,
     # more than the Infinity Cache, so each step reads its batch cold)
@@ -947,7 +1043,7 @@ def extra_workloads(tq4, torch, dev, w, pmc, cpu=True):
            "cache": "cold (2 batches of 0.3 GB rotated)",
            "decode_only": {**row_times(resd), "GBps": round(dbytes / (resd["ms"] * 1e-3) / 1e9, 2),
                            "algorithmic_bytes": dbytes},
-           "roofline": roofline(dbytes, resd["ms"], bats[0].kernel(), pmc),
+           "roofline": roofline(dbytes, resd["ms"], "configs4_decode", pmc),
            "poll_timeouts": t_step}
     if t_step:
         row["INVALID"] = f"{t_step} combine rows gave up their bounded poll"
@@ -989,12 +1085,30 @@ def extra_workloads(tq4, torch, dev, w, pmc, cpu=True):
     out["codebook"] = {
         "lloydmax4_32M_fp32": {**row_times(res_l),
                                "GBps": round(lbytes / (res_l["ms"] * 1e-3) / 1e9, 1),
-                               "algorithmic_bytes": lbytes},
+                               "algorithmic_bytes": lbytes,
+                               "roofline": roofline(lbytes, res_l["ms"], "codebook_lloyd", pmc)},
         "icdf_64M_fp16": {**row_times(res_i), "GBps": round(ibytes / (res_i["ms"] * 1e-3) / 1e9, 1),
-                          "algorithmic_bytes": ibytes}}
+                          "algorithmic_bytes": ibytes,
+                          "roofline": roofline(ibytes, res_i["ms"], "codebook_icdf", pmc)}}
     log(f"codebook: Lloyd-Max {lbytes / (res_l['ms'] * 1e-3) / 1e9:.0f} GB/s, "
         f"ICDF {ibytes / (res_i['ms'] * 1e-3) / 1e9:.0f} GB/s")
-    out["kv4fp8_decode"] = kv4fp8_workloads(tq4, torch, dev, orc)
+    out["kv4fp8_decode"] = kv4fp8_workloads(tq4, torch, dev, orc, pmc=pmc)
+
+    # --- the practical streaming ceiling on this box: a plain device copy of
+    # 512 MiB (1 GiB read + written per launch), two buffer pairs rotated
+    n = (512 << 20) // 4
+    bufs = [(torch.ones(n, device=dev), torch.empty(n, device=dev)) for _ in range(2)]
+    res_c = time_launches(torch, [lambda i=i: bufs[i][1].copy_(bufs[i][0]) for i in range(2)],
+                          16, 4, samples=8, chunk=4)
+    cbytes = 2 * n * 4
+    out["device_copy"] = {"workload": "torch copy_ of 512 MiB float32 (read + write 1 GiB)",
+                          **row_times(res_c),
+                          "GBps": round(cbytes / (res_c["ms"] * 1e-3) / 1e9, 1),
+                          "pct_hbm_peak": round(100 * cbytes / (res_c["ms"] * 1e-3) / 1e9
+                                                / HBM_PEAK_GBS, 2),
+                          "algorithmic_bytes": cbytes}
+    log(f"device copy: {cbytes / (res_c['ms'] * 1e-3) / 1e9:.0f} GB/s")
+    del bufs
     return out
 
 
@@ -1005,7 +1119,7 @@ def kv4fp8_cache_bytes(tokens, ctx, kv_heads):
     return tokens * ctx * (kv_heads * 256 + 32)
 
 
-def kv4fp8_workloads(tq4, torch, dev, orc=None):
+def kv4fp8_workloads(tq4, torch, dev, orc=None, pmc=None, only=None, launches=0):
     """The KV4/FP8 NZ-tiled decode: the reference benchmark's shape
     (bench_turboquant_decode_splitk --impl fused-opt: 1 request, 16 q heads over
     one KV head, D=256, 128-row pages, FP32 pre-rotated query, FP16 output) at
@@ -1016,6 +1130,9 @@ def kv4fp8_workloads(tq4, torch, dev, orc=None):
     gain = 2.9832882881
     for name, (T, H, G, S_, ctx) in (("ref_shape_1x16q1kv_ctx4096", (1, 1, 16, 128, 4096)),
                                       ("batched_32x64q4kv_ctx8192", (32, 4, 16, 128, 8192))):
+        row_name = "kv4_ref_shape" if T == 1 else "kv4_batched"
+        if only is not None and only != row_name:
+            continue
         pages = (ctx + S_ - 1) // S_
         P = T * pages
         key = torch.randint(0, 256, (P * S_ * H * 128,), dtype=torch.uint8, device=dev,
@@ -1033,6 +1150,10 @@ def kv4fp8_workloads(tq4, torch, dev, orc=None):
         run()
         torch.cuda.synchronize()
         assert torch.isfinite(o.float()).all(), "kv4fp8 decode produced non-finite values"
+        if only is not None:  # the PMC workload: plain launches, no timing
+            for _ in range(launches):
+                run()
+            continue
         # The batched case follows the reference shape's CPU baseline (the GPU
         # idle for about a second); its first ~8 ms of launches then run at
         # 64-66 us and later ones at 57-58 us, so it warms up for three
@@ -1047,7 +1168,8 @@ def kv4fp8_workloads(tq4, torch, dev, orc=None):
                      "tokens": T, "q_heads": H * G, "kv_heads": H, "head_dim": 256,
                      "ctx": ctx, "page_size": S_, "algorithmic_bytes": nbytes,
                      "cache": "warm" if nbytes < (256 << 20) else "beyond the Infinity Cache",
-                     "poll_timeouts": timeouts}
+                     "poll_timeouts": timeouts,
+                     "roofline": roofline(nbytes, r["ms"], row_name, pmc)}
         if timeouts:
             res[name]["INVALID"] = f"{timeouts} combine rows gave up their bounded poll"
         log(f"kv4fp8 {name}: {r['ms'] * 1e3:.2f} us -> {gbs:.0f} GB/s")
@@ -1061,7 +1183,7 @@ def kv4fp8_workloads(tq4, torch, dev, orc=None):
     return res
 
 
-def split_sweep(tq4, torch, dev, w, orc=None):
+def split_sweep(tq4, torch, dev, w, orc=None, pmc=None):
     """the fused decode at ctx {4096, 16384, 32768, 65536} x K
     {2, 4, 8, 16, auto}, plus the ragged ctx 4103 at auto; cold (each time
     rotates over enough sequences that >= 512 MB are read between re-reads).
@@ -1070,8 +1192,7 @@ def split_sweep(tq4, torch, dev, w, orc=None):
     gen = torch.Generator(device=dev)
     gen.manual_seed(0x71340004)
     rows = []
-    for ctx, ks in ((4096, (2, 4, 8, 16, 0)), (16384, (2, 4, 8, 16, 0)),
-                    (32768, (2, 4, 8, 16, 0)), (65536, (8, 16, 0)), (4103, (0,))):
+    for ctx, ks in SWEEP:
         pages = (ctx + S - 1) // S
         if pages > w.pool:
             continue
@@ -1098,7 +1219,8 @@ def split_sweep(tq4, torch, dev, w, orc=None):
             gbs = nbytes / (r["ms"] * 1e-3) / 1e9
             row = {"ctx": ctx, "splits": kk, "auto": k == 0, **row_times(r),
                    "GBps": round(gbs, 1), "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
-                   "algorithmic_bytes": nbytes, "poll_timeouts": timeouts}
+                   "algorithmic_bytes": nbytes, "poll_timeouts": timeouts,
+                   "roofline": roofline(nbytes, r["ms"], sweep_row(ctx, k or "auto"), pmc)}
             if timeouts:
                 row["INVALID"] = f"{timeouts} combine rows gave up their bounded poll"
             if orc is not None and k == 0:

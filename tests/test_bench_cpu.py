@@ -51,27 +51,36 @@ def _write_counters(path, rows):
 
 
 def test_pmc_summary_scales_by_the_calibration_copy(tmp_path, monkeypatch):
+    """Each row's dispatches (its kernel and grid) are averaged over the passes
+    of its own directory and scaled by that run's plain copy."""
     monkeypatch.setattr(bench, "PMC_FILE", str(tmp_path / "pmc.json"))
     copy = "void at::native::vectorized_elementwise_kernel<4, MulFunctor<float> >"
     dec = "void tq4::(anonymous namespace)::decode_kernel<128, 1>(tq4::DecodeParams)"
     cal_kib = bench.CALIB_BYTES / 1024
-    _write_counters(str(tmp_path / "p1" / "run_counter_collection.csv"), [
+    row = tmp_path / "configs2_decode"
+    _write_counters(str(row / "p1" / "run_counter_collection.csv"), [
         (copy, 4096, "FETCH_SIZE", cal_kib / 2),  # the counter reads half the bytes
         (copy, 64, "FETCH_SIZE", 1.0),            # a smaller multiply is not the copy
         (dec, 128, "FETCH_SIZE", 1000.0), (dec, 128, "FETCH_SIZE", 3000.0),
-        (dec, 16, "FETCH_SIZE", 7.0)])
-    _write_counters(str(tmp_path / "p2" / "run_counter_collection.csv"), [
+        (dec, 16, "FETCH_SIZE", 7.0)])           # another grid: not this row's kernel
+    _write_counters(str(row / "p2" / "run_counter_collection.csv"), [
         (copy, 4096, "WRITE_SIZE", cal_kib), (dec, 128, "WRITE_SIZE", 100.0),
         (dec, 16, "WRITE_SIZE", 1.0)])
+    sw = tmp_path / "sweep_ctx4096_K2"
+    _write_counters(str(sw / "p1" / "run_counter_collection.csv"), [
+        (copy, 4096, "FETCH_SIZE", cal_kib), (dec, 16, "FETCH_SIZE", 7.0)])
+    _write_counters(str(sw / "p2" / "run_counter_collection.csv"), [
+        (copy, 4096, "WRITE_SIZE", cal_kib), (dec, 16, "WRITE_SIZE", 1.0)])
     bench.summarize_pmc(str(tmp_path))
     out = json.load(open(tmp_path / "pmc.json"))
-    assert out["calibration"]["fetch_scale"] == pytest.approx(2.0)
-    assert out["calibration"]["write_scale"] == pytest.approx(1.0)
-    e = out["decode_kernel<128,1>@128"]
+    e = out["configs2_decode"]
+    assert e["calibration"]["fetch_scale"] == pytest.approx(2.0)
+    assert e["calibration"]["write_scale"] == pytest.approx(1.0)
+    assert e["dispatches"] == 2 and e["workgroups"] == 128
     assert e["fetch_bytes"] == pytest.approx(2000.0 * 1024 * 2)
     assert e["write_bytes"] == pytest.approx(100.0 * 1024)
-    assert out["decode_kernel<128,1>@16"]["fetch_bytes"] == pytest.approx(7.0 * 2048)
-    r = bench.roofline(4_473_860, 0.01, "decode_kernel<128,1>@128", out)
+    assert out["sweep_ctx4096_K2"]["fetch_bytes"] == pytest.approx(7.0 * 1024)
+    r = bench.roofline(4_473_860, 0.01, "configs2_decode", out)
     assert r["traffic"] == round(e["traffic_bytes"])
     assert r["frac"] == pytest.approx(4_473_860 / 1e-5 / 1e9 / 8000, abs=1e-4)
 
