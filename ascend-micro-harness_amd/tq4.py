@@ -80,6 +80,8 @@ def lib():
     L.tq4_decode_workspace_bytes.argtypes = [_U32] * 5
     L.tq4_decode_auto_splits.restype = _U32
     L.tq4_decode_auto_splits.argtypes = [_U32] * 4
+    L.tq4_decode_auto_splits_lens.restype = _U32
+    L.tq4_decode_auto_splits_lens.argtypes = [_U32] * 4 + [_P]
     L.tq4_decode_workspace_init.restype = _I32
     L.tq4_decode_workspace_init.argtypes = [_P, _P, _SZ]
     L.tq4_decode_poll_timeouts.restype = _I32
@@ -278,9 +280,19 @@ def decode_workspace_bytes(num_seqs, num_heads, num_kv_heads, head_size, num_spl
                                                 num_splits))
 
 
-def auto_splits(num_seqs, num_kv_heads, max_blocks_per_seq, block_size):
-    return int(lib().tq4_decode_auto_splits(num_seqs, num_kv_heads, max_blocks_per_seq,
-                                            block_size))
+def auto_splits(num_seqs, num_kv_heads, max_blocks_per_seq, block_size, context_lens=None):
+    """The decode's split count (tq4_decode_auto_splits); with the context
+    lengths on the host (a sequence of ints, not a device tensor), the
+    length-aware rule (tq4_decode_auto_splits_lens)."""
+    if context_lens is None:
+        return int(lib().tq4_decode_auto_splits(num_seqs, num_kv_heads, max_blocks_per_seq,
+                                                block_size))
+    import numpy as np
+    lens = np.ascontiguousarray(np.asarray(context_lens, dtype=np.int32))
+    if lens.size != num_seqs:
+        raise ValueError(f"auto_splits: {lens.size} context lengths for {num_seqs} sequences")
+    return int(lib().tq4_decode_auto_splits_lens(num_seqs, num_kv_heads, max_blocks_per_seq,
+                                                 block_size, lens.ctypes.data))
 
 
 def decode_workspace_init(workspace, stream=None):

@@ -470,7 +470,8 @@ class Batch:
     way tests/test_gpu_scatter.py builds its cache (whole strips by the
     aligned writer, each partial tail by the scatter writer), so the timed
     decode sees the data the parity test checks; one new token per sequence
-    for the step's scatter. Decoded at the auto split count."""
+    for the step's scatter. Decoded at the split count of the length-aware
+    auto rule (tq4_decode_auto_splits_lens)."""
 
     def __init__(self, tq4, torch, dev, seed, signs):
         S_ = S
@@ -522,7 +523,8 @@ class Batch:
         self.kn = torch.randn((bsz, HKV, D), generator=gen, device=dev).to(torch.bfloat16)
         self.vn = torch.randn((bsz, HKV, D), generator=gen, device=dev).to(torch.bfloat16)
         self.out = torch.empty_like(self.q)
-        self.K = tq4.auto_splits(bsz, HKV, tab.shape[1], S_)
+        # the host holds the lengths: the length-aware split rule
+        self.K = tq4.auto_splits(bsz, HKV, tab.shape[1], S_, context_lens=[c + 1 for c in self.ctxs])
         self.ws = tq4.decode_workspace(bsz, HQ, HKV, D, self.K) if self.K > 1 else None
 
     def scatter(self):

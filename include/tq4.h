@@ -180,6 +180,15 @@ uint32_t tq4_decode_auto_splits(uint32_t num_seqs, uint32_t num_kv_heads,
  * call (its counters, and its records, which it consumes and clears); a
  * workspace that tq4_paged_decode_partials has written since must be zeroed
  * again before tq4_paged_decode uses it. */
+/* tq4_decode_auto_splits for a caller that holds the context lengths on the
+ * host (context_lens: num_seqs host integers; NULL gives the plain rule): a
+ * ragged batch (longest >= 1.6 x mean) whose num_seqs * num_kv_heads lies
+ * between 256 and 768 takes at least 3 splits. No reference counterpart (the
+ * reference's callers pass their split count). */
+uint32_t tq4_decode_auto_splits_lens(uint32_t num_seqs, uint32_t num_kv_heads,
+                                     uint32_t max_blocks_per_seq, uint32_t block_size,
+                                     const int32_t* context_lens);
+
 int tq4_decode_workspace_init(void* stream, void* workspace, size_t workspace_bytes);
 
 /* The fused entry's timeout count: rows (times 16-split record chunks) whose

@@ -231,3 +231,34 @@ def test_noalloc_refusals_before_any_hip_call(lib):
     assert to(None, 1, 8, None) == -1                   # no count pointer
     assert to(None, 0, 8, C.byref(cnt)) == -3           # no sequences
     assert to(None, 1 << 20, 8, C.byref(cnt)) == -13    # a tail beyond the scratch
+
+
+def test_auto_splits_lens_rule(lib):
+    """The length-aware split rule is a host function: NULL lengths give the
+    plain rule; a ragged batch (longest >= 1.6 x mean) of 256..768 (seq, kv
+    head) items takes at least 3 splits; uniform, mildly ragged and larger
+    batches keep the plain rule."""
+    import numpy as np
+    f = lib.tq4_decode_auto_splits_lens
+    f.restype = C.c_uint32
+    f.argtypes = [C.c_uint32] * 4 + [C.c_void_p]
+    plain = lib.tq4_decode_auto_splits
+    plain.restype = C.c_uint32
+
+    def lens(a):
+        a = np.ascontiguousarray(np.asarray(a, np.int32))
+        return a, a.ctypes.data
+    r = np.random.default_rng(0x71340005)
+    ragged, p = lens(r.integers(512, 8193, 64) + 1)
+    assert f(64, 8, 513, 16, None) == plain(64, 8, 513, 16) == 2
+    assert f(64, 8, 513, 16, p) == 3                       # configs[4]
+    uni, pu = lens([8192] * 64)
+    assert f(64, 8, 512, 16, pu) == plain(64, 8, 512, 16)  # uniform
+    mild, pm = lens(np.random.default_rng(7).integers(2048, 8193, 64))
+    assert f(64, 8, 513, 16, pm) == plain(64, 8, 513, 16)  # max/mean 1.53
+    big, pb = lens(np.random.default_rng(7).integers(512, 8193, 128))
+    assert f(128, 8, 513, 16, pb) == plain(128, 8, 513, 16)  # 1024 items
+    small, ps = lens([4096] + [16] * 15)
+    assert f(16, 8, 256, 16, ps) == plain(16, 8, 256, 16)  # 128 items
+    wide, pw = lens(np.random.default_rng(3).integers(1, 32769, 64))
+    assert f(64, 8, 2048, 16, pw) == max(3, plain(64, 8, 2048, 16)) == 4

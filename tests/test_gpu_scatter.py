@@ -147,15 +147,18 @@ def test_config5_batched_decode_step(tq4, oracle):
     after = [host(kc), host(vc), host(sc)]
     assert_same(after, o)
     # split-K decode over ctx + 1, against the oracle on the same cache image:
-    # the auto split count (one launch, local finish), which bench.py times
-    # for this batch, and K = 3, which runs the persistent work-queue kernel
-    # (64 x 8 x 3 items > the resident workgroup slots) on a fresh workspace
+    # the length-blind auto split count (K = 2 for this 513-page table), and
+    # the length-aware one that bench.py times for this batch (K = 3: the
+    # persistent work-queue kernel, 64 x 8 x 3 items > the resident workgroup
+    # slots) on a fresh workspace
     q = f32_to_bf16(rng.standard_normal((B, Hq, d)).astype(np.float32))
     ctx1 = (ctx + 1).astype(np.int32)
     scale = np.float32(1 / math.sqrt(d))
     _, want = oracle.paged_decode(q, after[0], after[1], after[2], tables, ctx1, signs, None, Hq,
                                   H, d, S, P, 1, scale, np.float32(isl), 1, threads=16)
-    for K in (0, 3):
+    k_lens = tq4.auto_splits(B, H, maxb, S, context_lens=ctx1)
+    assert k_lens == 3, k_lens  # the ragged batch the rule is for
+    for K in (0, k_lens):
         ws = tq4.decode_workspace(B, Hq, H, d, K) if K else None
         print(f"configs[4] decode K={K or 'auto'}", flush=True)
         out = tq4.paged_decode(dev(q), kc, vc, sc, dev(tables), dev(ctx1), dev(signs), H, S, P,
