@@ -33,7 +33,8 @@ process may run on, each on a bounded sample of the row's workload.
 Usage:
   python bench.py [--gpus 1] [--steps K] [--warmup W]
   python bench.py --pmc-run              # workload for rocprofv3 --pmc passes
-  python bench.py --summarize-pmc DIR    # DIR/<pass>/run_counter_collection.csv
+  python bench.py --summarize-pmc DIR    # DIR/<row>/<pass>/run_counter_collection.csv
+  python bench.py --pmc-table            # the committed summary as markdown
   python bench.py --summarize-trace DIR  # a rocprofv3 --kernel-trace csv run
 """
 from __future__ import annotations
@@ -269,8 +270,10 @@ def summarize_pmc(root):
 
 
 def print_pmc_table(out):
-    """Markdown view of the PMC summary, one column per row."""
-    keys = list(out)
+    """Markdown view of the PMC summary: HBM traffic for every row, then the
+    LDS, occupancy and instruction counters of the rows that have them (one
+    line per bench row, per-dispatch means)."""
+    keys = sorted(out)
     cals = [out[k]["calibration"] for k in keys if "calibration" in out[k]]
     if cals:
         fs = [c["fetch_scale"] for c in cals]
@@ -282,38 +285,30 @@ def print_pmc_table(out):
     def c(e, n):
         return e["counters"].get(n, float("nan"))
 
-    lines = [
-        ("kernel", lambda e: f"`{e['kernel']}`"),
-        ("dispatches", lambda e: f"{e['dispatches']}"),
-        ("workgroups x size", lambda e: f"{e['workgroups']} x {e['workgroup_size']}"),
-        ("arch VGPRs / AGPRs / SGPRs", lambda e: f"{e['vgprs']} / {e['agprs']} / {e['sgprs']}"),
-        ("LDS bytes / scratch bytes", lambda e: f"{e['lds_bytes']} / {e['scratch_bytes']}"),
-        ("FETCH_SIZE KiB raw -> bytes", lambda e: f"{c(e, 'FETCH_SIZE'):.1f} -> {e.get('fetch_bytes', 0):.0f}"),
-        ("WRITE_SIZE KiB raw -> bytes", lambda e: f"{c(e, 'WRITE_SIZE'):.1f} -> {e.get('write_bytes', 0):.0f}"),
-        ("HBM traffic bytes", lambda e: f"{e.get('traffic_bytes', 0):.0f}"),
-        ("SQ_LDS_BANK_CONFLICT / SQ_LDS_IDX_ACTIVE (cycles)",
-         lambda e: f"{c(e, 'SQ_LDS_BANK_CONFLICT'):.0f} / {c(e, 'SQ_LDS_IDX_ACTIVE'):.0f}"),
-        ("bank-conflict share of LDS-active cycles",
-         lambda e: f"{c(e, 'SQ_LDS_BANK_CONFLICT') / max(1.0, c(e, 'SQ_LDS_IDX_ACTIVE')):.3f}"),
-        ("LDSBankConflict (derived)", lambda e: f"{c(e, 'LDSBankConflict'):.3f}"),
-        ("SQ_INSTS_LDS", lambda e: f"{c(e, 'SQ_INSTS_LDS'):.0f}"),
-        ("MeanOccupancyPerActiveCU (derived)", lambda e: f"{c(e, 'MeanOccupancyPerActiveCU'):.3f}"),
-        ("SQ_WAVES / SQ_WAVE_CYCLES", lambda e: f"{c(e, 'SQ_WAVES'):.0f} / {c(e, 'SQ_WAVE_CYCLES'):.0f}"),
-        ("SQ_BUSY_CU_CYCLES / GRBM_GUI_ACTIVE",
-         lambda e: f"{c(e, 'SQ_BUSY_CU_CYCLES'):.0f} / {c(e, 'GRBM_GUI_ACTIVE'):.0f}"),
-        ("SQ_INSTS_VALU / SQ_INSTS_MFMA", lambda e: f"{c(e, 'SQ_INSTS_VALU'):.0f} / {c(e, 'SQ_INSTS_MFMA'):.0f}"),
-        ("SQ_VALU_MFMA_BUSY_CYCLES", lambda e: f"{c(e, 'SQ_VALU_MFMA_BUSY_CYCLES'):.0f}"),
-        ("SQ_INSTS_VMEM_RD", lambda e: f"{c(e, 'SQ_INSTS_VMEM_RD'):.0f}"),
-        ("SQ_WAIT_INST_ANY / SQ_WAIT_ANY", lambda e: f"{c(e, 'SQ_WAIT_INST_ANY'):.0f} / {c(e, 'SQ_WAIT_ANY'):.0f}"),
-        ("SQ_VMEM_TA_ADDR_FIFO_FULL / _CMD_FIFO_FULL",
-         lambda e: f"{c(e, 'SQ_VMEM_TA_ADDR_FIFO_FULL'):.0f} / {c(e, 'SQ_VMEM_TA_CMD_FIFO_FULL'):.0f}"),
-        ("TA_ADDR_STALLED_BY_TC_CYCLES_sum / TA_BUSY_avr",
-         lambda e: f"{c(e, 'TA_ADDR_STALLED_BY_TC_CYCLES_sum'):.0f} / {c(e, 'TA_BUSY_avr'):.0f}"),
-    ]
-    print("| per dispatch | " + " | ".join(f"{k}" for k in keys) + " |")
-    print("|---|" + "---|" * len(keys))
-    for label, fn in lines:
-        print(f"| {label} | " + " | ".join(fn(out[k]) for k in keys) + " |")
+    print("| row | kernel | workgroups | dispatches | FETCH_SIZE KiB | WRITE_SIZE KiB | "
+          "HBM bytes (scaled) |")
+    print("|---|---|---|---|---|---|---|")
+    for k in keys:
+        e = out[k]
+        print(f"| {k} | `{e['kernel']}` | {e['workgroups']} | {e['dispatches']} | "
+              f"{c(e, 'FETCH_SIZE'):.1f} | {c(e, 'WRITE_SIZE'):.1f} | "
+              f"{e.get('traffic_bytes', 0):.0f} |")
+    detail = [k for k in keys if not math.isnan(c(out[k], "SQ_WAVES"))]
+    if not detail:
+        return
+    print("\n| row | LDS bank-conflict cycles / LDS-active cycles | SQ_INSTS_LDS | "
+          "MeanOccupancyPerActiveCU | SQ_WAVES | SQ_INSTS_VALU | SQ_INSTS_MFMA | "
+          "SQ_INSTS_VMEM_RD | SQ_BUSY_CU_CYCLES / GRBM_GUI_ACTIVE |")
+    print("|---|---|---|---|---|---|---|---|---|")
+    for k in detail:
+        e = out[k]
+        bc, act = c(e, "SQ_LDS_BANK_CONFLICT"), c(e, "SQ_LDS_IDX_ACTIVE")
+        share = f"{bc / act:.3f}" if act > 0 else "no LDS"
+        print(f"| {k} | {share} ({bc:.0f} / {act:.0f}) | {c(e, 'SQ_INSTS_LDS'):.0f} | "
+              f"{c(e, 'MeanOccupancyPerActiveCU'):.3f} | {c(e, 'SQ_WAVES'):.0f} | "
+              f"{c(e, 'SQ_INSTS_VALU'):.0f} | {c(e, 'SQ_INSTS_MFMA'):.0f} | "
+              f"{c(e, 'SQ_INSTS_VMEM_RD'):.0f} | "
+              f"{c(e, 'SQ_BUSY_CU_CYCLES'):.0f} / {c(e, 'GRBM_GUI_ACTIVE'):.0f} |")
 
 
 def summarize_trace(root, limit=0):
@@ -570,6 +565,8 @@ def main():
                          "stamps (libtq4_stamps.so), the split tail delta, and the host enqueue "
                          "cost of one decode call")
     ap.add_argument("--summarize-pmc", metavar="DIR")
+    ap.add_argument("--pmc-table", action="store_true",
+                    help="print the committed PMC summary as markdown")
     ap.add_argument("--summarize-trace", metavar="DIR")
     ap.add_argument("--trace-limit", type=int, default=0,
                     help="with --summarize-trace: the first N dispatches of each kernel and grid")
@@ -577,6 +574,10 @@ def main():
 
     if args.summarize_pmc:
         summarize_pmc(args.summarize_pmc)
+        return
+    if args.pmc_table:
+        with open(PMC_FILE) as f:
+            print_pmc_table(json.load(f))
         return
     if args.summarize_trace:
         summarize_trace(args.summarize_trace, args.trace_limit)
