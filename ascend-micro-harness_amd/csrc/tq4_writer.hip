@@ -141,11 +141,211 @@ __device__ __forceinline__ void store_key_codes(int8_t* dst, const int (&q)[CPL]
 }
 
 // ------------------------------------------------------------ strip writer
-// grid.x = strips * (H / NH); a workgroup owns one strip of NH heads, both
-// planes: every lane runs 2*NH independent row jobs (plane fastest), all of
-// whose loads go out before the first rotation, and the launch has 2*NH
-// times fewer waves to dispatch than one workgroup per (strip, head, plane).
-template <int D, typename In, int NH>
+// The strip writer's row order and arithmetic, tuned for the VALU issue rate
+// (with two waves per SIMD the writer's rotation, quantisation and packing
+// are issue-bound, four cycles per wave64 instruction):
+//
+// * Lane order. A row's 16 lanes hold logical lanes l (channels l*CPL ..) at
+//   physical lane p(l) = l ^ (l & 4 ? 3 : 0), a linear map that puts logical
+//   bits 1, 2, 4, 8 at physical xor masks 1, 2, 7, 8. Each cross-lane
+//   butterfly stage is then one DPP-fed add: quad_perm (xor 1, xor 2),
+//   row_half_mirror (xor 7 inside each 8-lane half) and row_ror:8 (xor 8).
+//   p is its own inverse.
+// * Quantiser. t = fma(y, 2^(2-e), kQMagic) with kQMagic = 1.5 * 2^23 + 8:
+//   y * 2^(2-e) is exact and |y * 2^(2-e)| < 8, so the one rounding of the
+//   sum is the round-to-nearest-even of y * 2^(2-e) (kQMagic is even: ties
+//   keep their parity), and t = kQMagic + n exactly; min(t, kQMagic + 7) is
+//   the clamp at 7. Bits 0..3 of t then hold n + 8 and bits 4..7 are zero,
+//   so codes pack with one shift-or per pair and byte permutes, and the
+//   packed word is XORed with 0x8...8 to give the two's-complement nibbles.
+//   Non-finite inputs saturate: +inf and NaN give 7, -inf gives -8.
+// * One barrier: the slot vote and the value-strip transpose share it; the
+//   rotation runs while the slot loads are in flight.
+
+constexpr float kQMagic = 12582920.0f;     // 1.5 * 2^23 + 8
+constexpr float kQMagicTop = 12582927.0f;  // kQMagic + 7
+
+__device__ __forceinline__ int writer_lane(int p) { return p ^ ((p & 4) ? 3 : 0); }
+
+// The value at logical lane l ^ (1 << k) of the row (k = 0..3).
+__device__ __forceinline__ float writer_partner(float v, int k)
+{
+    const int x = __float_as_int(v);
+    int r;
+    switch (k) {
+        case 0: r = __builtin_amdgcn_update_dpp(x, x, 0xB1, 0xF, 0xF, true); break;   // quad_perm 1,0,3,2
+        case 1: r = __builtin_amdgcn_update_dpp(x, x, 0x4E, 0xF, 0xF, true); break;   // quad_perm 2,3,0,1
+        case 2: r = __builtin_amdgcn_update_dpp(x, x, 0x141, 0xF, 0xF, true); break;  // row_half_mirror
+        default: r = __builtin_amdgcn_update_dpp(x, x, 0x128, 0xF, 0xF, true); break; // row_ror:8
+    }
+    return __int_as_float(r);
+}
+
+// w += c * w[partner] for eight values at once: v_fmac_f32 with its first
+// source read through DPP from the partner lane (k selects the pattern, as in
+// writer_partner). One asm block, so nothing is scheduled inside it; it
+// opens with two wait states, which a DPP read of a VGPR written by the
+// instruction just before it needs.
+#define TQ4_FMAC_DPP8(CTRL)                                                                      \
+    asm volatile("s_nop 1\n\t"                                                                   \
+                 "v_fmac_f32_dpp %0, %0, %8 " CTRL " row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t" \
+                 "v_fmac_f32_dpp %1, %1, %8 " CTRL " row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t" \
+                 "v_fmac_f32_dpp %2, %2, %8 " CTRL " row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t" \
+                 "v_fmac_f32_dpp %3, %3, %8 " CTRL " row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t" \
+                 "v_fmac_f32_dpp %4, %4, %8 " CTRL " row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t" \
+                 "v_fmac_f32_dpp %5, %5, %8 " CTRL " row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t" \
+                 "v_fmac_f32_dpp %6, %6, %8 " CTRL " row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t" \
+                 "v_fmac_f32_dpp %7, %7, %8 " CTRL " row_mask:0xf bank_mask:0xf bound_ctrl:1"     \
+                 : "+v"(x[0]), "+v"(x[1]), "+v"(x[2]), "+v"(x[3]), "+v"(x[4]), "+v"(x[5]),       \
+                   "+v"(x[6]), "+v"(x[7])                                                        \
+                 : "v"(c))
+
+__device__ __forceinline__ void fmac_partner8(float* x, float c, int k)
+{
+    switch (k) {
+        case 0: TQ4_FMAC_DPP8("quad_perm:[1,0,3,2]"); break;
+        case 1: TQ4_FMAC_DPP8("quad_perm:[2,3,0,1]"); break;
+        case 2: TQ4_FMAC_DPP8("row_half_mirror"); break;
+        default: TQ4_FMAC_DPP8("row_ror:8"); break;
+    }
+}
+#undef TQ4_FMAC_DPP8
+
+// One butterfly stage over the writer's two rows (key, value) in the writer
+// lane order (l: this lane's logical lane), on values held with a per-lane
+// sign: a lane stores w = sigma * v, sigma = (-1)^(number of logical lane
+// bits below the stage's that are set). In-register stages and the sign
+// diagonal commute with sigma. A cross-lane stage pairs lanes with the same
+// sigma; the butterfly
+//   out[i] = in[i ^ s] + ((i & s) ? -in[i] : in[i])
+// is then, on the stored values, w' = w + c * w_partner with c = -1 on the
+// upper lane and +1 on the lower (the upper lane's sigma flips): one
+// DPP-fed fused multiply-add per element. c * w_partner is exact, so the
+// one rounding is that of the reference's add or subtract.
+template <int CPL>
+__device__ __forceinline__ void writer_butterfly(float (&v)[2][CPL], int stride, int l)
+{
+    if (stride < CPL) {
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) {
+                if (j & stride) continue;
+                const float a = v[r][j];
+                const float b = v[r][j + stride];
+                v[r][j] = b + a;
+                v[r][j + stride] = a - b;
+            }
+        }
+    } else {
+        const int k = __builtin_ctz(stride / CPL);
+        const float c = ((l >> k) & 1) ? -1.0f : 1.0f;
+        if constexpr (CPL >= 8) {
+#pragma unroll
+            for (int r = 0; r < 2; ++r) {
+#pragma unroll
+                for (int j = 0; j < CPL; j += 8) fmac_partner8(&v[r][j], c, k);
+            }
+        } else {
+            float x[8] = {v[0][0], v[0][1], v[0][2], v[0][3], v[1][0], v[1][1], v[1][2], v[1][3]};
+            fmac_partner8(x, c, k);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) v[0][j] = x[j], v[1][j] = x[4 + j];
+        }
+    }
+}
+
+// Rotate both rows (strides 1..16, the sign diagonal, 32..D/2). The results
+// are held as sigma * v with sigma = (-1)^popcount(l) (writer_sigma).
+template <int D, int CPL>
+__device__ __forceinline__ void writer_rotate(float (&v)[2][CPL], const float (&sign)[CPL], int l)
+{
+#pragma unroll
+    for (int s = 1; s < 32 && s < D; s <<= 1) writer_butterfly<CPL>(v, s, l);
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) v[r][j] *= sign[j];
+    }
+#pragma unroll
+    for (int s = 32; s < D; s <<= 1) writer_butterfly<CPL>(v, s, l);
+}
+
+__device__ __forceinline__ float writer_sigma(int l)
+{
+    return (__builtin_popcount(l) & 1) ? -1.0f : 1.0f;
+}
+
+// Each row's absmax over its 16 lanes, starting from `floor` (1.0 for the
+// prefill policy, 0 for the exact one).
+template <int CPL>
+__device__ __forceinline__ void writer_absmax(const float (&v)[2][CPL], float floor, float (&a)[2])
+{
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+        a[r] = floor;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) a[r] = fmaxf(a[r], fabsf(v[r][j]));
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+#pragma unroll
+        for (int r = 0; r < 2; ++r) a[r] = fmaxf(a[r], writer_partner(a[r], k));
+    }
+}
+
+// Rotate both rows, take each row's absmax (prefill policy: floored at 1.0)
+// and quantise: t[r][j] receives kQMagic + code as bits; scale[r] is the
+// row's stored scale.
+template <int D, int CPL>
+__device__ __forceinline__ void writer_rotate_quantise(float (&v)[2][CPL], const float (&sign)[CPL],
+                                                       int l, float inv_sqrt_len,
+                                                       uint32_t (&t)[2][CPL], float (&scale)[2])
+{
+    writer_rotate<D, CPL>(v, sign, l);
+    float a[2];
+    writer_absmax<CPL>(v, 1.0f, a);
+    // the stored values are sigma * v: the quantiser's exact power of two
+    // carries sigma
+    const float sigma = writer_sigma(l);
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+        // a >= 1 (the prefill floor; NaN never wins fmaxf): the exponent
+        // field alone, 0 .. 128 (128: infinity); 2^(2-e) is a normal float
+        const int e = (int)(__float_as_uint(a[r]) >> 23) - 127;
+        const float p2 = sigma * ldexpf(1.0f, 2 - e);
+#pragma unroll
+        for (int j = 0; j < CPL; ++j)
+            t[r][j] = __float_as_uint(fminf(__builtin_fmaf(v[r][j], p2, kQMagic), kQMagicTop));
+        scale[r] = ldexpf(1.0f, e - 2) * inv_sqrt_len;
+    }
+}
+
+// Eight codes (t[k] bits 0..3 = code + 8, bits 4..7 zero) as one word of
+// signed nibbles, code k at bits 4k.
+__device__ __forceinline__ uint32_t pack8(const uint32_t* t)
+{
+    const uint32_t p01 = (t[1] << 4) | t[0];
+    const uint32_t p23 = (t[3] << 4) | t[2];
+    const uint32_t p45 = (t[5] << 4) | t[4];
+    const uint32_t p67 = (t[7] << 4) | t[6];
+    const uint32_t lo = __builtin_amdgcn_perm(p23, p01, 0x0C0C0400u);  // p01.b0, p23.b0
+    const uint32_t hi = __builtin_amdgcn_perm(p67, p45, 0x0C0C0400u);
+    return __builtin_amdgcn_perm(hi, lo, 0x05040100u) ^ 0x88888888u;
+}
+
+// Four codes as 16 bits of signed nibbles.
+__device__ __forceinline__ uint32_t pack4(const uint32_t* t)
+{
+    const uint32_t p01 = (t[1] << 4) | t[0];
+    const uint32_t p23 = (t[3] << 4) | t[2];
+    return (__builtin_amdgcn_perm(p23, p01, 0x0C0C0400u) ^ 0x8888u) & 0xffffu;
+}
+
+// grid = (strips, H): a workgroup owns one strip of one head, both planes;
+// every lane runs two row jobs (key, value), whose loads go out together
+// with the slot loads before the first rotation.
+template <int D, typename In>
 __global__ __launch_bounds__(kWriterThreads) void strip_writer(
     const In* __restrict__ key, const In* __restrict__ value, int8_t* __restrict__ key_cache,
     int8_t* __restrict__ value_cache, float* __restrict__ scale_cache,
@@ -154,104 +354,89 @@ __global__ __launch_bounds__(kWriterThreads) void strip_writer(
     float inv_sqrt_len)
 {
     constexpr int CPL = D / 16;
-    constexpr int NJ = 2 * NH;
-    constexpr int TS = 20;       // token stride of the transpose buffer, in words
-    // per value job: [channel / 8][token, padded to TS] words of 8 channel
-    // codes; 20-word rows put the 64 lanes of a wave (16 lanes x 4 tokens)
-    // on distinct banks
-    __shared__ __align__(16) uint32_t lds_t[NH][D / 8][TS];
+    constexpr int TS = 20;  // token stride of the transpose buffer, in words
+    // [channel / 8][token, padded to TS] words of 8 channel codes; 20-word
+    // rows put the 64 lanes of a wave (16 lanes x 4 tokens) on distinct banks
+    __shared__ __align__(16) uint32_t lds_t[D / 8][TS];
     __shared__ __align__(16) int ok_w[kWriterThreads / 64];  // per-wave slot checks
 
-    const uint32_t groups = H / NH;
-    const uint32_t head0 = (blockIdx.x % groups) * NH;
-    const uint32_t strip = blockIdx.x / groups;
+    const uint32_t strip = blockIdx.x, head = blockIdx.y;
     const int tid = threadIdx.x;
-    const int row = tid >> 4;        // token within the strip
-    const int lane_in_row = tid & 15;
+    const int row = tid >> 4;                 // token within the strip
+    const int l = writer_lane(tid & 15);      // logical lane: channels l*CPL ..
 
-    // The rows and the signs do not depend on the slots: their loads go out
-    // together with the slot loads (one round trip, not two).
-    float v[NJ][CPL], sign[CPL];
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-        const In* src = ((j & 1) == 0 ? key : value) +
-                        ((size_t)((size_t)strip * kStrip + row) * H + head0 + j / 2) * D +
-                        lane_in_row * CPL;
-        load_row<CPL>(src, v[j]);
-    }
-    load_signs<CPL>(pi_signs, tables, tables_bf16, lane_in_row * CPL, sign);
-
-    // Slot contract for this strip: consecutive, strip-aligned, in range.
+    // slots first, then the rows and the signs: one round trip for all
     const int32_t slot0 = slots[(size_t)strip * kStrip];
     const int32_t mine = slots[(size_t)strip * kStrip + row];
+    float v[2][CPL], sign[CPL];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const In* src = (j == 0 ? key : value) +
+                        ((size_t)((size_t)strip * kStrip + row) * H + head) * D + l * CPL;
+        load_row<CPL>(src, v[j]);
+    }
+    load_signs<CPL>(pi_signs, tables, tables_bf16, l * CPL, sign);
+
+    uint32_t t[2][CPL];
+    float scale[2];
+    writer_rotate_quantise<D, CPL>(v, sign, l, inv_sqrt_len, t, scale);
+
+    // Slot contract for this strip: consecutive, strip-aligned, in range.
+    // Each wave votes; the vote is read behind the transpose's barrier.
     const bool ok = slot0 >= 0 && (slot0 % kStrip) == 0 && mine == slot0 + row &&
                     (uint32_t)slot0 / S < P;
-    // One barrier: every wave writes its own vote, so nothing needs clearing.
     static_assert(kWriterThreads == 256, "four wave votes");
+    const int wv = __all(ok);
+    if ((tid & 63) == 0) ok_w[tid >> 6] = wv;
+    // value codes into the transpose buffer: one word of 8 channels per store
+    // (at d = 64 two lanes share a word, 16 bits each)
+    if constexpr (CPL >= 8) {
+#pragma unroll
+        for (int k = 0; k < CPL / 8; ++k) lds_t[l * (CPL / 8) + k][row] = pack8(&t[1][8 * k]);
+    } else {
+        ((uint16_t*)&lds_t[l >> 1][row])[l & 1] = (uint16_t)pack4(t[1]);
+    }
+    lds_barrier();
     {
-        const int wv = __all(ok);
-        if ((tid & 63) == 0) ok_w[tid >> 6] = wv;
-        __syncthreads();
         const int4 w4 = *(const int4*)ok_w;
         if (!(w4.x & w4.y & w4.z & w4.w)) return;
     }
     const uint32_t page = (uint32_t)slot0 / S;
     const uint32_t tip = (uint32_t)slot0 % S + (uint32_t)row;
-    int q[NJ][CPL];
-    float scale[NJ];
-#pragma unroll
-    for (int j = 0; j < NJ; ++j)
-        scale[j] = rotate_quantise<D, CPL>(v[j], sign, lane_in_row, inv_sqrt_len, kPolicyPrefill,
-                                           q[j]);
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-        const uint32_t plane = j & 1, head = head0 + j / 2;
-        const size_t head_base = ((size_t)page * H + head) * S;  // in tokens
-        if (lane_in_row == 0) scale_cache[(((size_t)plane * P + page) * H + head) * S + tip] = scale[j];
-        if (plane == 0) {
-            store_key_codes<CPL>(key_cache + (head_base + tip) * (D / 2) + lane_in_row * (CPL / 2),
-                                 q[j]);
-        } else {
-            // value plane: this token's codes of 8 channels per word, into
-            // the transpose buffer (one 32-bit LDS store per word; at d = 64
-            // two lanes share a word, a 16-bit store each)
-            if constexpr (CPL >= 8) {
-#pragma unroll
-                for (int k = 0; k < CPL / 8; ++k) {
-                    uint32_t w = 0;
-#pragma unroll
-                    for (int c = 0; c < 8; ++c) w |= ((uint32_t)q[j][8 * k + c] & 0xfu) << (4 * c);
-                    lds_t[j / 2][lane_in_row * (CPL / 8) + k][row] = w;
-                }
-            } else {
-                uint32_t w = 0;
-#pragma unroll
-                for (int c = 0; c < CPL; ++c) w |= ((uint32_t)q[j][c] & 0xfu) << (4 * c);
-                ((uint16_t*)&lds_t[j / 2][lane_in_row >> 1][row])[lane_in_row & 1] = (uint16_t)w;
-            }
-        }
+    const size_t head_base = ((size_t)page * H + head) * S;  // in tokens
+    if ((tid & 15) == 0) {
+        scale_cache[((size_t)page * H + head) * S + tip] = scale[0];
+        scale_cache[(((size_t)P + page) * H + head) * S + tip] = scale[1];
     }
-    __syncthreads();
-    // ... then each value strip leaves as d*8 contiguous bytes: output word
-    // (channel, half) holds that channel's codes of tokens 8*half .. +7, one
-    // nibble from each of 8 consecutive buffer words (two 16-byte reads)
-#pragma unroll
-    for (int h = 0; h < NH; ++h) {
-        const size_t head_base = ((size_t)page * H + head0 + h) * S;
-        uint32_t* strip_words =
-            (uint32_t*)(value_cache + (head_base + (tip & ~(uint32_t)15)) * (D / 2));
-        for (int w = tid; w < D * 2; w += kWriterThreads) {
-            const int channel = w >> 1, half = w & 1;
-            const uint32_t* src = &lds_t[h][channel >> 3][8 * half];
-            const uint4 a = *(const uint4*)src;
-            const uint4 b = *(const uint4*)(src + 4);
-            const uint32_t t8[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-            const uint32_t sh = 4u * (uint32_t)(channel & 7);
-            uint32_t out = 0;
-#pragma unroll
-            for (int t = 0; t < 8; ++t) out |= ((t8[t] >> sh) & 0xfu) << (4 * t);
-            strip_words[w] = out;
-        }
+    int8_t* kdst = key_cache + (head_base + tip) * (D / 2) + l * (CPL / 2);
+    if constexpr (CPL == 16)
+        *(uint2*)kdst = make_uint2(pack8(t[0]), pack8(&t[0][8]));
+    else if constexpr (CPL == 8)
+        *(uint32_t*)kdst = pack8(t[0]);
+    else
+        *(uint16_t*)kdst = (uint16_t)pack4(t[0]);
+    // the value strip leaves as d*8 contiguous bytes: output word (channel,
+    // half) holds that channel's codes of tokens 8*half .. +7, one nibble
+    // from each of 8 consecutive buffer words (two 16-byte reads)
+    uint32_t* strip_words =
+        (uint32_t*)(value_cache + (head_base + (tip & ~(uint32_t)15)) * (D / 2));
+    for (int w = tid; w < D * 2; w += kWriterThreads) {
+        const int channel = w >> 1, half = w & 1;
+        const uint32_t* src = &lds_t[channel >> 3][8 * half];
+        const uint4 a = *(const uint4*)src;
+        const uint4 b = *(const uint4*)(src + 4);
+        const uint32_t sh = 4u * (uint32_t)(channel & 7);
+        const uint32_t n[8] = {__builtin_amdgcn_ubfe(a.x, sh, 4), __builtin_amdgcn_ubfe(a.y, sh, 4),
+                               __builtin_amdgcn_ubfe(a.z, sh, 4), __builtin_amdgcn_ubfe(a.w, sh, 4),
+                               __builtin_amdgcn_ubfe(b.x, sh, 4), __builtin_amdgcn_ubfe(b.y, sh, 4),
+                               __builtin_amdgcn_ubfe(b.z, sh, 4), __builtin_amdgcn_ubfe(b.w, sh, 4)};
+        const uint32_t p01 = (n[1] << 4) | n[0];
+        const uint32_t p23 = (n[3] << 4) | n[2];
+        const uint32_t p45 = (n[5] << 4) | n[4];
+        const uint32_t p67 = (n[7] << 4) | n[6];
+        const uint32_t lo = __builtin_amdgcn_perm(p23, p01, 0x0C0C0400u);
+        const uint32_t hi = __builtin_amdgcn_perm(p67, p45, 0x0C0C0400u);
+        strip_words[w] = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
     }
 }
 
@@ -384,7 +569,7 @@ __global__ __launch_bounds__(kWriterThreads) void scatter_token_writer(
     constexpr int NW = 2 * CPL;  // strip words of a lane's channels
     const int tid = threadIdx.x;
     const int grp = tid >> 4;
-    const int lane_in_row = tid & 15;
+    const int l = writer_lane(tid & 15);  // logical lane: channels l*CPL ..
 
     if (probe != nullptr && blockIdx.x == 0 && tid < 32) {
         const int32_t fields[4] = {0, (int32_t)probe_grid, 1, (int32_t)item_count};
@@ -392,28 +577,25 @@ __global__ __launch_bounds__(kWriterThreads) void scatter_token_writer(
     }
 
     float sign[CPL];
-    load_signs<CPL>(pi_signs, nullptr, 0, lane_in_row * CPL, sign);
-    const uint64_t item_end = (uint64_t)item_begin + item_count;
-    for (uint64_t item = (uint64_t)item_begin + (uint64_t)blockIdx.x * 16u + (uint32_t)grp;
-         item < item_end; item += (uint64_t)gridDim.x * 16u) {
-        const uint32_t request = (uint32_t)(item / H);
-        const uint32_t head = (uint32_t)(item % H);
-        if (request >= num_requests) continue;
+    load_signs<CPL>(pi_signs, nullptr, 0, l * CPL, sign);
+    const float sigma = writer_sigma(l);
+    auto one = [&](uint32_t request, uint32_t head) {
+        if (request >= num_requests) return;
         // The rows do not depend on the slot: their loads go out with its
         // load. A pad or out-of-pool slot reads page 0's strip and stores
         // nothing (so no load waits behind a branch).
-        const size_t src_off = ((size_t)request * H + head) * D + lane_in_row * CPL;
+        const size_t src_off = ((size_t)request * H + head) * D + l * CPL;
         const int32_t slot = slots[request];
-        float kx[CPL], vx[CPL];
-        load_row<CPL>(key + src_off, kx);
-        load_row<CPL>(value + src_off, vx);
-        const bool ok = slot >= 0 && (uint32_t)slot / S < P;
-        const uint32_t page = ok ? (uint32_t)slot / S : 0u;
-        const uint32_t tip = ok ? (uint32_t)slot % S : 0u;
+        float v[2][CPL];
+        load_row<CPL>(key + src_off, v[0]);
+        load_row<CPL>(value + src_off, v[1]);
+        const uint32_t page_raw = (uint32_t)slot / S;
+        const bool ok = slot >= 0 && page_raw < P;
+        const uint32_t page = ok ? page_raw : 0u;
+        const uint32_t tip = ok ? (uint32_t)slot - page_raw * S : 0u;
         const uint32_t col = tip % kStrip;
         const size_t head_base = ((size_t)page * H + head) * S;
-        uint4* strip = (uint4*)(value_cache + (head_base + (tip - col)) * (D / 2)) +
-                       lane_in_row * (NW / 4);
+        uint4* strip = (uint4*)(value_cache + (head_base + (tip - col)) * (D / 2)) + l * (NW / 4);
         uint32_t w[NW];
 #pragma unroll
         for (int i = 0; i < NW / 4; ++i) {
@@ -423,27 +605,70 @@ __global__ __launch_bounds__(kWriterThreads) void scatter_token_writer(
             w[4 * i + 2] = u.z;
             w[4 * i + 3] = u.w;
         }
-        int qk[CPL], qv[CPL];
-        const float sk = rotate_quantise<D, CPL>(kx, sign, lane_in_row, inv_sqrt_len,
-                                                 kPolicyExact, qk);
-        const float sv = rotate_quantise<D, CPL>(vx, sign, lane_in_row, inv_sqrt_len,
-                                                 kPolicyExact, qv);
-        if (!ok) continue;
-        if (lane_in_row == 0) {
-            scale_cache[((size_t)page * H + head) * S + tip] = sk;
-            scale_cache[(((size_t)P + page) * H + head) * S + tip] = sv;
+        // exact policy: absmax as is; a zero row (every element +-0 or
+        // NaN) stores codes 0 and scale 1.0
+        writer_rotate<D, CPL>(v, sign, l);
+        float a[2];
+        writer_absmax<CPL>(v, 0.0f, a);
+        int e[2];
+        float sc[2];
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+            e[r] = a[r] == 0.0f ? 2 : exponent_of(a[r]);
+            sc[r] = a[r] == 0.0f ? 1.0f : ldexpf(1.0f, e[r] - 2) * inv_sqrt_len;
         }
-        store_key_codes<CPL>(key_cache + (head_base + tip) * (D / 2) + lane_in_row * (CPL / 2),
-                             qk);
-        const uint32_t sh = 4u * (col & 7u), half = col >> 3;
+        // y = v * 2^(2-e) by ldexp (e may be as low as -149), then the
+        // magic-number rounding with sigma folded into the multiplier: keys
+        // with kQMagic (code + 8 in bits 0..3, packed), values with
+        // kQMagic - 8 (the two's-complement nibble in bits 0..3, spliced)
+        uint32_t tk[CPL], tv[CPL];
 #pragma unroll
         for (int j = 0; j < CPL; ++j) {
-            uint32_t& x = w[2 * j + half];
-            x = (x & ~(0xfu << sh)) | (((uint32_t)qv[j] & 0xfu) << sh);
+            const float yk = a[0] == 0.0f ? 0.0f : ldexpf(v[0][j], 2 - e[0]);
+            const float yv = a[1] == 0.0f ? 0.0f : ldexpf(v[1][j], 2 - e[1]);
+            tk[j] = __float_as_uint(fminf(__builtin_fmaf(yk, sigma, kQMagic), kQMagicTop));
+            tv[j] = __float_as_uint(
+                fminf(__builtin_fmaf(yv, sigma, kQMagic - 8.0f), kQMagicTop - 8.0f));
+        }
+        if (!ok) return;
+        if ((tid & 15) == 0) {
+            scale_cache[((size_t)page * H + head) * S + tip] = sc[0];
+            scale_cache[(((size_t)P + page) * H + head) * S + tip] = sc[1];
+        }
+        int8_t* kdst = key_cache + (head_base + tip) * (D / 2) + l * (CPL / 2);
+        if constexpr (CPL == 16)
+            *(uint2*)kdst = make_uint2(pack8(tk), pack8(&tk[8]));
+        else if constexpr (CPL == 8)
+            *(uint32_t*)kdst = pack8(tk);
+        else
+            *(uint16_t*)kdst = (uint16_t)pack4(tk);
+        // the column's nibble in word 2j (tokens 0..7) or 2j + 1 (8..15):
+        // both words take a bit-field insert, one under an empty mask (no
+        // register array indexed by a lane value)
+        const uint32_t sh = 4u * (col & 7u);
+        const uint32_t m1 = (col >> 3) ? 0xfu << sh : 0u, m0 = (0xfu << sh) ^ m1;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+            const uint32_t y = tv[j] << sh;
+            w[2 * j] = (w[2 * j] & ~m0) | (y & m0);
+            w[2 * j + 1] = (w[2 * j + 1] & ~m1) | (y & m1);
         }
 #pragma unroll
         for (int i = 0; i < NW / 4; ++i)
             strip[i] = make_uint4(w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]);
+    };
+    const uint64_t item_end = (uint64_t)item_begin + item_count;
+    const uint32_t stride = gridDim.x * 16u;  // at most 4096 * 16
+    if (item_end + stride <= 0xffffffffull) {
+        // 32-bit item arithmetic: no item, nor the step past the last one,
+        // reaches 2^32
+        for (uint32_t item = item_begin + blockIdx.x * 16u + (uint32_t)grp;
+             item < (uint32_t)item_end; item += stride)
+            one(item / H, item % H);
+    } else {
+        for (uint64_t item = (uint64_t)item_begin + (uint64_t)blockIdx.x * 16u + (uint32_t)grp;
+             item < item_end; item += (uint64_t)gridDim.x * 16u)
+            one((uint32_t)(item / H), (uint32_t)(item % H));
     }
 }
 
@@ -460,10 +685,11 @@ static hipError_t launch_strip_writer_t(hipStream_t stream, const In* key, const
     // One head per workgroup (two row jobs per lane) measured faster than
     // two (four jobs): with one wave per SIMD nothing hides the rotation's
     // dependent lane exchanges.
-    const uint64_t blocks = (uint64_t)strips * H;
-    hipLaunchKernelGGL((strip_writer<D, In, 1>), dim3((uint32_t)blocks), dim3(kWriterThreads), 0,
-                       stream, key, value, key_cache, value_cache, scale_cache, slots, pi_signs,
-                       tables, tables_bf16, H, S, P, inv_sqrt_len);
+    if (strips == 0 || H == 0) return hipSuccess;
+    if (H > 65535u) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((strip_writer<D, In>), dim3(strips, H), dim3(kWriterThreads), 0, stream,
+                       key, value, key_cache, value_cache, scale_cache, slots, pi_signs, tables,
+                       tables_bf16, H, S, P, inv_sqrt_len);
     return hipGetLastError();
 }
 

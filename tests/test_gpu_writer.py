@@ -108,6 +108,23 @@ def test_config2_bf16_normal_1024(tq4, oracle):
     assert_images_equal(got, want)
 
 
+@pytest.mark.parametrize("d", [64, 128, 256])
+def test_wide_range_rows(tq4, oracle, d):
+    """Rows scaled by 2^k, k in [-40, 100] per (token, head, plane): the
+    quantiser's exponent runs from the prefill floor (e = 0) to e ~ 110, and
+    rows of one strip differ by up to 2^140; bit-exact against the oracle."""
+    rng = np.random.default_rng(0x7134000D + d)
+    H, S, P, T = 4, 16, 128, 256
+    k = rng.integers(-40, 101, (2, T, H, 1)).astype(np.float64)
+    x = rng.standard_normal((2, T, H, d)) * np.exp2(k)
+    key, val = (f32_to_bf16(x[i].astype(np.float32)) for i in range(2))
+    slots = (rng.permutation(P)[: T // 16, None] * 16 + np.arange(16)).reshape(-1).astype(np.int32)
+    got, want, skipped = run_pair(tq4, oracle, IN_BF16, key, val, slots, H, d, S, P,
+                                  signs=oracle.canonical_signs(d))
+    assert skipped == 0
+    assert_images_equal(got, want)
+
+
 @pytest.mark.parametrize("S", [32, 64])
 def test_multi_strip_pages(tq4, oracle, S):
     """block_size > 16: strips land at their strip-in-page, strip-blocked value layout."""
