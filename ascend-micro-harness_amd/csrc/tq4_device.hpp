@@ -65,6 +65,95 @@ __device__ __forceinline__ float xor_lanes(float v, int mask)
     return __uint_as_float((lane & 32u) ? p[0] : p[1]);
 }
 
+// Row lane order for rows of 16 lanes (the writers): logical lane l
+// (channels l*CPL ..) lives on physical lane p(l) = l ^ (l & 4 ? 3 : 0), a
+// linear map that puts logical bits 1, 2, 4, 8 at physical xor masks 1, 2, 7,
+// 8, so that each is one DPP pattern: quad_perm (xor 1, xor 2),
+// row_half_mirror (xor 7 inside each 8-lane half) and row_ror:8 (xor 8).
+// p is its own inverse.
+__device__ __forceinline__ int row_lane(int p) { return p ^ ((p & 4) ? 3 : 0); }
+
+// The value at logical lane l ^ (1 << k) of the row (k = 0..3).
+__device__ __forceinline__ float row_partner(float v, int k)
+{
+    const int x = __float_as_int(v);
+    int r;
+    switch (k) {
+        case 0: r = __builtin_amdgcn_update_dpp(x, x, 0xB1, 0xF, 0xF, true); break;   // quad_perm 1,0,3,2
+        case 1: r = __builtin_amdgcn_update_dpp(x, x, 0x4E, 0xF, 0xF, true); break;   // quad_perm 2,3,0,1
+        case 2: r = __builtin_amdgcn_update_dpp(x, x, 0x141, 0xF, 0xF, true); break;  // row_half_mirror
+        default: r = __builtin_amdgcn_update_dpp(x, x, 0x128, 0xF, 0xF, true); break; // row_ror:8
+    }
+    return __int_as_float(r);
+}
+
+// w += c * w[logical lane l ^ (1 << k)] for 8 (or 4) values: v_fmac_f32 with
+// its first source read through DPP. One asm block, so nothing is scheduled
+// inside it; it opens with the two wait states that a DPP read of a VGPR
+// written by the instruction just before it needs. (The compiler does not
+// fold a DPP move into v_fmac_f32.)
+#define TQ4_FMAC_DPP(I, C, CTRL) \
+    "v_fmac_f32_dpp %" #I ", %" #I ", %" #C " " CTRL " row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+#define TQ4_FMAC_DPP8(CTRL)                                                                       \
+    asm volatile("s_nop 1\n\t" TQ4_FMAC_DPP(0, 8, CTRL) TQ4_FMAC_DPP(1, 8, CTRL)                 \
+                     TQ4_FMAC_DPP(2, 8, CTRL) TQ4_FMAC_DPP(3, 8, CTRL) TQ4_FMAC_DPP(4, 8, CTRL)  \
+                         TQ4_FMAC_DPP(5, 8, CTRL) TQ4_FMAC_DPP(6, 8, CTRL) TQ4_FMAC_DPP(7, 8, CTRL) \
+                 : "+v"(x[0]), "+v"(x[1]), "+v"(x[2]), "+v"(x[3]), "+v"(x[4]), "+v"(x[5]),        \
+                   "+v"(x[6]), "+v"(x[7])                                                         \
+                 : "v"(c))
+#define TQ4_FMAC_DPP4(CTRL)                                                                       \
+    asm volatile("s_nop 1\n\t" TQ4_FMAC_DPP(0, 4, CTRL) TQ4_FMAC_DPP(1, 4, CTRL)                 \
+                     TQ4_FMAC_DPP(2, 4, CTRL) TQ4_FMAC_DPP(3, 4, CTRL)                            \
+                 : "+v"(x[0]), "+v"(x[1]), "+v"(x[2]), "+v"(x[3])                                 \
+                 : "v"(c))
+
+__device__ __forceinline__ void fmac_partner8(float* x, float c, int k)
+{
+    switch (k) {
+        case 0: TQ4_FMAC_DPP8("quad_perm:[1,0,3,2]"); break;
+        case 1: TQ4_FMAC_DPP8("quad_perm:[2,3,0,1]"); break;
+        case 2: TQ4_FMAC_DPP8("row_half_mirror"); break;
+        default: TQ4_FMAC_DPP8("row_ror:8"); break;
+    }
+}
+
+__device__ __forceinline__ void fmac_partner4(float* x, float c, int k)
+{
+    switch (k) {
+        case 0: TQ4_FMAC_DPP4("quad_perm:[1,0,3,2]"); break;
+        case 1: TQ4_FMAC_DPP4("quad_perm:[2,3,0,1]"); break;
+        case 2: TQ4_FMAC_DPP4("row_half_mirror"); break;
+        default: TQ4_FMAC_DPP4("row_ror:8"); break;
+    }
+}
+#undef TQ4_FMAC_DPP4
+#undef TQ4_FMAC_DPP8
+#undef TQ4_FMAC_DPP
+
+// One cross-lane butterfly stage of a row in the row lane order, on values
+// held with a per-lane sign: a lane stores w = sigma * v, sigma = (-1)^(the
+// number of logical lane bits below the stage's that are set). The stage's
+// pair shares sigma, and the butterfly
+//   out[i] = in[i ^ s] + ((i & s) ? -in[i] : in[i])
+// is w' = w + c * w_partner with c = -1 on the upper lane (whose sigma then
+// flips) and +1 on the lower: one fused multiply-add per element, exact in
+// the product (c = +-1), so its one rounding is that of the add or subtract.
+// In-register stages and sign diagonals commute with sigma; after the last
+// stage sigma = (-1)^popcount(l) (row_sigma).
+template <int CPL>
+__device__ __forceinline__ void row_fmac_stage(float (&v)[CPL], float c, int k)
+{
+    if constexpr (CPL >= 8) {
+#pragma unroll
+        for (int j = 0; j < CPL; j += 8) fmac_partner8(&v[j], c, k);
+    } else {
+        static_assert(CPL == 4, "4, 8 or 16 channels per lane");
+        fmac_partner4(v, c, k);
+    }
+}
+
+__device__ __forceinline__ float row_sigma(int l) { return (__builtin_popcount(l) & 1) ? -1.0f : 1.0f; }
+
 // One butterfly stage at `stride` over a row spread across lanes, CPL
 // consecutive channels per lane (channel = lane_in_row * CPL + j):
 //   out[i] = in[i ^ s] + ((i & s) ? -in[i] : in[i])

@@ -17,10 +17,10 @@
 //
 // MI355X design: a vector is spread over 16 lanes of one wave row, d/16
 // consecutive channels per lane (one 16-byte load of BF16 at d = 128), 16
-// vectors per 256-lane workgroup. The FWHT runs in registers below d/16 and as
-// DPP lane exchanges above (the butterfly of the TQ4 writer, same a+b / a-b
-// bits); the sum of squares is a sequential per-lane sum and a 4-step xor
-// tree over the row. The level needs no table walk: since t_{14-i} = -t_i and
+// vectors per 256-lane workgroup, in the row lane order of the TQ4 writers
+// (row_lane). The FWHT runs in registers below d/16 and as DPP-fed fused
+// butterflies above (row_fmac_stage, same a+b / a-b bits); the sum of
+// squares is a sequential per-lane sum and a 4-step tree over logical lanes. The level needs no table walk: since t_{14-i} = -t_i and
 // t_7 = 0, a positive z counts 8 + #{t_8..t_14 < z} and a negative one
 // 7 - #{t_8..t_14 <= -z}, each a 3-step binary search over seven constants.
 // A row's d/2 packed bytes leave as one coalesced run (d/32 bytes per lane).
@@ -102,14 +102,18 @@ __global__ __launch_bounds__(kRmsThreads) void rms_writer(
 {
     constexpr int CPL = D / kRowLanes;
     const int lane = threadIdx.x & (kRowLanes - 1);
+    const int l = row_lane(lane);  // logical lane: channels l*CPL ..
     const uint64_t row = (uint64_t)blockIdx.x * (kRmsThreads / kRowLanes) + threadIdx.x / kRowLanes;
     const uint32_t planes = 2 * H;
-    if (row >= (uint64_t)tokens * planes) return;
-    const uint32_t t = (uint32_t)(row / planes), plane = (uint32_t)(row % planes);
+    const uint64_t rows = (uint64_t)tokens * planes;
+    if (row >= rows) return;
+    // 32-bit division when every row index fits (a uniform branch)
+    const uint32_t t = rows <= 0xffffffffull ? (uint32_t)row / planes : (uint32_t)(row / planes);
+    const uint32_t plane = (uint32_t)row - t * planes;
     const uint32_t h = plane < H ? plane : plane - H;
     const int32_t slot = slots[t];
     // the row's channels lane*CPL .. +CPL: one vector load, and the signs
-    const uint16_t* src = (plane < H ? key : value) + ((uint64_t)t * H + h) * D + lane * CPL;
+    const uint16_t* src = (plane < H ? key : value) + ((uint64_t)t * H + h) * D + l * CPL;
     uint16_t raw[CPL];
     if constexpr (CPL == 4) {
         const uint2 w = *(const uint2*)src;
@@ -129,27 +133,46 @@ __global__ __launch_bounds__(kRmsThreads) void rms_writer(
     float sg[CPL], v[CPL];
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
-        sg[j] = pi_signs[lane * CPL + j];
+        sg[j] = pi_signs[l * CPL + j];
         v[j] = IN_BF16 ? bf16_to_f32(raw[j]) : (float)__builtin_bit_cast(_Float16, raw[j]);
     }
     if (slot < 0 || (uint64_t)slot >= slot_count) return;  // a pad token or a slot past the pool
 
-    // ApplyPi: signs, FWHT at strides 1 .. D/2, x inv_sqrt_len, signs
+    // ApplyPi: signs, FWHT at strides 1 .. D/2, x inv_sqrt_len, signs. The
+    // FWHT's cross-lane stages run on sign-tracked values (row_fmac_stage):
+    // v holds sigma * y afterwards, sigma = row_sigma(l)
 #pragma unroll
     for (int j = 0; j < CPL; ++j) v[j] = v[j] * sg[j];
 #pragma unroll
-    for (int s = 1; s < D; s <<= 1) butterfly<CPL>(v, s, lane);
+    for (int s = 1; s < D; s <<= 1) {
+        if (s < CPL) {
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) {
+                if (j & s) continue;
+                const float a = v[j];
+                const float b = v[j + s];
+                v[j] = b + a;
+                v[j + s] = a - b;
+            }
+        } else {
+            const int k = __builtin_ctz(s / CPL);
+            row_fmac_stage<CPL>(v, ((l >> k) & 1) ? -1.0f : 1.0f, k);
+        }
+    }
 #pragma unroll
     for (int j = 0; j < CPL; ++j) v[j] = (v[j] * inv_sqrt_len) * sg[j];
 
-    // scale = sqrt(sum y^2) * inv_sqrt_len + eps: per-lane sequential sum, xor tree
+    // scale = sqrt(sum y^2) * inv_sqrt_len + eps: per-lane sequential sum,
+    // then the tree over logical lanes l ^ 1, l ^ 2, l ^ 4, l ^ 8 ((sigma y)^2
+    // is y^2 exactly)
     float ss = v[0] * v[0];
 #pragma unroll
     for (int j = 1; j < CPL; ++j) ss = ss + v[j] * v[j];
 #pragma unroll
-    for (int m = 1; m < kRowLanes; m <<= 1) ss = ss + xor_lanes(ss, m);
+    for (int k = 0; k < 4; ++k) ss = ss + row_partner(ss, k);
     const float scale = sqrt_rn(ss) * inv_sqrt_len + kRmsEps;
-    const float rcp = __fdiv_rn(1.0f, scale);
+    // sigma rides on the reciprocal: (sigma y) * (sigma r) rounds as y * r
+    const float rcp = row_sigma(l) * __fdiv_rn(1.0f, scale);
 
     // levels, packed (even | odd << 4) ^ 0x80 -- the -128 bias of the int8 byte
     uint32_t pk[CPL / 8 > 0 ? CPL / 8 : 1] = {};
@@ -159,7 +182,7 @@ __global__ __launch_bounds__(kRmsThreads) void rms_writer(
         pk[j / 8] |= q << (4 * (j % 8));
     }
     int8_t* dst = (plane < H ? key_cache : value_cache) + ((uint64_t)slot * H + h) * (D / 2) +
-                  lane * (CPL / 2);
+                  l * (CPL / 2);
     if constexpr (CPL == 4) {
         *(uint16_t*)dst = (uint16_t)(pk[0] ^ 0x8080u);
     } else if constexpr (CPL == 8) {

@@ -145,12 +145,10 @@ __device__ __forceinline__ void store_key_codes(int8_t* dst, const int (&q)[CPL]
 // (with two waves per SIMD the writer's rotation, quantisation and packing
 // are issue-bound, four cycles per wave64 instruction):
 //
-// * Lane order. A row's 16 lanes hold logical lanes l (channels l*CPL ..) at
-//   physical lane p(l) = l ^ (l & 4 ? 3 : 0), a linear map that puts logical
-//   bits 1, 2, 4, 8 at physical xor masks 1, 2, 7, 8. Each cross-lane
-//   butterfly stage is then one DPP-fed add: quad_perm (xor 1, xor 2),
-//   row_half_mirror (xor 7 inside each 8-lane half) and row_ror:8 (xor 8).
-//   p is its own inverse.
+// * Lane order and butterflies: the row lane order of tq4_device.hpp
+//   (row_lane), where every cross-lane stride is one DPP pattern, and the
+//   sign-tracked butterfly (row_fmac_stage): one DPP-fed v_fmac_f32 per
+//   element and stage.
 // * Quantiser. t = fma(y, 2^(2-e), kQMagic) with kQMagic = 1.5 * 2^23 + 8:
 //   y * 2^(2-e) is exact and |y * 2^(2-e)| < 8, so the one rounding of the
 //   sum is the round-to-nearest-even of y * 2^(2-e) (kQMagic is even: ties
@@ -165,63 +163,9 @@ __device__ __forceinline__ void store_key_codes(int8_t* dst, const int (&q)[CPL]
 constexpr float kQMagic = 12582920.0f;     // 1.5 * 2^23 + 8
 constexpr float kQMagicTop = 12582927.0f;  // kQMagic + 7
 
-__device__ __forceinline__ int writer_lane(int p) { return p ^ ((p & 4) ? 3 : 0); }
-
-// The value at logical lane l ^ (1 << k) of the row (k = 0..3).
-__device__ __forceinline__ float writer_partner(float v, int k)
-{
-    const int x = __float_as_int(v);
-    int r;
-    switch (k) {
-        case 0: r = __builtin_amdgcn_update_dpp(x, x, 0xB1, 0xF, 0xF, true); break;   // quad_perm 1,0,3,2
-        case 1: r = __builtin_amdgcn_update_dpp(x, x, 0x4E, 0xF, 0xF, true); break;   // quad_perm 2,3,0,1
-        case 2: r = __builtin_amdgcn_update_dpp(x, x, 0x141, 0xF, 0xF, true); break;  // row_half_mirror
-        default: r = __builtin_amdgcn_update_dpp(x, x, 0x128, 0xF, 0xF, true); break; // row_ror:8
-    }
-    return __int_as_float(r);
-}
-
-// w += c * w[partner] for eight values at once: v_fmac_f32 with its first
-// source read through DPP from the partner lane (k selects the pattern, as in
-// writer_partner). One asm block, so nothing is scheduled inside it; it
-// opens with two wait states, which a DPP read of a VGPR written by the
-// instruction just before it needs.
-#define TQ4_FMAC_DPP8(CTRL)                                                                      \
-    asm volatile("s_nop 1\n\t"                                                                   \
-                 "v_fmac_f32_dpp %0, %0, %8 " CTRL " row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t" \
-                 "v_fmac_f32_dpp %1, %1, %8 " CTRL " row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t" \
-                 "v_fmac_f32_dpp %2, %2, %8 " CTRL " row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t" \
-                 "v_fmac_f32_dpp %3, %3, %8 " CTRL " row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t" \
-                 "v_fmac_f32_dpp %4, %4, %8 " CTRL " row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t" \
-                 "v_fmac_f32_dpp %5, %5, %8 " CTRL " row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t" \
-                 "v_fmac_f32_dpp %6, %6, %8 " CTRL " row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t" \
-                 "v_fmac_f32_dpp %7, %7, %8 " CTRL " row_mask:0xf bank_mask:0xf bound_ctrl:1"     \
-                 : "+v"(x[0]), "+v"(x[1]), "+v"(x[2]), "+v"(x[3]), "+v"(x[4]), "+v"(x[5]),       \
-                   "+v"(x[6]), "+v"(x[7])                                                        \
-                 : "v"(c))
-
-__device__ __forceinline__ void fmac_partner8(float* x, float c, int k)
-{
-    switch (k) {
-        case 0: TQ4_FMAC_DPP8("quad_perm:[1,0,3,2]"); break;
-        case 1: TQ4_FMAC_DPP8("quad_perm:[2,3,0,1]"); break;
-        case 2: TQ4_FMAC_DPP8("row_half_mirror"); break;
-        default: TQ4_FMAC_DPP8("row_ror:8"); break;
-    }
-}
-#undef TQ4_FMAC_DPP8
-
-// One butterfly stage over the writer's two rows (key, value) in the writer
-// lane order (l: this lane's logical lane), on values held with a per-lane
-// sign: a lane stores w = sigma * v, sigma = (-1)^(number of logical lane
-// bits below the stage's that are set). In-register stages and the sign
-// diagonal commute with sigma. A cross-lane stage pairs lanes with the same
-// sigma; the butterfly
-//   out[i] = in[i ^ s] + ((i & s) ? -in[i] : in[i])
-// is then, on the stored values, w' = w + c * w_partner with c = -1 on the
-// upper lane and +1 on the lower (the upper lane's sigma flips): one
-// DPP-fed fused multiply-add per element. c * w_partner is exact, so the
-// one rounding is that of the reference's add or subtract.
+// One butterfly stage over the writer's two rows (key, value), l being this
+// lane's logical lane: in registers below CPL, else row_fmac_stage on the
+// sign-tracked values.
 template <int CPL>
 __device__ __forceinline__ void writer_butterfly(float (&v)[2][CPL], int stride, int l)
 {
@@ -240,23 +184,13 @@ __device__ __forceinline__ void writer_butterfly(float (&v)[2][CPL], int stride,
     } else {
         const int k = __builtin_ctz(stride / CPL);
         const float c = ((l >> k) & 1) ? -1.0f : 1.0f;
-        if constexpr (CPL >= 8) {
-#pragma unroll
-            for (int r = 0; r < 2; ++r) {
-#pragma unroll
-                for (int j = 0; j < CPL; j += 8) fmac_partner8(&v[r][j], c, k);
-            }
-        } else {
-            float x[8] = {v[0][0], v[0][1], v[0][2], v[0][3], v[1][0], v[1][1], v[1][2], v[1][3]};
-            fmac_partner8(x, c, k);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) v[0][j] = x[j], v[1][j] = x[4 + j];
-        }
+        row_fmac_stage<CPL>(v[0], c, k);
+        row_fmac_stage<CPL>(v[1], c, k);
     }
 }
 
 // Rotate both rows (strides 1..16, the sign diagonal, 32..D/2). The results
-// are held as sigma * v with sigma = (-1)^popcount(l) (writer_sigma).
+// are held as sigma * v with sigma = (-1)^popcount(l) (row_sigma).
 template <int D, int CPL>
 __device__ __forceinline__ void writer_rotate(float (&v)[2][CPL], const float (&sign)[CPL], int l)
 {
@@ -269,11 +203,6 @@ __device__ __forceinline__ void writer_rotate(float (&v)[2][CPL], const float (&
     }
 #pragma unroll
     for (int s = 32; s < D; s <<= 1) writer_butterfly<CPL>(v, s, l);
-}
-
-__device__ __forceinline__ float writer_sigma(int l)
-{
-    return (__builtin_popcount(l) & 1) ? -1.0f : 1.0f;
 }
 
 // Each row's absmax over its 16 lanes, starting from `floor` (1.0 for the
@@ -290,7 +219,7 @@ __device__ __forceinline__ void writer_absmax(const float (&v)[2][CPL], float fl
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
 #pragma unroll
-        for (int r = 0; r < 2; ++r) a[r] = fmaxf(a[r], writer_partner(a[r], k));
+        for (int r = 0; r < 2; ++r) a[r] = fmaxf(a[r], row_partner(a[r], k));
     }
 }
 
@@ -307,7 +236,7 @@ __device__ __forceinline__ void writer_rotate_quantise(float (&v)[2][CPL], const
     writer_absmax<CPL>(v, 1.0f, a);
     // the stored values are sigma * v: the quantiser's exact power of two
     // carries sigma
-    const float sigma = writer_sigma(l);
+    const float sigma = row_sigma(l);
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
         // a >= 1 (the prefill floor; NaN never wins fmaxf): the exponent
@@ -363,7 +292,7 @@ __global__ __launch_bounds__(kWriterThreads) void strip_writer(
     const uint32_t strip = blockIdx.x, head = blockIdx.y;
     const int tid = threadIdx.x;
     const int row = tid >> 4;                 // token within the strip
-    const int l = writer_lane(tid & 15);      // logical lane: channels l*CPL ..
+    const int l = row_lane(tid & 15);      // logical lane: channels l*CPL ..
 
     // slots first, then the rows and the signs: one round trip for all
     const int32_t slot0 = slots[(size_t)strip * kStrip];
@@ -569,7 +498,7 @@ __global__ __launch_bounds__(kWriterThreads) void scatter_token_writer(
     constexpr int NW = 2 * CPL;  // strip words of a lane's channels
     const int tid = threadIdx.x;
     const int grp = tid >> 4;
-    const int l = writer_lane(tid & 15);  // logical lane: channels l*CPL ..
+    const int l = row_lane(tid & 15);  // logical lane: channels l*CPL ..
 
     if (probe != nullptr && blockIdx.x == 0 && tid < 32) {
         const int32_t fields[4] = {0, (int32_t)probe_grid, 1, (int32_t)item_count};
@@ -578,7 +507,7 @@ __global__ __launch_bounds__(kWriterThreads) void scatter_token_writer(
 
     float sign[CPL];
     load_signs<CPL>(pi_signs, nullptr, 0, l * CPL, sign);
-    const float sigma = writer_sigma(l);
+    const float sigma = row_sigma(l);
     auto one = [&](uint32_t request, uint32_t head) {
         if (request >= num_requests) return;
         // The rows do not depend on the slot: their loads go out with its
