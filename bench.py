@@ -33,7 +33,7 @@ process may run on, each on a bounded sample of the row's workload.
 Usage:
   python bench.py [--gpus 1] [--steps K] [--warmup W]
   python bench.py --pmc-run              # workload for rocprofv3 --pmc passes
-  python bench.py --summarize-pmc DIR    # DIR/<row>/<pass>/run_counter_collection.csv
+  python bench.py --summarize-pmc DIR [--pmc-merge]  # DIR/<row>/<pass>/run_counter_collection.csv
   python bench.py --pmc-table            # the committed summary as markdown
   python bench.py --summarize-trace DIR  # a rocprofv3 --kernel-trace csv run
 """
@@ -211,7 +211,7 @@ def roofline(nbytes, ms, kernel, pmc=None):
             "traffic_source": "profiles/pmc_summary.json" if "traffic_bytes" in t else None}
 
 
-def summarize_pmc(root):
+def summarize_pmc(root, merge=False):
     """Mean counter value per dispatch of each profiled row: root/<row>/<pass>/
     run_counter_collection.csv (rocprofv3 --output-format csv) over the passes
     of `bench.py --pmc-run <row>`; the row's dispatches are those of its
@@ -263,6 +263,10 @@ def summarize_pmc(root):
         out[row] = e
     if not out:
         raise SystemExit(f"no profiled rows under {root}")
+    if merge and os.path.exists(PMC_FILE):
+        # a re-run of some rows: the others keep their committed figures
+        with open(PMC_FILE) as f:
+            out = {**json.load(f), **out}
     os.makedirs(os.path.dirname(PMC_FILE), exist_ok=True)
     with open(PMC_FILE, "w") as f:
         json.dump(out, f, indent=1)
@@ -565,6 +569,8 @@ def main():
                          "stamps (libtq4_stamps.so), the split tail delta, and the host enqueue "
                          "cost of one decode call")
     ap.add_argument("--summarize-pmc", metavar="DIR")
+    ap.add_argument("--pmc-merge", action="store_true",
+                    help="with --summarize-pmc: keep the committed rows not under DIR")
     ap.add_argument("--pmc-table", action="store_true",
                     help="print the committed PMC summary as markdown")
     ap.add_argument("--summarize-trace", metavar="DIR")
@@ -573,7 +579,7 @@ def main():
     args = ap.parse_args()
 
     if args.summarize_pmc:
-        summarize_pmc(args.summarize_pmc)
+        summarize_pmc(args.summarize_pmc, merge=args.pmc_merge)
         return
     if args.pmc_table:
         with open(PMC_FILE) as f:
@@ -759,10 +765,10 @@ def pmc_kernel_of(row):
     """(kernel-name fragment, workgroups or None) of a PMC row's dispatches."""
     fixed = {"configs2_decode": ("decode_kernel<128, 1>", B * HKV * 16),
              "configs4_step_scatter": ("scatter_token_writer<128>", None),
-             "configs1_writer": ("strip_writer<128, unsigned short, 1>", 512),
+             "configs1_writer": ("strip_writer<128, unsigned short>", 512),
              "configs1_scatter": ("scatter_token_writer<128>", None),
              "rms_writer": ("rms_writer<128, 1>", None),
-             "configs0_a8": ("strip_writer<128, signed char, 1>", None),
+             "configs0_a8": ("strip_writer<128, signed char>", None),
              "kv4_ref_shape": ("kv4_decode_kernel", None), "kv4_batched": ("kv4_decode_kernel", None),
              "codebook_lloyd": ("quantize_kernel", None), "codebook_icdf": ("icdf_kernel", None)}
     if row in fixed:
