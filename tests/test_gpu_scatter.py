@@ -61,6 +61,45 @@ def test_decode_step_single_tokens(tq4, oracle, d):
     assert_same(got, want)
 
 
+@pytest.mark.parametrize("d", [64, 128, 256])
+def test_single_tokens_zero_pad_wide_rows(tq4, oracle, d):
+    """The one-token writer (cu_seqlens NULL) on random prior bytes: an
+    all-zero key and value row (codes 0, scale 1.0), slot -1 pads, a slot past
+    the pool, and rows scaled by 2^k, k in [-60, 60] (the exact policy's
+    exponent far below the prefill floor)."""
+    rng = np.random.default_rng(0x5CA7 + d)
+    R, H, S, P = 48, 4, 32, 64
+    slots = strip_disjoint_slots(rng, R, P, S)
+    slots[5] = -1
+    slots[17] = -1
+    slots[30] = P * S + 3  # past the pool
+    k = rng.integers(-60, 61, (2, R, H, 1)).astype(np.float64)
+    x = rng.standard_normal((2, R, H, d)) * np.exp2(k)
+    key, val = (f32_to_bf16(x[i].astype(np.float32)) for i in range(2))
+    key[9] = 0
+    val[9] = 0
+    nb = P * H * S * d // 2
+    prior = (rng.integers(-128, 128, nb, dtype=np.int8), rng.integers(-128, 128, nb, dtype=np.int8),
+             rng.standard_normal(2 * P * H * S).astype(np.float32))
+    got, want = scatter_pair(tq4, oracle, key, val, slots, None, R, H, d, S, P, prior=prior)
+    assert_same(got, want)
+
+
+def test_single_tokens_item_window_past_2_32(tq4, oracle):
+    """An item window reaching past 2^32 (the writer's 64-bit item loop):
+    every item there belongs to no request, so nothing is written."""
+    R, H, d, S, P = 8, 4, 128, 16, 16
+    rng = np.random.default_rng(32)
+    slots = strip_disjoint_slots(rng, R, P, S)
+    key = f32_to_bf16(rng.standard_normal((R, H, d)).astype(np.float32))
+    val = f32_to_bf16(rng.standard_normal((R, H, d)).astype(np.float32))
+    got, want = scatter_pair(tq4, oracle, key, val, slots, None, R, H, d, S, P,
+                             item_begin=0xFFFFFF00, item_count=0x200)
+    assert_same(got, want)
+    nb = P * H * S * d // 2
+    assert np.array_equal(got[0].view(np.uint8), canary_bytes(nb).view(np.uint8))
+
+
 def test_runs_pads_zero_rows_and_preservation(tq4, oracle):
     """Runs that cross strips, slot -1 pads, an all-zero row, random prior bytes."""
     rng = np.random.default_rng(9)
