@@ -52,7 +52,8 @@ int writer_checks(const void* key, const void* value, const int8_t* key_cache,
         return TQ4_ERR_NULL_POINTER;
     if (!pi_signs && !tables) return TQ4_ERR_ROTATION;
     const uint64_t blocks = (uint64_t)(num_tokens / kStrip) * num_kv_heads * 2u;
-    if (blocks > 0x7fffffffull) return TQ4_ERR_RANGE;
+    // the strip writer's grid is (strips, kv heads): at most 65535 heads
+    if (blocks > 0x7fffffffull || num_kv_heads > 65535u) return TQ4_ERR_RANGE;
     return TQ4_OK;
 }
 

@@ -70,6 +70,8 @@ uint32_t tq4_version(void);
  * num_tokens must be a whole number of tokens_per_core strips
  * (TQ4_ERR_PARTIAL_STRIP otherwise), tokens_per_core a multiple of 16; it is
  * accepted for signature compatibility, the grid is chosen here.
+ * num_kv_heads <= 65535 and 2 * num_tokens / 16 * num_kv_heads < 2^31
+ * (TQ4_ERR_RANGE otherwise).
  * Rotation signs: pi_signs (float[head_size] of +-1) when non-NULL, else the
  * first column of `tables` (the reference's 2*(d/32) row-major 32x32 INT8
  * blocks, T[0][g][c0][0] = sign[g*32+c0]). reuse_mode4_flags selects an

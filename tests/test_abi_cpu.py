@@ -51,6 +51,7 @@ def test_writer_refusals(lib):
     assert f(*args(32, 2, 128, 16, 4, 24)) == -4         # tokens_per_core % 16
     assert f(*args(16, 2, 128, 16, 4, 16, None)) == -8   # no rotation operand
     assert f(*args(0, 2, 128, 16, 4, 16)) == 0           # nothing to do
+    assert f(*args(16, 65536, 128, 16, 4, 16)) == -10    # more heads than the grid's y
     g = lib.tq4_reshape_and_cache_bf16
     assert g(None, None, dummy, dummy, dummy, dummy, dummy, dummy, None, 16, 2, 128, 16, 4, 16,
              0.1, True) == -1                            # NULL key
