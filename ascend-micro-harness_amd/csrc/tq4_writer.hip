@@ -157,8 +157,9 @@ __device__ __forceinline__ void store_key_codes(int8_t* dst, const int (&q)[CPL]
 //   so codes pack with one shift-or per pair and byte permutes, and the
 //   packed word is XORed with 0x8...8 to give the two's-complement nibbles.
 //   Non-finite inputs saturate: +inf and NaN give 7, -inf gives -8.
-// * One barrier: the slot vote and the value-strip transpose share it; the
-//   rotation runs while the slot loads are in flight.
+// * One barrier: the slot vote and the value-strip transpose share it. The
+//   slot loads go out first, ahead of the rows they do not depend on, so
+//   their round trip is the rows' round trip.
 
 constexpr float kQMagic = 12582920.0f;     // 1.5 * 2^23 + 8
 constexpr float kQMagicTop = 12582927.0f;  // kQMagic + 7
