@@ -88,6 +88,24 @@ def decode_algorithmic_bytes(ctx_lens, hq, hkv, d, s):
     return kv + tables + qo + 4 * len(ctx_lens)
 
 
+def decode_overhead_bytes(ctx_lens, hq, hkv, d, s, splits, max_blocks):
+    """Workspace traffic of one fused decode, kept out of the algorithmic
+    bytes: for each (seq, kv head) with more than one live split, the split
+    records [m, l, 0, 0, acc[d]] of its q heads, stored by every live split
+    but the combiner and loaded and zeroed by the combiner:
+    (3 k_live - 1) x G x (d + 4) x 4 bytes."""
+    if splits <= 1:
+        return 0
+    g = hq // hkv
+    width = -(-max_blocks // splits)
+    total = 0
+    for c in ctx_lens:
+        k_live = -(-(-(-c // s)) // width)
+        if k_live > 1:
+            total += hkv * (3 * k_live - 1) * g * (d + 4) * 4
+    return total
+
+
 def writer_algorithmic_bytes(tokens, hkv, d, in_bytes):
     """Inputs read + packed nibbles + scales written + slot mapping read."""
     return tokens * (2 * hkv * d * in_bytes + hkv * d + 2 * hkv * 4 + 4)
@@ -678,6 +696,7 @@ def main():
                       "warm": round(warm["ms"] * 1e3, 3), "warm_spread": warm["spread"]},
         "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
         "roofline": roofline(dec_bytes, cold_ms, "configs2_decode", pmc),
+        "overhead_bytes": decode_overhead_bytes([CTX], HQ, HKV, D, S, w.splits, PAGES),
         "launch_floor_note": "a back-to-back graph launch of an empty kernel of 128 workgroups "
                              "costs about 1.7 us; one launch moving 4.47 MB therefore tops "
                              "out near 33 % of peak",
@@ -1051,7 +1070,10 @@ def extra_workloads(tq4, torch, dev, w, pmc, cpu=True):
            "splits": bats[0].K, "auto_splits": True, "algorithmic_bytes": sbytes,
            "cache": "cold (2 batches of 0.3 GB rotated)",
            "decode_only": {**row_times(resd), "GBps": round(dbytes / (resd["ms"] * 1e-3) / 1e9, 2),
-                           "algorithmic_bytes": dbytes},
+                           "algorithmic_bytes": dbytes,
+                           "overhead_bytes": decode_overhead_bytes(
+                               [c + 1 for c in bats[0].ctxs], HQ, HKV, D, S, bats[0].K,
+                               bats[0].tables.shape[1])},
            "roofline": roofline(dbytes, resd["ms"], "configs4_decode", pmc),
            "poll_timeouts": t_step}
     if t_step:
@@ -1228,7 +1250,9 @@ def split_sweep(tq4, torch, dev, w, orc=None, pmc=None):
             gbs = nbytes / (r["ms"] * 1e-3) / 1e9
             row = {"ctx": ctx, "splits": kk, "auto": k == 0, **row_times(r),
                    "GBps": round(gbs, 1), "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
-                   "algorithmic_bytes": nbytes, "poll_timeouts": timeouts,
+                   "algorithmic_bytes": nbytes,
+                   "overhead_bytes": decode_overhead_bytes([ctx], HQ, HKV, D, S, kk, pages),
+                   "poll_timeouts": timeouts,
                    "roofline": roofline(nbytes, r["ms"], sweep_row(ctx, k or "auto"), pmc)}
             if timeouts:
                 row["INVALID"] = f"{timeouts} combine rows gave up their bounded poll"

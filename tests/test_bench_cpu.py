@@ -104,3 +104,17 @@ def test_trace_summary_limits_per_kernel_and_grid(tmp_path, capsys):
     cells = [c.strip() for c in line.strip("|").split("|")]
     assert cells[1] == "8" and cells[2] == "4"  # 4 x 2 workgroups, 4 dispatches kept
     assert float(cells[3]) == pytest.approx(9.5)
+
+
+def test_decode_overhead_bytes_closed_form():
+    """The workspace traffic reported beside the algorithmic bytes: (3 k_live
+    - 1) records of (d + 4) floats per q head of every (seq, kv head) with
+    more than one live split; none for a single split or a short sequence."""
+    import bench
+    rec = (128 + 4) * 4
+    # configs[2]: 16 live splits, 8 kv heads x 4 q heads
+    assert bench.decode_overhead_bytes([4096], 32, 8, 128, 16, 16, 256) == 8 * 47 * 4 * rec
+    assert bench.decode_overhead_bytes([4096], 32, 8, 128, 16, 1, 256) == 0
+    # a sequence inside the first split's window, and one reaching three splits
+    assert bench.decode_overhead_bytes([100, 2 * 16 * 16 + 1], 32, 8, 128, 16, 16, 256) == \
+        8 * (3 * 3 - 1) * 4 * rec
