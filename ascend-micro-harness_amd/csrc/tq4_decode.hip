@@ -25,13 +25,15 @@
 //     T2 the same token + 4 -- chosen so that the score tile leaves each lane
 //     holding exactly the 8 consecutive tokens whose value nibbles form ONE
 //     dword of the channel-major value strip.
-//   * nibbles decode to fp16 (1 + u/64), u = nibble ^ 8, with one and-or per
-//     pair of codes (no conversion instruction); the MFMA accumulator starts
-//     at -1.125 * sum(q), which removes the offset, so the product is
-//     sum(q * nibble) / 64.
+//   * key nibbles decode to normal fp16 (1 + u/64 or 16 + u/64), u = nibble
+//     ^ 8, one bitop3 per pair of codes (no conversion instruction); the
+//     MFMA accumulator starts at -sum(q * offset), which removes the
+//     offsets, so the product is sum(q * nibble) / 64.
+//   * value nibbles decode to fp16 subnormals (u * 2^-24 or u * 2^-20, no
+//     implicit 1), the same one bitop3 per pair of codes.
 //   * the score tile IS the A operand of P.V (same lane, same token order),
 //     so P never leaves the lane; O += P.V per 16-channel block, plus one
-//     MFMA against a constant 1.125 column that tracks the value offset.
+//     MFMA against a constant column that tracks the values' +8.
 //   * softmax in the exp2 domain with a lazy maximum: the running maximum
 //     moves only when a score exceeds it by more than 2^8 (or a value scale
 //     outgrows the fp16 headroom), so the accumulator rescale -- the only
@@ -98,11 +100,14 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr uint32_t kNib = 0x00F000F0u;   // a code at fp16 mantissa bits [7:4], both halves
 constexpr uint32_t kCodeBase = 0x3C803C80u;  // fp16 1.0 outside kNib; the nibble sign bit inside
-constexpr float kCodeOffset = 1.125f;    // fp16 code value is 1 + u/64 = 1.125 + n/64
-constexpr uint32_t kNibLo = 0x000F000Fu;     // a key code at fp16 mantissa bits [3:0], both halves
+constexpr float kCodeOffset = 1.125f;    // fp16 key code value is 1 + u/64 = 1.125 + n/64
+constexpr uint32_t kNibLo = 0x000F000Fu;     // a code at fp16 mantissa bits [3:0], both halves
 constexpr uint32_t kCodeBaseLo = 0x4C084C08u;  // fp16 16.0 outside kNibLo; the nibble sign bit inside
 constexpr float kCodeOffsetLo = 16.125f;     // fp16 key code value is 16 + u/64 = 16.125 + n/64
-constexpr float kCodeUnit = 64.0f;
+constexpr float kKeyUnit = 64.0f;            // key codes step 1/64 (score units)
+constexpr uint32_t kValBase = 0x00800080u;   // exponent 0: the nibble at [7:4] is u * 2^-20
+constexpr uint32_t kValBaseLo = 0x00080008u; // exponent 0: the nibble at [3:0] is u * 2^-24
+constexpr float kValueUnit = 16777216.0f;    // value codes step 2^-24 (product units)
 constexpr float kTau = 8.0f;             // lazy-maximum headroom, log2 units
 constexpr float kShiftLimit = 100.0f;    // bound of a row's product normalisation shift
 constexpr float kXLimit = 32768.0f;      // a normalised product at or above this rescales (fp16 max 65504)
@@ -126,25 +131,32 @@ __device__ __forceinline__ int fresh_tid()
     return t;
 }
 
-// Eight codes of one dword as fp16 (1 + u/64), u = nibble ^ 8; halves in
-// nibble order 0,4,1,5,2,6,3,7 (every operand built against this table uses
-// that order). Each pair is one v_bitop3: kNib ? (bits ^ kCodeBase) :
-// kCodeBase (truth table 0x6A over S0 = bits, S1 = kNib, S2 = kCodeBase),
-// i.e. the nibble with its sign bit flipped under an fp16 1.0.
-__device__ __forceinline__ h8_t codes8(uint32_t w)
+// Eight value codes of one dword as fp16 subnormals, u = nibble ^ 8 (the
+// code plus 8); halves in nibble order 0,4,1,5,2,6,3,7 (every operand built
+// against this table uses that order). Each pair is one v_bitop3:
+// (bits & mask) ^ base, truth table 0x6A over S0 = bits, S1 = mask, S2 =
+// base, the base flipping the nibble's sign bit under a zero exponent. Under
+// a zero exponent there is no implicit leading 1, so the only offset is the
+// code's +8: nibbles 1,5 and 3,7 sit at mantissa bits [7:4] and are u *
+// 2^-20, nibbles 0,4 and 2,6 at bits [3:0] are u * 2^-24 -- the caller
+// builds the odd nibbles' A operands with 2^-4 in their exponent, so every
+// product is P'vs * u * 2^-24.
+__device__ __forceinline__ h8_t value_codes8(uint32_t w)
 {
-    const uint32_t p04 = __builtin_amdgcn_bitop3_b32(w << 4, kNib, kCodeBase, 0x6A);
-    const uint32_t p15 = __builtin_amdgcn_bitop3_b32(w, kNib, kCodeBase, 0x6A);
-    const uint32_t p26 = __builtin_amdgcn_bitop3_b32(w >> 4, kNib, kCodeBase, 0x6A);
-    const uint32_t p37 = __builtin_amdgcn_bitop3_b32(w >> 8, kNib, kCodeBase, 0x6A);
+    const uint32_t w8 = w >> 8;
+    const uint32_t p04 = __builtin_amdgcn_bitop3_b32(w, kNibLo, kValBaseLo, 0x6A);
+    const uint32_t p15 = __builtin_amdgcn_bitop3_b32(w, kNib, kValBase, 0x6A);
+    const uint32_t p26 = __builtin_amdgcn_bitop3_b32(w8, kNibLo, kValBaseLo, 0x6A);
+    const uint32_t p37 = __builtin_amdgcn_bitop3_b32(w8, kNib, kValBase, 0x6A);
     return __builtin_bit_cast(h8_t, u4_t{p04, p15, p26, p37});
 }
 
-// The key side of codes8 with one shift instead of three: the halves of
-// nibbles 0,4 and 2,6 sit at mantissa bits [3:0] under an fp16 16.0, so
-// their value is 16 + u/64 (the same step as 1 + u/64 at bits [7:4]). The
-// score's start value removes both offsets; they cancel inside each pair's
-// score, so the larger one costs nothing that accumulates across the split.
+// Eight key codes of one dword as normal fp16, in the same nibble order and
+// with the same one shift: nibbles 1,5 and 3,7 at mantissa bits [7:4] under
+// an fp16 1.0 are 1 + u/64, nibbles 0,4 and 2,6 at bits [3:0] under an fp16
+// 16.0 are 16 + u/64 (the same step). The score's start value removes both
+// offsets; they cancel inside each pair's score, so the larger one costs
+// nothing that accumulates across the split.
 __device__ __forceinline__ h8_t key_codes8(uint32_t w)
 {
     const uint32_t w8 = w >> 8;
@@ -448,10 +460,11 @@ __host__ __device__ constexpr size_t region_floats(uint32_t G, uint32_t D)
 template <int D>
 struct RowState {
     f4_t acc[D / 16];
-    f4_t cr;       // offset column: 1.125 * sum P'vs per row
+    f4_t cr;       // offset column: 8 * 2^-24 * sum P'vs per row
     float m_used;  // the row maximum in use (log2 units)
     float smax;    // partials only: this lane's exact maximum score (log2 units)
     float sh, mo, lpart, thr;
+    float mo4;     // mo + 4: the odd tokens' exponent offset (value_codes8)
     bool virgin;   // no rescale yet in this stream (wave-uniform)
 
     __device__ __forceinline__ void reset(bool row_live)
@@ -466,15 +479,17 @@ struct RowState {
         smax = -INFINITY;
         sh = 0.0f;
         mo = row_live ? 0.0f : INFINITY;
+        mo4 = mo + 4.0f;
         lpart = 0.0f;
         thr = row_live ? -INFINITY : kTau;
         virgin = true;
     }
 };
 
-// This lane's B operands (q head n, channels g4*d/4 ..) in the codes8
-// channel order, the MFMA start value that removes the code offset, and the
-// score factor 64 * log2(e) * 2^q_exp.
+// This lane's B operands (q head n, channels g4*d/4 ..) in the key_codes8
+// channel order, the MFMA start value that removes the code offsets, and the
+// score factor 64 * log2(e) * 2^q_exp (1 for a padded row, whose scores the
+// infinite mo silences: a factor of 0 would make 0 * -inf of a dead token).
 template <int D>
 struct QOps {
     h8_t qop[D / 32];
@@ -498,8 +513,11 @@ __device__ __forceinline__ void process_pair(RowState<D>& st, const QOps<D>& qo,
     constexpr int NJ = D / 32;
     constexpr int NB = D / 16;
     const int half = (lane >> 4) & 1, sp = lane >> 5;
-    const _Float16 off16 = (_Float16)kCodeOffset;
-    const h8_t offset_col = h8_t{off16, off16, off16, off16, off16, off16, off16, off16};
+    // the value codes' +8 in each slot's unit (value_codes8): 8 * 2^-24 for
+    // nibbles 0,4,2,6, 8 * 2^-20 for the odd nibbles, whose P' carries 2^-4
+    // -- so the column sums 8 * 2^-24 * P'vs over the row
+    const _Float16 oe = (_Float16)0x1p-21f, oo = (_Float16)0x1p-17f;
+    const h8_t offset_col = h8_t{oe, oe, oo, oo, oe, oe, oo, oo};
     f4_t c1 = qo.bias4, c2 = qo.bias4;
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
@@ -523,30 +541,36 @@ __device__ __forceinline__ void process_pair(RowState<D>& st, const QOps<D>& qo,
 #pragma unroll
         for (int i = 0; i < 8; ++i) live[i] = true;
     }
-    // scores (log2 units) and value scales; a dead token is overwritten
-    float sc8[8], vs[8];
+    // raw scores (the row's factor cf > 0 turns them into log2 units inside
+    // each exponent's FMA) and value scales; a dead token is overwritten
+    float sr[8], vs[8];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        sc8[i] = live[i] ? c1[i] * (qo.cf * ks1[i]) : -INFINITY;
-        sc8[4 + i] = live[4 + i] ? c2[i] * (qo.cf * ks2[i]) : -INFINITY;
+        sr[i] = live[i] ? c1[i] * ks1[i] : -INFINITY;
+        sr[4 + i] = live[4 + i] ? c2[i] * ks2[i] : -INFINITY;
         vs[i] = live[i] ? vs1[i] : 0.0f;
         vs[4 + i] = live[4 + i] ? vs2[i] : 0.0f;
     }
     // Rescale when a score passes the lazy maximum by kTau, or when a
     // product could reach kXLimit: exp2(tmax) * vmax bounds every
     // product (one exp per lane; the products themselves are formed
-    // after the branch, so nothing of them stays live across it).
-    float tmax = -INFINITY, vmax = 0.0f;
+    // after the branch, so nothing of them stays live across it). cf > 0,
+    // so cf times the largest raw score is the largest score.
+    float rmax = -INFINITY, vmax = 0.0f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        tmax = fmaxf(tmax, sc8[i]);
+        rmax = fmaxf(rmax, sr[i]);
         vmax = fmaxf(vmax, vs[i]);
     }
-    if constexpr (EXACT) st.smax = fmaxf(st.smax, tmax);
-    tmax -= st.mo;  // a live row's mo is finite; a padded row's is +inf
+    if constexpr (EXACT) st.smax = fmaxf(st.smax, qo.cf * rmax);
+    // a live row's mo is finite; a padded row's is +inf
+    const float tmax = fmaf(qo.cf, rmax, -st.mo);
     if (__builtin_expect(
             __any(tmax > st.thr || __builtin_amdgcn_exp2f(tmax) * vmax >= kXLimit), 0)) {
         // Move the row maximum and re-normalise the row's products.
+        float sc8[8];  // scores, log2 units
+#pragma unroll
+        for (int i = 0; i < 8; ++i) sc8[i] = qo.cf * sr[i];
         float smax = -INFINITY;
 #pragma unroll
         for (int i = 0; i < 8; ++i) smax = fmaxf(smax, sc8[i]);
@@ -566,6 +590,7 @@ __device__ __forceinline__ void process_pair(RowState<D>& st, const QOps<D>& qo,
                 shn = fminf(fmaxf(-(float)exponent_of(ymax), -kShiftLimit), kShiftLimit);
             st.m_used = mn;
             st.mo = mn - shn;
+            st.mo4 = st.mo + 4.0f;
             st.sh = shn;
             st.thr = kTau + shn;
             st.virgin = false;
@@ -604,6 +629,7 @@ __device__ __forceinline__ void process_pair(RowState<D>& st, const QOps<D>& qo,
             }
             st.m_used = mn;
             st.mo = mon;
+            st.mo4 = mon + 4.0f;
             st.sh = shn;
             st.thr = kTau + shn;
         }
@@ -614,11 +640,14 @@ __device__ __forceinline__ void process_pair(RowState<D>& st, const QOps<D>& qo,
     float pr[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        pr[i] = __builtin_amdgcn_exp2f(sc8[i] - st.mo);
+        // an odd token's code unit is 16 times an even one's
+        // (value_codes8): its P' carries 2^-4, and counts 16 times in l
+        pr[i] = __builtin_amdgcn_exp2f(fmaf(qo.cf, sr[i], (i & 1) ? -st.mo4 : -st.mo));
         x[i] = (_Float16)(pr[i] * vs[i]);
     }
-    st.lpart += ((pr[0] + pr[1]) + (pr[2] + pr[3])) + ((pr[4] + pr[5]) + (pr[6] + pr[7]));
-    // A operand in the codes8 token order: (T1[0], T2[0], T1[1], T2[1], ...)
+    st.lpart += (fmaf(16.0f, pr[1], pr[0]) + fmaf(16.0f, pr[3], pr[2])) +
+                (fmaf(16.0f, pr[5], pr[4]) + fmaf(16.0f, pr[7], pr[6]));
+    // A operand in the value_codes8 token order: (T1[0], T2[0], T1[1], T2[1], ...)
     const h8_t P = h8_t{x[0], x[4], x[1], x[5], x[2], x[6], x[3], x[7]};
     // B operands: block b = 4q + 2hb + e is channel n*d/16 + b. The lane
     // pair (half 0, half 1) swaps so each holds its own 8-token half:
@@ -631,8 +660,8 @@ __device__ __forceinline__ void process_pair(RowState<D>& st, const QOps<D>& qo,
         for (int e = 0; e < 2; ++e) {
             const auto sw = __builtin_amdgcn_permlane16_swap(r.v[4 * q + 2 * e],
                                                              r.v[4 * q + 2 * e + 1], false, false);
-            st.acc[4 * q + e] = mfma32(P, codes8(sw[0]), st.acc[4 * q + e]);
-            st.acc[4 * q + 2 + e] = mfma32(P, codes8(sw[1]), st.acc[4 * q + 2 + e]);
+            st.acc[4 * q + e] = mfma32(P, value_codes8(sw[0]), st.acc[4 * q + e]);
+            st.acc[4 * q + 2 + e] = mfma32(P, value_codes8(sw[1]), st.acc[4 * q + 2 + e]);
         }
     }
     st.cr = mfma32(P, offset_col, st.cr);
@@ -690,7 +719,7 @@ __device__ __forceinline__ void build_qops(QOps<D>& qo, const float* q_st, const
     const int n = lane & 15, g4 = lane >> 4;
     qo.row_live = (uint32_t)n < G;
     float bias = 0.0f;  // sum of q times each key_codes8 half's offset (negated below)
-    qo.cf = 0.0f;
+    qo.cf = 1.0f;
     if (qo.row_live) {
         const float* qrow = q_st + n * kQRow<D> + g4 * (D / 4);
 #pragma unroll
@@ -704,7 +733,7 @@ __device__ __forceinline__ void build_qops(QOps<D>& qo, const float* q_st, const
             for (int e = 0; e < 8; ++e)
                 bias += (float)h[e] * ((e & 2) == 0 ? kCodeOffsetLo : kCodeOffset);
         }
-        qo.cf = ldexpf(kCodeUnit * kLog2e, q_exp[n]);
+        qo.cf = ldexpf(kKeyUnit * kLog2e, q_exp[n]);
     } else {
 #pragma unroll
         for (int j = 0; j < NJ; ++j) qo.qop[j] = h8_t{0, 0, 0, 0, 0, 0, 0, 0};
@@ -817,7 +846,7 @@ __device__ __forceinline__ void finish_item(const DecodeParams& p, uint32_t seq,
 #pragma unroll
         for (int w = 0; w < kWaves; ++w) {
             const float4 x = *(const float4*)(part + (size_t)w * G * D + 4 * e4);
-            const float fw = f[w] * kCodeUnit;
+            const float fw = f[w] * kValueUnit;
             v.x += x.x * fw;
             v.y += x.y * fw;
             v.z += x.z * fw;
