@@ -87,6 +87,42 @@ __device__ __forceinline__ float row_partner(float v, int k)
     return __int_as_float(r);
 }
 
+// v = OP(v, v at logical lane l ^ (1 << k)) for two values (row_max2: max,
+// row_add1: sum), the partner read through DPP by the operation itself: one
+// instruction per value instead of a DPP move plus the operation (plus, for
+// fmaxf, a canonicalisation of the moved value). Each block opens with the two
+// wait states a DPP read of a VGPR written just before it needs; a max or a
+// sum of two finite or infinite floats returns the same bits either way.
+#define TQ4_DPP_OP(OP, I, CTRL) \
+    "v_" OP "_f32_dpp %" #I ", %" #I ", %" #I " " CTRL " row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+#define TQ4_MAX_DPP2(CTRL) \
+    asm volatile("s_nop 1\n\t" TQ4_DPP_OP("max", 0, CTRL) TQ4_DPP_OP("max", 1, CTRL) \
+                 : "+v"(a0), "+v"(a1))
+#define TQ4_ADD_DPP1(CTRL) asm volatile("s_nop 1\n\t" TQ4_DPP_OP("add", 0, CTRL) : "+v"(a0))
+
+__device__ __forceinline__ void row_max2(float& a0, float& a1, int k)
+{
+    switch (k) {
+        case 0: TQ4_MAX_DPP2("quad_perm:[1,0,3,2]"); break;
+        case 1: TQ4_MAX_DPP2("quad_perm:[2,3,0,1]"); break;
+        case 2: TQ4_MAX_DPP2("row_half_mirror"); break;
+        default: TQ4_MAX_DPP2("row_ror:8"); break;
+    }
+}
+
+__device__ __forceinline__ void row_add1(float& a0, int k)
+{
+    switch (k) {
+        case 0: TQ4_ADD_DPP1("quad_perm:[1,0,3,2]"); break;
+        case 1: TQ4_ADD_DPP1("quad_perm:[2,3,0,1]"); break;
+        case 2: TQ4_ADD_DPP1("row_half_mirror"); break;
+        default: TQ4_ADD_DPP1("row_ror:8"); break;
+    }
+}
+#undef TQ4_ADD_DPP1
+#undef TQ4_MAX_DPP2
+#undef TQ4_DPP_OP
+
 // w += c * w[logical lane l ^ (1 << k)] for 8 (or 4) values: v_fmac_f32 with
 // its first source read through DPP. One asm block, so nothing is scheduled
 // inside it; it opens with the two wait states that a DPP read of a VGPR

@@ -169,7 +169,7 @@ __global__ __launch_bounds__(kRmsThreads) void rms_writer(
 #pragma unroll
     for (int j = 1; j < CPL; ++j) ss = ss + v[j] * v[j];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) ss = ss + row_partner(ss, k);
+    for (int k = 0; k < 4; ++k) row_add1(ss, k);
     const float scale = sqrt_rn(ss) * inv_sqrt_len + kRmsEps;
     // sigma rides on the reciprocal: (sigma y) * (sigma r) rounds as y * r
     const float rcp = row_sigma(l) * __fdiv_rn(1.0f, scale);

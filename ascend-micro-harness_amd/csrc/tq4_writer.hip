@@ -218,10 +218,7 @@ __device__ __forceinline__ void writer_absmax(const float (&v)[2][CPL], float fl
         for (int j = 0; j < CPL; ++j) a[r] = fmaxf(a[r], fabsf(v[r][j]));
     }
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-#pragma unroll
-        for (int r = 0; r < 2; ++r) a[r] = fmaxf(a[r], row_partner(a[r], k));
-    }
+    for (int k = 0; k < 4; ++k) row_max2(a[0], a[1], k);
 }
 
 // Rotate both rows, take each row's absmax (prefill policy: floored at 1.0)
