@@ -36,6 +36,8 @@ Usage:
   python bench.py --summarize-pmc DIR [--pmc-merge]  # DIR/<row>/<pass>/run_counter_collection.csv
   python bench.py --pmc-table            # the committed summary as markdown
   python bench.py --summarize-trace DIR  # a rocprofv3 --kernel-trace csv run
+  python bench.py --phases               # configs[2] phase timeline (libtq4_stamps.so)
+  python bench.py --floor                # compute-free floors (libtq4_floor.so)
 """
 from __future__ import annotations
 
@@ -586,6 +588,9 @@ def main():
                     help="configs[2] per-phase timeline from the measurement build's in-kernel "
                          "stamps (libtq4_stamps.so), the split tail delta, and the host enqueue "
                          "cost of one decode call")
+    ap.add_argument("--floor", action="store_true",
+                    help="compute-free copies of the configs[2] decode chain and the configs[1] "
+                         "writer traffic (libtq4_floor.so) beside the real kernels")
     ap.add_argument("--summarize-pmc", metavar="DIR")
     ap.add_argument("--pmc-merge", action="store_true",
                     help="with --summarize-pmc: keep the committed rows not under DIR")
@@ -631,6 +636,9 @@ def main():
         return
     if args.phases:
         phases(tq4, torch, dev)
+        return
+    if args.floor:
+        floor(tq4, torch, dev)
         return
 
     log(f"prefilling {SLICES} config-3 sequences ({SLICES * PAGES} pages)")
@@ -768,6 +776,97 @@ def phases(tq4, torch, dev, samples=64):
            "samples": samples, "workgroups": int(nblk), "library": "libtq4_stamps.so",
            "clock": "s_memrealtime, 100 MHz"}
     print(json.dumps(res), flush=True)
+
+
+def floor(tq4, torch, dev, rounds=2):
+    """Compute-free copies beside the real kernels (libtq4_floor.so, built by
+    `make -C ascend-micro-harness_amd/csrc floor`): the configs[2] decode's
+    chain by cumulative stage (0: launch and output words; 1: + phase 0;
+    2: + the strip loads of two pairs per wave and the merge barrier; 3: +
+    tickets, device-coherent record export, the last ticket's poll and
+    zeroing) on the headline's own cold workload and grid, and the configs[1]
+    writer's traffic (0: stores only; 1: loads and stores) on its own inputs.
+    Every case is timed as the bench rows are (1024 launches, graph replays),
+    `rounds` times alternating, in one process."""
+    import ctypes
+
+    class FloorDecode(ctypes.Structure):
+        _fields_ = [(n, ctypes.c_void_p) for n in (
+            "q", "key_cache", "value_cache", "scale_cache", "block_tables", "context_lens",
+            "pi_signs", "records", "tickets", "out")] + \
+            [(n, ctypes.c_uint32) for n in ("B", "Hq", "Hkv", "G", "S", "P", "max_blocks", "K",
+                                            "mode")]
+
+    class FloorWriter(ctypes.Structure):
+        _fields_ = [(n, ctypes.c_void_p) for n in (
+            "key", "value", "slots", "key_cache", "value_cache", "scale_cache")] + \
+            [(n, ctypes.c_uint32) for n in ("H", "D", "S", "P", "tokens", "mode")]
+
+    import __graft_entry__
+    lib = ctypes.CDLL(os.path.join(__graft_entry__.PKG_DIR, "libtq4_floor.so"))
+    for fn in (lib.tq4_floor_decode_launch, lib.tq4_floor_writer_launch):
+        fn.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+        fn.restype = ctypes.c_int
+    log(f"prefilling {SLICES} config-3 sequences ({SLICES * PAGES} pages)")
+    w = Workload(tq4, torch, dev, SLICES)
+    if w.splits != 16:
+        raise SystemExit(f"the decode floor copies the 16-split chain; auto splits gave {w.splits}")
+    records = torch.zeros(B * HQ * 16 * (D + 4), dtype=torch.float32, device=dev)
+    tickets = torch.zeros(B * HKV * 32, dtype=torch.int32, device=dev)
+    out = torch.empty((B, HQ, D), dtype=torch.bfloat16, device=dev)
+
+    def decode_case(mode):
+        ps = []
+        for i in range(SLICES):
+            fp = FloorDecode(w.q[i].data_ptr(), w.kc.data_ptr(), w.vc.data_ptr(),
+                             w.sc.data_ptr(), w.tables[i].data_ptr(), w.ctx.data_ptr(),
+                             w.signs.data_ptr(), records.data_ptr(), tickets.data_ptr(),
+                             out.data_ptr(), B, HQ, HKV, HQ // HKV, S, w.pool, PAGES, 16, mode)
+            ps.append(fp)
+
+        def launch(fp):
+            rc = lib.tq4_floor_decode_launch(torch.cuda.current_stream().cuda_stream,
+                                             ctypes.addressof(fp))
+            if rc != 0:
+                raise RuntimeError(f"tq4_floor_decode_launch returned {rc}")
+        return [lambda fp=fp: launch(fp) for fp in ps]
+
+    wr = WriterInputs(tq4, torch, dev, w, 32, 1024)
+
+    def writer_case(mode):
+        ps = []
+        for k, v, slots in wr.ins:
+            ps.append(FloorWriter(k.data_ptr(), v.data_ptr(), slots.data_ptr(), wr.kc.data_ptr(),
+                                  wr.vc.data_ptr(), wr.sc.data_ptr(), HKV, D, S, wr.pool,
+                                  wr.tokens, mode))
+
+        def launch(fp):
+            rc = lib.tq4_floor_writer_launch(torch.cuda.current_stream().cuda_stream,
+                                             ctypes.addressof(fp))
+            if rc != 0:
+                raise RuntimeError(f"tq4_floor_writer_launch returned {rc}")
+        return [lambda fp=fp: launch(fp) for fp in ps]
+
+    cases = [("decode_stage0", decode_case(0)), ("decode_stage1", decode_case(1)),
+             ("decode_stage2", decode_case(2)), ("decode_stage3", decode_case(3)),
+             ("decode", [lambda i=i: w.decode(i) for i in range(SLICES)]),
+             ("writer_stores", writer_case(0)), ("writer_loads_stores", writer_case(1)),
+             ("writer", [lambda i=i: wr.write(i) for i in range(len(wr.ins))])]
+    res = {name: [] for name, _ in cases}
+    for _ in range(rounds):
+        for name, fns in cases:
+            r = time_launches(torch, fns, 1024, 128)
+            res[name].append(round(r["ms"] * 1e3, 3))
+            log(f"{name}: {res[name][-1]} us")
+    torch.cuda.synchronize()
+    if int(tickets.abs().sum().item()) != 0:
+        raise RuntimeError("the decode floor left a ticket counter set")
+    print(json.dumps({
+        "floor_us": res,
+        "workload": "configs[2] cold (the headline's sequences, grid and buffers) and configs[1] "
+                    "(1024 BF16 tokens, 32 input sets); compute-free copies beside the real "
+                    "kernels, 1024-launch graphs, alternating",
+        "library": "libtq4_floor.so"}), flush=True)
 
 
 def pmc_row_names():

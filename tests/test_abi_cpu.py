@@ -263,3 +263,37 @@ def test_auto_splits_lens_rule(lib):
     assert f(16, 8, 256, 16, ps) == plain(16, 8, 256, 16)  # 128 items
     wide, pw = lens(np.random.default_rng(3).integers(1, 32769, 64))
     assert f(64, 8, 2048, 16, pw) == max(3, plain(64, 8, 2048, 16)) == 4
+
+
+def test_floor_library_refuses_other_geometry():
+    """libtq4_floor.so (bench.py --floor's compute-free copies) loads, exports
+    its two launchers, and refuses any geometry but the measured rows' before
+    it launches anything."""
+    path = os.path.join(REPO, "ascend-micro-harness_amd", "libtq4_floor.so")
+    if not os.path.exists(path):
+        pytest.skip("libtq4_floor.so is not built (make -C ascend-micro-harness_amd/csrc floor)")
+    fl = C.CDLL(path)
+    for fn in (fl.tq4_floor_decode_launch, fl.tq4_floor_writer_launch):
+        fn.argtypes = [C.c_void_p, C.c_void_p]
+        fn.restype = C.c_int
+
+    class FloorDecode(C.Structure):
+        _fields_ = [(f"p{i}", C.c_void_p) for i in range(10)] + \
+            [(n, C.c_uint32) for n in ("B", "Hq", "Hkv", "G", "S", "P", "max_blocks", "K", "mode")]
+
+    class FloorWriter(C.Structure):
+        _fields_ = [(f"p{i}", C.c_void_p) for i in range(6)] + \
+            [(n, C.c_uint32) for n in ("H", "D", "S", "P", "tokens", "mode")]
+
+    assert fl.tq4_floor_decode_launch(None, None) == -1
+    d = FloorDecode(B=1, Hq=32, Hkv=8, G=4, S=16, P=32768, max_blocks=256, K=16, mode=0)
+    for field, bad in (("G", 8), ("S", 32), ("K", 8), ("max_blocks", 128), ("mode", 4),
+                       ("Hq", 16)):
+        e = FloorDecode.from_buffer_copy(d)
+        setattr(e, field, bad)
+        assert fl.tq4_floor_decode_launch(None, C.addressof(e)) == -1, field
+    wp = FloorWriter(H=8, D=128, S=16, P=4096, tokens=1024, mode=0)
+    for field, bad in (("D", 64), ("S", 32), ("tokens", 1000), ("mode", 2)):
+        e = FloorWriter.from_buffer_copy(wp)
+        setattr(e, field, bad)
+        assert fl.tq4_floor_writer_launch(None, C.addressof(e)) == -1, field
