@@ -1,4 +1,4 @@
-// libtq4_floor.so: compute-free copies of two launches, for measurement only
+// libtq4_floor.so: compute-free copies of three launches, for measurement only
 // (bench.py --floor). Nothing in libtq4.so uses them.
 //
 // tq4_floor_decode_launch: the configs[2] decode's memory chain without its
@@ -18,6 +18,13 @@
 // and value rows in; one 64-byte key row per token, the 1 KiB value strip
 // and 32 scales out. mode 0 stores only; mode 1 loads and stores (each store
 // depends on the loaded words).
+//
+// tq4_floor_gather_launch: the configs[4] decode's cache reads without its
+// arithmetic, queue or combine: every listed strip (one live (sequence, kv
+// head, page) of 16 tokens: its 1 KiB key strip, 1 KiB value strip and two
+// 64-byte scale rows) is read once, four strips in flight per wave, over a
+// grid of the caller's size; the list is built on the host from the block
+// tables, so the kernel reads nothing but the cache and its own index.
 //
 // Geometry is fixed to the rows measured and checked on the host (-1
 // otherwise): decode d = 128, GQA 4, 16-token pages, K = 16, 256-page
@@ -50,6 +57,15 @@ struct FloorWriter {
     int8_t* value_cache;
     float* scale_cache;
     uint32_t H, D, S, P, tokens, mode;
+};
+
+struct FloorGather {
+    const int8_t* key_cache;
+    const int8_t* value_cache;
+    const float* scale_cache;
+    const uint32_t* rows;  // first cache row ((page * Hkv + head) * 16) of each strip
+    uint32_t* out;         // one word per workgroup
+    uint32_t n_rows, P, Hkv;
 };
 
 constexpr int kD = 128, kRS = kD + 4;
@@ -238,7 +254,59 @@ __global__ __launch_bounds__(256) void floor_writer_kernel(FloorWriter p)
     }
 }
 
+__global__ __launch_bounds__(256) void floor_gather_kernel(FloorGather p)
+{
+    const int lane = threadIdx.x & 63;
+    const uint32_t waves = gridDim.x * 4u;
+    const uint32_t w = blockIdx.x * 4u + (threadIdx.x >> 6);
+    const size_t plane = (size_t)p.P * p.Hkv * 16;
+    uint32_t acc = 0;
+    // rows of the next four strips, loaded one batch ahead (clamped indices)
+    uint32_t nxt[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) nxt[u] = p.rows[min(w + u * waves, p.n_rows - 1)];
+    for (uint32_t i = w; i < p.n_rows; i += 4 * waves) {
+        uint32_t cur[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) cur[u] = nxt[u];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) nxt[u] = p.rows[min(i + (4 + u) * waves, p.n_rows - 1)];
+        u4 kw[4], vw[4];
+        float sk[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            kw[u] = *(const u4*)(p.key_cache + (size_t)cur[u] * (kD / 2) + lane * 16);
+            vw[u] = *(const u4*)(p.value_cache + (size_t)cur[u] * (kD / 2) + lane * 16);
+            // lanes 0..15: key scales, 16..31: value scales, the rest reload the key scales
+            sk[u] = p.scale_cache[((lane >> 4) == 1 ? plane : 0) + cur[u] + (lane & 15)];
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const bool live = i + u * waves < p.n_rows;
+            const uint32_t x = kw[u][0] ^ kw[u][1] ^ kw[u][2] ^ kw[u][3] ^ vw[u][0] ^ vw[u][1] ^
+                               vw[u][2] ^ vw[u][3] ^ __float_as_uint(sk[u]);
+            acc ^= live ? x : 0u;
+        }
+    }
+    __shared__ uint32_t red[256];
+    red[threadIdx.x] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t a = 0;
+        for (int t = 0; t < 256; ++t) a ^= red[t];
+        p.out[blockIdx.x] = a;
+    }
+}
+
 }  // namespace
+
+extern "C" int tq4_floor_gather_launch(void* stream, const FloorGather* p, uint32_t workgroups)
+{
+    if (p == nullptr || p->n_rows == 0 || workgroups == 0 || workgroups > 65535) return -1;
+    hipLaunchKernelGGL(floor_gather_kernel, dim3(workgroups), dim3(256), 0, (hipStream_t)stream,
+                       *p);
+    return hipGetLastError() == hipSuccess ? 0 : -2;
+}
 
 extern "C" int tq4_floor_decode_launch(void* stream, const FloorDecode* p)
 {

@@ -784,10 +784,14 @@ def floor(tq4, torch, dev, rounds=2):
     chain by cumulative stage (0: launch and output words; 1: + phase 0;
     2: + the strip loads of two pairs per wave and the merge barrier; 3: +
     tickets, device-coherent record export, the last ticket's poll and
-    zeroing) on the headline's own cold workload and grid, and the configs[1]
-    writer's traffic (0: stores only; 1: loads and stores) on its own inputs.
-    Every case is timed as the bench rows are (1024 launches, graph replays),
-    `rounds` times alternating, in one process."""
+    zeroing) on the headline's own cold workload and grid; the configs[1]
+    writer's traffic (0: stores only; 1: loads and stores) on its own inputs;
+    and the configs[4] decode's cache strips read once each, at 2, 4 and 8
+    workgroups per CU, beside the real batched decode; and the strips of one
+    ctx-65536 sequence (rotated, cold) at 1 and 4 workgroups per CU, the
+    former the decode's K = 32 grid size. Every case is timed as
+    the bench rows are (graph replays), `rounds` times alternating, in one
+    process."""
     import ctypes
 
     class FloorDecode(ctypes.Structure):
@@ -802,11 +806,18 @@ def floor(tq4, torch, dev, rounds=2):
             "key", "value", "slots", "key_cache", "value_cache", "scale_cache")] + \
             [(n, ctypes.c_uint32) for n in ("H", "D", "S", "P", "tokens", "mode")]
 
+    class FloorGather(ctypes.Structure):
+        _fields_ = [(n, ctypes.c_void_p) for n in (
+            "key_cache", "value_cache", "scale_cache", "rows", "out")] + \
+            [(n, ctypes.c_uint32) for n in ("n_rows", "P", "Hkv")]
+
     import __graft_entry__
     lib = ctypes.CDLL(os.path.join(__graft_entry__.PKG_DIR, "libtq4_floor.so"))
     for fn in (lib.tq4_floor_decode_launch, lib.tq4_floor_writer_launch):
         fn.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
         fn.restype = ctypes.c_int
+    lib.tq4_floor_gather_launch.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint32]
+    lib.tq4_floor_gather_launch.restype = ctypes.c_int
     log(f"prefilling {SLICES} config-3 sequences ({SLICES * PAGES} pages)")
     w = Workload(tq4, torch, dev, SLICES)
     if w.splits != 16:
@@ -847,25 +858,91 @@ def floor(tq4, torch, dev, rounds=2):
                 raise RuntimeError(f"tq4_floor_writer_launch returned {rc}")
         return [lambda fp=fp: launch(fp) for fp in ps]
 
+    # the two batches the bench rotates, as strip lists
+    log("prefilling two configs[4] batches")
+    bats = [Batch(tq4, torch, dev, 0x71340050 + k, w.signs) for k in range(2)]
+    gbufs, gbytes = [], []
+    for b in bats:
+        rows = []
+        for i, c in enumerate(b.ctxs):
+            pages = (c + 1 + S - 1) // S  # the step's context: c + 1 tokens
+            phys = b.tab_np[i, :pages].astype(np.int64)
+            rows.append(((phys[:, None] * HKV + np.arange(HKV)[None, :]) * S).reshape(-1))
+        rows = np.concatenate(rows).astype(np.uint32)
+        gbufs.append((b, torch.from_numpy(rows.view(np.int32)).to(dev)))
+        gbytes.append(int(rows.size) * (S * D + 2 * S * 4))
+    gout = torch.zeros(65536, dtype=torch.int32, device=dev)
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+
+    def gather_case(per_cu):
+        ps = [FloorGather(b.kc.data_ptr(), b.vc.data_ptr(), b.sc.data_ptr(), rows.data_ptr(),
+                          gout.data_ptr(), rows.numel(), b.pool, HKV) for b, rows in gbufs]
+
+        def launch(fp):
+            rc = lib.tq4_floor_gather_launch(torch.cuda.current_stream().cuda_stream,
+                                             ctypes.addressof(fp), cus * per_cu)
+            if rc != 0:
+                raise RuntimeError(f"tq4_floor_gather_launch returned {rc}")
+        return [lambda fp=fp: launch(fp) for fp in ps]
+
+    # configs[3] ctx 65536: single sequences of random pool pages, rotated
+    # over enough of them that each is read cold (as the split sweep does)
+    lctx = 65536
+    lpages = lctx // S
+    nseq = max(4, (512 << 20) // (lctx * HKV * (D + 8)))
+    lrng = np.random.default_rng(0x71340004)
+    lrows = []
+    for _ in range(nseq):
+        phys = lrng.permutation(w.pool)[:lpages].astype(np.int64)
+        r = ((phys[:, None] * HKV + np.arange(HKV)[None, :]) * S).reshape(-1).astype(np.uint32)
+        lrows.append(torch.from_numpy(r.view(np.int32)).to(dev))
+    lbytes = lpages * HKV * (S * D + 2 * S * 4)
+
+    def long_case(per_cu):
+        ps = [FloorGather(w.kc.data_ptr(), w.vc.data_ptr(), w.sc.data_ptr(), rows.data_ptr(),
+                          gout.data_ptr(), rows.numel(), w.pool, HKV) for rows in lrows]
+
+        def launch(fp):
+            rc = lib.tq4_floor_gather_launch(torch.cuda.current_stream().cuda_stream,
+                                             ctypes.addressof(fp), cus * per_cu)
+            if rc != 0:
+                raise RuntimeError(f"tq4_floor_gather_launch returned {rc}")
+        return [lambda fp=fp: launch(fp) for fp in ps]
+
     cases = [("decode_stage0", decode_case(0)), ("decode_stage1", decode_case(1)),
              ("decode_stage2", decode_case(2)), ("decode_stage3", decode_case(3)),
              ("decode", [lambda i=i: w.decode(i) for i in range(SLICES)]),
              ("writer_stores", writer_case(0)), ("writer_loads_stores", writer_case(1)),
-             ("writer", [lambda i=i: wr.write(i) for i in range(len(wr.ins))])]
+             ("writer", [lambda i=i: wr.write(i) for i in range(len(wr.ins))]),
+             ("gather_2_per_cu", gather_case(2)), ("gather_4_per_cu", gather_case(4)),
+             ("gather_8_per_cu", gather_case(8)),
+             ("batched_decode", [b.decode for b in bats]),
+             ("ctx65536_gather_1_per_cu", long_case(1)), ("ctx65536_gather_4_per_cu", long_case(4))]
     res = {name: [] for name, _ in cases}
     for _ in range(rounds):
         for name, fns in cases:
-            r = time_launches(torch, fns, 1024, 128)
+            big = name.startswith(("gather", "batched", "ctx65536"))
+            r = time_launches(torch, fns, 32 if big else 1024, 4 if big else 128)
             res[name].append(round(r["ms"] * 1e3, 3))
             log(f"{name}: {res[name][-1]} us")
     torch.cuda.synchronize()
     if int(tickets.abs().sum().item()) != 0:
         raise RuntimeError("the decode floor left a ticket counter set")
+    cache_bytes = sum(gbytes) / len(gbytes)
+    tbs = {name: [round(cache_bytes / (us * 1e-6) / 1e12, 2) for us in res[name]]
+           for name in res if name.startswith(("gather", "batched"))}
+    ltbs = {name: [round(lbytes / (us * 1e-6) / 1e12, 2) for us in res[name]]
+            for name in res if name.startswith("ctx65536")}
     print(json.dumps({
         "floor_us": res,
-        "workload": "configs[2] cold (the headline's sequences, grid and buffers) and configs[1] "
-                    "(1024 BF16 tokens, 32 input sets); compute-free copies beside the real "
-                    "kernels, 1024-launch graphs, alternating",
+        "configs4_cache_bytes": int(cache_bytes),
+        "configs4_cache_TBps": tbs,
+        "ctx65536_cache_bytes": int(lbytes),
+        "ctx65536_cache_TBps": ltbs,
+        "workload": "configs[2] cold (the headline's sequences, grid and buffers), configs[1] "
+                    "(1024 BF16 tokens, 32 input sets) and configs[4] (its two batches rotated; "
+                    "cache strips only); compute-free copies beside the real kernels, graphs of "
+                    "1024 (32 for configs[4]) launches, alternating",
         "library": "libtq4_floor.so"}), flush=True)
 
 
