@@ -71,24 +71,42 @@ __device__ __forceinline__ float sqrt_rn(float x)
     return tiny ? s * 0x1.0p-16f : s;
 }
 
-// #{k : kPos[k] < a} for a >= 0 or +inf (a 3-step binary search).
-__device__ __forceinline__ uint32_t count_below(float a)
-{
-    uint32_t c = kPos[3] < a ? 4u : 0u;
-    c += (c ? kPos[5] : kPos[1]) < a ? 2u : 0u;
-    const float p = c == 0 ? kPos[0] : c == 2 ? kPos[2] : c == 4 ? kPos[4] : kPos[6];
-    c += p < a ? 1u : 0u;
-    return c;
-}
+// The level search by bins of |z| a quarter wide: bin b < 10 is [b/4,
+// (b+1)/4), bin 10 is [2.5, inf]. The positive thresholds lie more than a
+// quarter apart and none on a multiple of a quarter, so a bin holds at most
+// one of them: #{k : kPos[k] < a} = below + (inside < a) of a's bin, `below`
+// counting the thresholds under the bin and `inside` its own (+inf when it
+// has none). 4a and its truncation are exact, so the count is.
+struct LevelBin {
+    float inside;
+    uint32_t below;
+};
+constexpr int kLevelBins = 11;
+constexpr LevelBin kBins[kLevelBins] = {
+    {__builtin_inff(), 0}, {kPos[0], 0}, {kPos[1], 1}, {kPos[2], 2}, {kPos[3], 3},
+    {kPos[4], 4},          {__builtin_inff(), 5}, {kPos[5], 5}, {__builtin_inff(), 6},
+    {kPos[6], 6},          {__builtin_inff(), 7}};
+static_assert((int)(kPos[0] * 4) == 1 && (int)(kPos[1] * 4) == 2 && (int)(kPos[2] * 4) == 3 &&
+                  (int)(kPos[3] * 4) == 4 && (int)(kPos[4] * 4) == 5 &&
+                  (int)(kPos[5] * 4) == 7 && (int)(kPos[6] * 4) == 9,
+              "each threshold sits in the bin the table gives it");
+static_assert(kPos[0] * 4 != 1 && kPos[1] * 4 != 2 && kPos[2] * 4 != 3 && kPos[3] * 4 != 4 &&
+                  kPos[4] * 4 != 5 && kPos[5] * 4 != 7 && kPos[6] * 4 != 9,
+              "no threshold on a bin boundary");
 
-// The codec's level of z = y * (1/scale): #{i : t_i < z} (NaN -> 0).
-__device__ __forceinline__ uint32_t level_of(float z)
+// The codec's level of z = y * (1/scale): #{i : t_i < z} (NaN -> 0). lut:
+// kBins staged in LDS.
+__device__ __forceinline__ uint32_t level_of(float z, const LevelBin* lut)
 {
     const float a = fabsf(z);
     // for z < 0 the count is 7 - #{t_k <= |z|} = 7 - #{t_k < nextup(|z|)}
     const float up = __uint_as_float(min(__float_as_uint(a) + 1u, 0x7F800000u));
     const bool neg = z < 0.0f;
-    const uint32_t c = count_below(neg ? up : a);
+    const float b = neg ? up : a;
+    // truncation: a NaN gives bin 0, +inf saturates to the last bin
+    const uint32_t bin = min(__float2uint_rz(b * 4.0f), (uint32_t)(kLevelBins - 1));
+    const LevelBin e = lut[bin];
+    const uint32_t c = e.below + (e.inside < b ? 1u : 0u);
     return z > 0.0f ? 8u + c : neg ? 7u - c : (z == 0.0f ? 7u : 0u);
 }
 
@@ -103,6 +121,13 @@ __global__ __launch_bounds__(kRmsThreads) void rms_writer(
     constexpr int CPL = D / kRowLanes;
     const int lane = threadIdx.x & (kRowLanes - 1);
     const int l = row_lane(lane);  // logical lane: channels l*CPL ..
+    // the level search's bins, staged before any lane leaves
+    __shared__ LevelBin lut[kLevelBins];
+    if (threadIdx.x == 0) {
+#pragma unroll
+        for (int b = 0; b < kLevelBins; ++b) lut[b] = kBins[b];
+    }
+    __syncthreads();
     const uint64_t row = (uint64_t)blockIdx.x * (kRmsThreads / kRowLanes) + threadIdx.x / kRowLanes;
     const uint32_t planes = 2 * H;
     const uint64_t rows = (uint64_t)tokens * planes;
@@ -178,7 +203,7 @@ __global__ __launch_bounds__(kRmsThreads) void rms_writer(
     uint32_t pk[CPL / 8 > 0 ? CPL / 8 : 1] = {};
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
-        const uint32_t q = level_of(v[j] * rcp);
+        const uint32_t q = level_of(v[j] * rcp, lut);
         pk[j / 8] |= q << (4 * (j % 8));
     }
     int8_t* dst = (plane < H ? key_cache : value_cache) + ((uint64_t)slot * H + h) * (D / 2) +
