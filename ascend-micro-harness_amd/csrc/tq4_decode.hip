@@ -65,25 +65,44 @@
 namespace tq4 {
 
 // Phase stamps of the measurement build (make stamps: libtq4_stamps.so,
-// bench.py --phases): thread 0 of workgroup b < kStampBlocks writes the
-// 100 MHz realtime counter to slot [b][i] at each phase boundary -- 0 start,
-// 1 phase-0 loads retired, 2 first strip pairs issued, 3 q operands built,
-// 4 wave 0's strip loop done, 5 waves merged, 6 record exported (a split
-// that does not combine), 7 first row combined (poll complete + merge), 8
-// egress done (the combiner); slots a workgroup does not reach are 0. The
-// product library is built without them.
+// bench.py --phases): thread 0 of the workgroup running work item b <
+// kStampBlocks (blockIdx.x in the one-launch and partials grids; the queue
+// item in the persistent kernel, read from LDS, which the others avoid)
+// writes the 100 MHz realtime counter to slot [b][i] at each phase boundary -- 0 start, 1 phase-0 loads retired, 2 first strip pairs
+// issued, 3 q operands built, 4 wave 0's strip loop done, 5 waves merged, 6
+// record exported (a split that does not combine), 7 first row combined
+// (poll complete + merge), 8 egress done (the combiner); the persistent
+// kernel adds 9 its workgroup, 10 the item's start (before its coordinates),
+// 11 its end, 12 its sequence and 13 its split. Slots an item does not reach
+// keep an earlier launch's value. The product library is built without them.
 #ifdef TQ4_DECODE_STAMPS
 constexpr int kStampBlocks = 4096;
 constexpr int kStampSlots = 16;
 __device__ uint64_t g_decode_stamps[kStampBlocks * kStampSlots];
-#define TQ4_STAMP(i, v)                                                                \
-    do {                                                                               \
-        if (threadIdx.x == 0 && blockIdx.x < kStampBlocks)                             \
-            g_decode_stamps[blockIdx.x * kStampSlots + (i)] = (v);                     \
+__shared__ uint32_t g_stamp_item;  // the persistent kernel's current item
+#define TQ4_STAMP_ITEM(w)                       \
+    do {                                        \
+        if (threadIdx.x == 0) g_stamp_item = w; \
     } while (0)
+#define TQ4_STAMP_AT(b, i, v)                                                          \
+    do {                                                                               \
+        if (threadIdx.x == 0) {                                                        \
+            const uint32_t b_ = (b);                                                   \
+            if (b_ < kStampBlocks) g_decode_stamps[b_ * kStampSlots + (i)] = (v);      \
+        }                                                                              \
+    } while (0)
+// inside decode_item / finish_item (OWN is false only in the persistent kernel)
+#define TQ4_STAMP(i, v) TQ4_STAMP_AT(OWN ? blockIdx.x : g_stamp_item, i, v)
+#define TQ4_STAMP_P(i, v) TQ4_STAMP_AT(g_stamp_item, i, v)
 #else
+#define TQ4_STAMP_ITEM(w) \
+    do {                  \
+    } while (0)
 #define TQ4_STAMP(i, v) \
     do {                \
+    } while (0)
+#define TQ4_STAMP_P(i, v) \
+    do {                  \
     } while (0)
 #endif
 #define TQ4_NOW __builtin_amdgcn_s_memrealtime()
@@ -1445,7 +1464,12 @@ void decode_persistent_kernel(DecodeParams p)
     while (item < n_items) {
         uint32_t fetched = 0;
         uint32_t seq, kvh, split;
+        TQ4_STAMP_ITEM(item);
+        TQ4_STAMP_P(10, TQ4_NOW);
+        TQ4_STAMP_P(9, blockIdx.x);
         item_coords(p, item, n_full, full, splits, order, lpt, seq, kvh, split);
+        TQ4_STAMP_P(12, seq);
+        TQ4_STAMP_P(13, split);
         // the next item's queue fetch goes out after this item's first strip
         // loads (decode_item's hook); its value is read after the item
         decode_item<D, 1, false>(p, seq, kvh, split, [&]() {
@@ -1453,6 +1477,7 @@ void decode_persistent_kernel(DecodeParams p)
                 fetched = __hip_atomic_fetch_add(subq, 1u, __ATOMIC_RELAXED,
                                                  __HIP_MEMORY_SCOPE_AGENT);
         });
+        TQ4_STAMP_P(11, TQ4_NOW);
         if (tid == 0) {
             if (fetched == count - 1)
                 __hip_atomic_store(subq, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

@@ -36,7 +36,8 @@ Usage:
   python bench.py --summarize-pmc DIR [--pmc-merge]  # DIR/<row>/<pass>/run_counter_collection.csv
   python bench.py --pmc-table            # the committed summary as markdown
   python bench.py --summarize-trace DIR  # a rocprofv3 --kernel-trace csv run
-  python bench.py --phases               # configs[2] phase timeline (libtq4_stamps.so)
+  python bench.py --phases               # configs[2] phase timeline and the configs[4]
+                                         # per-item timeline (libtq4_stamps.so)
   python bench.py --floor                # compute-free floors (libtq4_floor.so)
 """
 from __future__ import annotations
@@ -586,8 +587,9 @@ def main():
     ap.add_argument("--pmc-rows", action="store_true", help="the rows --pmc-run knows")
     ap.add_argument("--phases", action="store_true",
                     help="configs[2] per-phase timeline from the measurement build's in-kernel "
-                         "stamps (libtq4_stamps.so), the split tail delta, and the host enqueue "
-                         "cost of one decode call")
+                         "stamps (libtq4_stamps.so), the split tail delta, the host enqueue "
+                         "cost of one decode call, and the configs[4] persistent decode's "
+                         "per-item timeline")
     ap.add_argument("--floor", action="store_true",
                     help="compute-free copies of the configs[2] decode chain and the configs[1] "
                          "writer traffic (libtq4_floor.so) beside the real kernels")
@@ -729,7 +731,8 @@ def phases(tq4, torch, dev, samples=64):
     workgroups of (stamp - the launch's first start), then the median over
     samples. The split tail delta is the slowest split's export minus the
     median split's. Host enqueue: wall time of eager tq4.paged_decode calls
-    (Python + ctypes + C ABI + launch), no synchronisation inside."""
+    (Python + ctypes + C ABI + launch), no synchronisation inside. Then the
+    configs[4] per-item timeline (batched_timeline)."""
     import ctypes as C
     lib_path = sys.modules[tq4.__name__ + ".tq4"].LIB_PATH
     assert lib_path.endswith("libtq4_stamps.so"), lib_path
@@ -775,7 +778,80 @@ def phases(tq4, torch, dev, samples=64):
                        "launches; stamps of the last launch (thread 0 of each workgroup)",
            "samples": samples, "workgroups": int(nblk), "library": "libtq4_stamps.so",
            "clock": "s_memrealtime, 100 MHz"}
+    res["configs4_timeline"] = batched_timeline(tq4, torch, dev, w.signs)
     print(json.dumps(res), flush=True)
+
+
+def batched_timeline(tq4, torch, dev, signs, samples=24, bin_us=2.0):
+    """The configs[4] persistent decode per queue item, from the measurement
+    build: graphs of 8 launches alternating the bench's two batches (each
+    read cold); after each replay the last launch's per-item stamps. Per
+    phase the median and 90th percentile over items; a least-squares fit of
+    item duration (start to end) = fixed + per_page * pages; and, per
+    `bin_us` bin from the launch's first item start, the items in flight and
+    the cache bytes streamed, each item's strips (pages x 2176 B) spread
+    evenly over its strip loop (first strip pairs issued to wave 0's loop
+    done) -- an attribution, not a counter. Medians over samples."""
+    import ctypes as C
+    bats = [Batch(tq4, torch, dev, 0x71340050 + k, signs) for k in range(2)]
+    K = bats[0].K
+    assert all(b.ctxs == bats[0].ctxs and b.K == K for b in bats)
+    pages_seq = np.array([(c + 1 + S - 1) // S for c in bats[0].ctxs])
+    width = -(-bats[0].tab_np.shape[1] // K)
+    n_items = int(HKV * (np.maximum(1, -(-pages_seq // width)) - 1).sum() + len(pages_seq) * HKV)
+    assert n_items <= 4096, n_items
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    g = _graph(torch, stream, [bats[i % 2].decode for i in range(8)])
+    buf = np.zeros((4096, 16), np.uint64)
+    names = (("queue item -> phase-0 loads retired", 10, 1),
+             ("phase-0 loads retired -> first strip pairs issued", 1, 2),
+             ("first strip pairs issued -> q operands built", 2, 3),
+             ("q operands built -> wave 0 strip loop done", 3, 4),
+             ("strip loop done -> waves merged", 4, 5), ("waves merged -> item end", 5, 11))
+    edges = np.arange(0.0, 200.0 + bin_us, bin_us)
+    fits, ends, last_start, bws, acts, phs = [], [], [], [], [], []
+    for k in range(samples + 2):
+        with torch.cuda.stream(stream):
+            g.replay()
+        torch.cuda.synchronize()
+        assert tq4.lib().tq4_decode_stamps(buf.ctypes.data_as(C.c_void_p), buf.nbytes) == 0
+        if k < 2:
+            continue  # the first replays warm the graph
+        st = buf[:n_items].astype(np.int64)
+        rel = (st - st[:, 10].min()) * 0.01  # 100 MHz counter -> us
+        pg = np.minimum(width, pages_seq[st[:, 12]] - st[:, 13] * width).astype(float)
+        start, end = rel[:, 10], rel[:, 11]
+        coef = np.linalg.lstsq(np.stack([np.ones_like(pg), pg], 1), end - start, rcond=None)[0]
+        fits.append(coef)
+        ends.append(end.max())
+        last_start.append(start.max())
+        phs.append([np.median(rel[:, b] - rel[:, a]) for _, a, b in names] +
+                   [np.percentile(rel[:, b] - rel[:, a], 90) for _, a, b in names])
+        bw = np.zeros(len(edges) - 1)
+        act = np.zeros(len(edges) - 1)
+        for a, b, nbytes, s0, s1 in zip(rel[:, 2], rel[:, 4], pg * (2 * S * D // 2 + 2 * S * 4),
+                                        start, end):
+            if b > a:
+                bw += nbytes * (np.clip(edges[1:], a, b) - np.clip(edges[:-1], a, b)) / (b - a)
+            act += (np.clip(edges[1:], s0, s1) - np.clip(edges[:-1], s0, s1)) / bin_us
+        bws.append(bw / (bin_us * 1e-6) / 1e12)
+        acts.append(act)
+    ph = np.median(np.array(phs), 0)
+    nb = int(np.ceil(np.median(ends) / bin_us))
+    fit = np.median(np.array(fits), 0)
+    return {
+        "splits": K, "items": n_items, "width_pages": int(width),
+        "phase_us_median_p90": {n: [round(float(ph[i]), 2), round(float(ph[i + len(names)]), 2)]
+                                for i, (n, _, _) in enumerate(names)},
+        "item_us_fit": {"fixed": round(float(fit[0]), 2), "per_page": round(float(fit[1]), 4)},
+        "last_item_start_us": round(float(np.median(last_start)), 2),
+        "launch_end_us": round(float(np.median(ends)), 2),
+        "bin_us": bin_us,
+        "items_in_flight": [round(float(x), 1) for x in np.median(np.array(acts), 0)[:nb]],
+        "attributed_TBps": [round(float(x), 2) for x in np.median(np.array(bws), 0)[:nb]],
+        "workload": "configs[4] decode (the bench's two batches alternating, K = the "
+                    "length-aware auto count), per-item stamps of the persistent kernel"}
 
 
 def floor(tq4, torch, dev, rounds=2):
