@@ -132,6 +132,48 @@ def test_multi_chunk_combine_one_launch(tq4, oracle, K):
         check_out(host(out), want, f"K {K} call {call}")
 
 
+def multi_call_case(tq4, oracle, rng, ctx, Hq, H, d, K, calls, label):
+    """`calls` decodes of one cache with fresh queries on one workspace, each
+    against the oracle (a consumed record left unzeroed would be taken by
+    the next call's poll)."""
+    import torch
+    P = sum((c + 15) // 16 for c in ctx) + 8
+    kc, vc, sc, tables, signs, isl = build_cache(oracle, rng, ctx, H, d, 16, P)
+    scale = np.float32(1 / math.sqrt(d))
+    ctx_a = np.array(ctx, np.int32)
+    ws = tq4.decode_workspace(len(ctx), Hq, H, d, K)
+    args = [dev(kc), dev(vc), dev(sc), dev(tables), dev(ctx_a), dev(signs)]
+    for call in range(calls):
+        q = f32_to_bf16(rng.standard_normal((len(ctx), Hq, d)).astype(np.float32))
+        _, want = oracle.paged_decode(q, kc, vc, sc, tables, ctx_a, signs, None, Hq, H, d, 16,
+                                      P, K, scale, isl, 1, threads=8)
+        out = tq4.paged_decode(dev(q), *args, H, 16, P, workspace=ws, num_splits=K,
+                               scale=float(scale), inv_sqrt_len=float(isl))
+        check_out(host(out), want, f"{label} call {call}")
+
+
+@pytest.mark.parametrize("d,K", [(64, 40), (256, 24)])
+def test_multi_chunk_combine_head_sizes(tq4, oracle, d, K):
+    """More than 16 live splits in the one-launch kernel at d = 64 (K = 40,
+    three poll chunks) and d = 256 (K = 24, two; 8 x 24 workgroups stay
+    within its 256 resident slots): the combiner's record loads, own-slot
+    substitution and zeroing in their two- and eight-word lane layouts."""
+    rng = np.random.default_rng(0x5E50 + d)
+    multi_call_case(tq4, oracle, rng, [4096 + 7], 32, 8, d, K, 2, f"d {d} K {K}")
+
+
+@pytest.mark.parametrize("d,K", [(128, 24), (128, 40), (256, 40)])
+def test_persistent_multi_chunk_combine(tq4, oracle, d, K):
+    """The persistent form with more than 16 live splits per (seq, kv head):
+    its combiner stores its own record and polls it with the others, chunk
+    by chunk (6 x 8 x K items exceed the resident workgroups: 512 at
+    d = 128, 256 at d = 256); ragged lengths with an empty and a one-page
+    sequence."""
+    rng = np.random.default_rng(0x5E60 + K + d)
+    multi_call_case(tq4, oracle, rng, [4103, 3001, 0, 17, 2500, 4096], 32, 8, d, K, 2,
+                    f"persistent d {d} K {K}")
+
+
 @pytest.fixture(scope="module")
 def long_context(oracle):
     """One ctx-32768 sequence (configs[3]'s longest), cache built once."""
