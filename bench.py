@@ -284,10 +284,14 @@ def summarize_pmc(root, merge=False):
         out[row] = e
     if not out:
         raise SystemExit(f"no profiled rows under {root}")
-    if merge and os.path.exists(PMC_FILE):
-        # a re-run of some rows: the others keep their committed figures
+    if os.path.exists(PMC_FILE):
         with open(PMC_FILE) as f:
-            out = {**json.load(f), **out}
+            old = json.load(f)
+        if merge:  # a re-run of some rows: the others keep their committed figures
+            out = {**old, **out}
+        elif set(old) - set(out):
+            raise SystemExit(f"{PMC_FILE} holds rows this run does not ({', '.join(sorted(set(old) - set(out)))}): "
+                             "pass --pmc-merge to keep them, or remove the file to replace it")
     os.makedirs(os.path.dirname(PMC_FILE), exist_ok=True)
     with open(PMC_FILE, "w") as f:
         json.dump(out, f, indent=1)
@@ -595,7 +599,8 @@ def main():
                          "writer traffic (libtq4_floor.so) beside the real kernels")
     ap.add_argument("--summarize-pmc", metavar="DIR")
     ap.add_argument("--pmc-merge", action="store_true",
-                    help="with --summarize-pmc: keep the committed rows not under DIR")
+                    help="with --summarize-pmc: keep the committed rows not under DIR "
+                         "(without it, a run that lacks committed rows is refused)")
     ap.add_argument("--pmc-table", action="store_true",
                     help="print the committed PMC summary as markdown")
     ap.add_argument("--summarize-trace", metavar="DIR")

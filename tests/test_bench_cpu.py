@@ -85,6 +85,30 @@ def test_pmc_summary_scales_by_the_calibration_copy(tmp_path, monkeypatch):
     assert r["frac"] == pytest.approx(4_473_860 / 1e-5 / 1e9 / 8000, abs=1e-4)
 
 
+def test_pmc_summary_keeps_committed_rows_only_when_merging(tmp_path, monkeypatch):
+    """Summarising a run of some rows over a summary that holds others is
+    refused unless merging, which keeps the others and replaces the re-run."""
+    pmc = tmp_path / "pmc.json"
+    monkeypatch.setattr(bench, "PMC_FILE", str(pmc))
+    pmc.write_text(json.dumps({"configs1_writer": {"kernel": "w", "workgroups": 512,
+                                                   "dispatches": 8, "counters": {}},
+                               "rms_writer": {"kernel": "old", "workgroups": 1024,
+                                              "dispatches": 8, "counters": {}}}))
+    copy = "void at::native::vectorized_elementwise_kernel<4, MulFunctor<float> >"
+    rms = "void tq4::(anonymous namespace)::rms_writer<128, 1>(tq4::RmsParams)"
+    cal_kib = bench.CALIB_BYTES / 1024
+    runs = tmp_path / "runs"
+    _write_counters(str(runs / "rms_writer" / "p1" / "run_counter_collection.csv"), [
+        (copy, 4096, "FETCH_SIZE", cal_kib), (rms, 1024, "FETCH_SIZE", 5.0)])
+    with pytest.raises(SystemExit, match="configs1_writer"):
+        bench.summarize_pmc(str(runs))
+    assert json.loads(pmc.read_text())["rms_writer"]["kernel"] == "old"  # untouched
+    bench.summarize_pmc(str(runs), merge=True)
+    out = json.loads(pmc.read_text())
+    assert set(out) == {"configs1_writer", "rms_writer"}
+    assert out["rms_writer"]["kernel"] != "old" and out["configs1_writer"]["kernel"] == "w"
+
+
 def test_trace_summary_limits_per_kernel_and_grid(tmp_path, capsys):
     cols = ["Kernel_Name", "Dispatch_Id", "Start_Timestamp", "End_Timestamp", "Grid_Size_X",
             "Grid_Size_Y", "Grid_Size_Z", "Workgroup_Size_X", "Workgroup_Size_Y",
