@@ -10,11 +10,16 @@
 //   packing          tests/common/lloydmax_oracle.hpp:58-62 (code i at bit (i*bits) % 8 of
 //                    byte i*bits/8)
 //
-// Every kernel is an elementwise HBM stream: a lane owns eight consecutive
-// elements (one 16-byte load of FP16/BF16, two of FP32), so a wave moves 1 KiB
-// or 2 KiB per load instruction, fully coalesced; codes leave as one 32-bit
-// (4-bit codes) or 16-bit (2-bit codes) store per lane. Grid-stride loops over
-// a grid sized to the device (a few waves per SIMD), so any length runs.
+// Every kernel is an elementwise HBM stream in which each load and store
+// instruction of a wave covers one contiguous span. ICDF: a lane owns eight
+// consecutive FP16/BF16 elements (one 16-byte load, a wave 1 KiB) and stores
+// their codes as one 32-bit word. FP32 Lloyd-Max / Gaussian-CDF: a lane owns
+// two quads of four elements, T lanes apart (a float4 each, a wave 1 KiB per
+// instruction, both loads in flight), and stores each quad's codes as one
+// 16-bit (4-bit codes) or 8-bit (2-bit codes) word; this measured 12 % faster
+// than eight consecutive elements per lane (two float4 loads 32 bytes apart
+// across the lanes). Grid-stride loops over a grid sized to the device (a few
+// waves per SIMD), so any length runs.
 //
 // Lloyd-Max codes without a table walk: the 4-bit thresholds are symmetric
 // about 0 (t[14-i] = -t[i], t[7] = 0), so the code is the sign plus a 3-step
@@ -129,32 +134,6 @@ __device__ __forceinline__ float lm_centroid(uint32_t q)
     }
 }
 
-__device__ __forceinline__ void load8(const float* src, float (&x)[8])
-{
-    const float4 a = *(const float4*)src;
-    const float4 b = *(const float4*)(src + 4);
-    x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
-    x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
-}
-
-__device__ __forceinline__ void store8(float* dst, const float (&y)[8])
-{
-    *(float4*)dst = make_float4(y[0], y[1], y[2], y[3]);
-    *(float4*)(dst + 4) = make_float4(y[4], y[5], y[6], y[7]);
-}
-
-template <int BITS>
-__device__ __forceinline__ void store_codes(uint8_t* codes, uint64_t g, const uint32_t (&q)[8])
-{
-    uint32_t w = 0;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) w |= q[i] << (BITS * i);
-    if constexpr (BITS == 4)
-        ((uint32_t*)codes)[g] = w;
-    else
-        ((uint16_t*)codes)[g] = (uint16_t)w;
-}
-
 // ---------------------------------------------------------------- kernels
 // book 0 Lloyd-Max, 1 Gaussian-CDF: FP32 -> codes (+ centroids when recon)
 template <int BITS, int BOOK>
@@ -163,11 +142,15 @@ __global__ __launch_bounds__(kCbThreads) void quantize_kernel(const float* __res
                                                               uint8_t* __restrict__ codes,
                                                               uint64_t groups)
 {
-    for (uint64_t g = (uint64_t)blockIdx.x * kCbThreads + threadIdx.x; g < groups;
-         g += (uint64_t)gridDim.x * kCbThreads) {
-        float x[8], y[8];
+    // quads of 4 values, lane-contiguous: quads u and u + T per iteration
+    const uint64_t nq = 2 * groups, T = (uint64_t)gridDim.x * kCbThreads;
+    for (uint64_t u = (uint64_t)blockIdx.x * kCbThreads + threadIdx.x; u < nq; u += 2 * T) {
+        const bool two = u + T < nq;
+        const float4 a = *(const float4*)(src + 4 * u);
+        float4 b = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (two) b = *(const float4*)(src + 4 * (u + T));
+        float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w}, y[8];
         uint32_t q[8];
-        load8(src + 8 * g, x);
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             if constexpr (BOOK == 0) {
@@ -177,8 +160,23 @@ __global__ __launch_bounds__(kCbThreads) void quantize_kernel(const float* __res
                 y[i] = cdf_centroid<BITS>(q[i]);
             }
         }
-        store_codes<BITS>(codes, g, q);
-        if (recon != nullptr) store8(recon + 8 * g, y);
+        uint32_t w0 = 0, w1 = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            w0 |= q[i] << (BITS * i);
+            w1 |= q[4 + i] << (BITS * i);
+        }
+        if constexpr (BITS == 4) {
+            ((uint16_t*)codes)[u] = (uint16_t)w0;
+            if (two) ((uint16_t*)codes)[u + T] = (uint16_t)w1;
+        } else {
+            codes[u] = (uint8_t)w0;
+            if (two) codes[u + T] = (uint8_t)w1;
+        }
+        if (recon != nullptr) {
+            *(float4*)(recon + 4 * u) = make_float4(y[0], y[1], y[2], y[3]);
+            if (two) *(float4*)(recon + 4 * (u + T)) = make_float4(y[4], y[5], y[6], y[7]);
+        }
     }
 }
 
@@ -188,13 +186,26 @@ __global__ __launch_bounds__(kCbThreads) void dequantize_kernel(const uint8_t* _
                                                                 float* __restrict__ recon,
                                                                 uint64_t groups)
 {
-    for (uint64_t g = (uint64_t)blockIdx.x * kCbThreads + threadIdx.x; g < groups;
-         g += (uint64_t)gridDim.x * kCbThreads) {
-        const uint32_t w = BITS == 4 ? ((const uint32_t*)codes)[g] : ((const uint16_t*)codes)[g];
+    // quads of 4 values, lane-contiguous: quads u and u + T per iteration
+    const uint64_t nq = 2 * groups, T = (uint64_t)gridDim.x * kCbThreads;
+    for (uint64_t u = (uint64_t)blockIdx.x * kCbThreads + threadIdx.x; u < nq; u += 2 * T) {
+        const bool two = u + T < nq;
+        uint32_t w0, w1 = 0;
+        if constexpr (BITS == 4) {
+            w0 = ((const uint16_t*)codes)[u];
+            if (two) w1 = ((const uint16_t*)codes)[u + T];
+        } else {
+            w0 = codes[u];
+            if (two) w1 = codes[u + T];
+        }
         float y[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) y[i] = lm_centroid<BITS>((w >> (BITS * i)) & ((1u << BITS) - 1u));
-        store8(recon + 8 * g, y);
+        for (int i = 0; i < 4; ++i) {
+            y[i] = lm_centroid<BITS>((w0 >> (BITS * i)) & ((1u << BITS) - 1u));
+            y[4 + i] = lm_centroid<BITS>((w1 >> (BITS * i)) & ((1u << BITS) - 1u));
+        }
+        *(float4*)(recon + 4 * u) = make_float4(y[0], y[1], y[2], y[3]);
+        if (two) *(float4*)(recon + 4 * (u + T)) = make_float4(y[4], y[5], y[6], y[7]);
     }
 }
 
