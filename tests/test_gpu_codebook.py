@@ -46,6 +46,18 @@ def test_icdf_reference_fixture(tq4, tag, dtype):
         assert np.array_equal(host(codes), f["packed"])
 
 
+@pytest.mark.parametrize("tag,dtype,bf16", [("fp16", torch.float16, 0), ("bf16", torch.bfloat16, 1)])
+def test_icdf_every_16bit_input(tq4, oracle, tag, dtype, bf16):
+    """Every one of the 65536 input bit patterns (zeros, subnormals, both
+    infinities, every NaN) against the C oracle's double evaluation: the
+    codes agree bit for bit everywhere, not only on the fixture's inputs."""
+    h = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
+    out = host(tq4.icdf_quantize(dev16(h, dtype)))
+    want = oracle.icdf_quantize(h, bf16)
+    bad = np.nonzero(out != want)[0]
+    assert bad.size == 0, f"{tag}: {bad.size} bytes differ, first pairs at {bad[:8] * 2}"
+
+
 def test_icdf_specials(tq4, oracle):
     x = np.array([0.0, -0.0, 100.0, -100.0, np.inf, -np.inf, np.nan, 60000.0] * 128, np.float32)
     h = x.astype(np.float16).view(np.uint16)
