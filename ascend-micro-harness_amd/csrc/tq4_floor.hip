@@ -1,4 +1,4 @@
-// libtq4_floor.so: compute-free copies of three launches, for measurement only
+// libtq4_floor.so: compute-free copies of four launches, for measurement only
 // (bench.py --floor). Nothing in libtq4.so uses them.
 //
 // tq4_floor_decode_launch: the configs[2] decode's memory chain without its
@@ -19,6 +19,12 @@
 // and 32 scales out. mode 0 stores only; mode 1 loads and stores (each store
 // depends on the loaded words).
 //
+// tq4_floor_scatter_launch: the token scatter writer's traffic without its
+// arithmetic (configs[1]'s secondary row, and the configs[4] step's writer):
+// per (token, kv head) the slot and the two BF16 rows in, the token's value
+// strip read after the slot and written back whole, its key row and two
+// scales out; mode 0 stores only, mode 1 loads and stores.
+//
 // tq4_floor_gather_launch: the configs[4] decode's cache reads without its
 // arithmetic, queue or combine: every listed strip (one live (sequence, kv
 // head, page) of 16 tokens: its 1 KiB key strip, 1 KiB value strip and two
@@ -28,8 +34,8 @@
 //
 // Geometry is fixed to the rows measured and checked on the host (-1
 // otherwise): decode d = 128, GQA 4, 16-token pages, K = 16, 256-page
-// tables (16 pages = 8 strip pairs per split, two per wave); writer d = 128,
-// 16-token pages, whole strips.
+// tables (16 pages = 8 strip pairs per split, two per wave); writers d = 128,
+// 16-token pages (whole strips for the strip writer's copy).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -50,6 +56,16 @@ struct FloorDecode {
 };
 
 struct FloorWriter {
+    const uint16_t* key;
+    const uint16_t* value;
+    const int32_t* slots;
+    int8_t* key_cache;
+    int8_t* value_cache;
+    float* scale_cache;
+    uint32_t H, D, S, P, tokens, mode;
+};
+
+struct FloorScatter {
     const uint16_t* key;
     const uint16_t* value;
     const int32_t* slots;
@@ -254,6 +270,45 @@ __global__ __launch_bounds__(256) void floor_writer_kernel(FloorWriter p)
     }
 }
 
+// The token scatter's traffic without its arithmetic: per (token, kv head)
+// item, a 16-lane group as in the scatter writer, sixteen items a workgroup.
+// mode 0 stores only (the token's key row, its whole 1 KiB value strip and
+// two scales, at a strip of its own); mode 1 adds the slot, the two BF16 rows
+// and, after the slot, the value strip's read (each store depends on the
+// loaded words).
+__global__ __launch_bounds__(256) void floor_scatter_kernel(FloorScatter p)
+{
+    const int tid = threadIdx.x, l = tid & 15;
+    const uint32_t item = blockIdx.x * 16 + (tid >> 4);
+    if (item >= p.tokens * p.H) return;
+    const uint32_t tok = item / p.H, h = item % p.H;
+    uint32_t x = 0x11u;
+    int32_t slot = (int32_t)(tok * 16u);
+    u4 sw[4] = {u4{0u, 0u, 0u, 0u}, u4{0u, 0u, 0u, 0u}, u4{0u, 0u, 0u, 0u}, u4{0u, 0u, 0u, 0u}};
+    if (p.mode >= 1) {
+        slot = p.slots[tok];
+        const u4 kw = *(const u4*)(p.key + ((size_t)tok * p.H + h) * kD + l * 8);
+        const u4 vw = *(const u4*)(p.value + ((size_t)tok * p.H + h) * kD + l * 8);
+        x = kw[0] ^ kw[1] ^ kw[2] ^ kw[3] ^ vw[0] ^ vw[1] ^ vw[2] ^ vw[3];
+        const uint32_t pg = (uint32_t)slot / 16u;
+        const size_t srow = ((size_t)(pg < p.P ? pg : 0u) * p.H + h) * 16;
+        const u4* strip = (const u4*)(p.value_cache + srow * 64 + (size_t)l * 64);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sw[i] = strip[i];
+    }
+    const uint32_t page = (uint32_t)slot / 16u, tip = (uint32_t)slot % 16u;
+    if (page >= p.P) return;  // the slots name pages of the pool
+    const size_t srow = ((size_t)page * p.H + h) * 16;
+    *(uint32_t*)(p.key_cache + (srow + tip) * 64 + (size_t)l * 4) = x;
+    u4* dst = (u4*)(p.value_cache + srow * 64 + (size_t)l * 64);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dst[i] = sw[i] ^ u4{x, x, x, x};
+    if (l == 0) {
+        p.scale_cache[srow + tip] = (float)(x & 0xff);
+        p.scale_cache[(size_t)p.P * p.H * 16 + srow + tip] = (float)(x & 0xff);
+    }
+}
+
 __global__ __launch_bounds__(256) void floor_gather_kernel(FloorGather p)
 {
     const int lane = threadIdx.x & 63;
@@ -299,6 +354,17 @@ __global__ __launch_bounds__(256) void floor_gather_kernel(FloorGather p)
 }
 
 }  // namespace
+
+extern "C" int tq4_floor_scatter_launch(void* stream, const FloorScatter* p)
+{
+    if (p == nullptr || p->D != 128 || p->S != 16 || p->tokens == 0 || p->mode > 1 ||
+        (uint64_t)p->tokens * p->H > (1ull << 26))
+        return -1;
+    const uint32_t items = p->tokens * p->H;
+    hipLaunchKernelGGL(floor_scatter_kernel, dim3((items + 15) / 16), dim3(256), 0,
+                       (hipStream_t)stream, *p);
+    return hipGetLastError() == hipSuccess ? 0 : -2;
+}
 
 extern "C" int tq4_floor_gather_launch(void* stream, const FloorGather* p, uint32_t workgroups)
 {

@@ -867,6 +867,8 @@ def floor(tq4, torch, dev, rounds=2):
     tickets, device-coherent record export, the last ticket's poll and
     zeroing) on the headline's own cold workload and grid; the configs[1]
     writer's traffic (0: stores only; 1: loads and stores) on its own inputs;
+    the same two stages for the token scatter (configs[1]'s secondary row:
+    slot, rows and the dependent value-strip read, strip written back whole);
     and the configs[4] decode's cache strips read once each, at 2, 4 and 8
     workgroups per CU, beside the real batched decode; and the strips of one
     ctx-65536 sequence (rotated, cold) at 1 and 4 workgroups per CU, the
@@ -887,6 +889,11 @@ def floor(tq4, torch, dev, rounds=2):
             "key", "value", "slots", "key_cache", "value_cache", "scale_cache")] + \
             [(n, ctypes.c_uint32) for n in ("H", "D", "S", "P", "tokens", "mode")]
 
+    class FloorScatter(ctypes.Structure):
+        _fields_ = [(n, ctypes.c_void_p) for n in (
+            "key", "value", "slots", "key_cache", "value_cache", "scale_cache")] + \
+            [(n, ctypes.c_uint32) for n in ("H", "D", "S", "P", "tokens", "mode")]
+
     class FloorGather(ctypes.Structure):
         _fields_ = [(n, ctypes.c_void_p) for n in (
             "key_cache", "value_cache", "scale_cache", "rows", "out")] + \
@@ -894,7 +901,8 @@ def floor(tq4, torch, dev, rounds=2):
 
     import __graft_entry__
     lib = ctypes.CDLL(os.path.join(__graft_entry__.PKG_DIR, "libtq4_floor.so"))
-    for fn in (lib.tq4_floor_decode_launch, lib.tq4_floor_writer_launch):
+    for fn in (lib.tq4_floor_decode_launch, lib.tq4_floor_writer_launch,
+               lib.tq4_floor_scatter_launch):
         fn.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
         fn.restype = ctypes.c_int
     lib.tq4_floor_gather_launch.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint32]
@@ -938,6 +946,32 @@ def floor(tq4, torch, dev, rounds=2):
             if rc != 0:
                 raise RuntimeError(f"tq4_floor_writer_launch returned {rc}")
         return [lambda fp=fp: launch(fp) for fp in ps]
+
+    # configs[1] secondary: the scatter row's own inputs (one token in each of
+    # 1024 distinct strips, random positions), built as extra_workloads does
+    srng = np.random.default_rng(0x71340012)
+    sins = []
+    for k, v, _ in wr.ins:
+        strips = srng.permutation(wr.pool * S // 16)[:wr.tokens]
+        sins.append((k, v, torch.from_numpy(
+            (strips * 16 + srng.integers(0, 16, wr.tokens)).astype(np.int32)).to(dev)))
+
+    def scatter_case(mode):
+        ps = [FloorScatter(k.data_ptr(), v.data_ptr(), sl.data_ptr(), wr.kc.data_ptr(),
+                           wr.vc.data_ptr(), wr.sc.data_ptr(), HKV, D, S, wr.pool, wr.tokens,
+                           mode) for k, v, sl in sins]
+
+        def launch(fp):
+            rc = lib.tq4_floor_scatter_launch(torch.cuda.current_stream().cuda_stream,
+                                              ctypes.addressof(fp))
+            if rc != 0:
+                raise RuntimeError(f"tq4_floor_scatter_launch returned {rc}")
+        return [lambda fp=fp: launch(fp) for fp in ps]
+
+    def real_scatter(i):
+        k, v, sl = sins[i]
+        tq4.reshape_scatter(k, v, wr.kc, wr.vc, wr.sc, sl, w.signs, num_blocks=wr.pool,
+                            block_size=S, inv_sqrt_len=w.isl)
 
     # the two batches the bench rotates, as strip lists
     log("prefilling two configs[4] batches")
@@ -995,6 +1029,8 @@ def floor(tq4, torch, dev, rounds=2):
              ("decode", [lambda i=i: w.decode(i) for i in range(SLICES)]),
              ("writer_stores", writer_case(0)), ("writer_loads_stores", writer_case(1)),
              ("writer", [lambda i=i: wr.write(i) for i in range(len(wr.ins))]),
+             ("scatter_stores", scatter_case(0)), ("scatter_loads_stores", scatter_case(1)),
+             ("scatter", [lambda i=i: real_scatter(i) for i in range(len(sins))]),
              ("gather_2_per_cu", gather_case(2)), ("gather_4_per_cu", gather_case(4)),
              ("gather_8_per_cu", gather_case(8)),
              ("batched_decode", [b.decode for b in bats]),
@@ -1021,9 +1057,10 @@ def floor(tq4, torch, dev, rounds=2):
         "ctx65536_cache_bytes": int(lbytes),
         "ctx65536_cache_TBps": ltbs,
         "workload": "configs[2] cold (the headline's sequences, grid and buffers), configs[1] "
-                    "(1024 BF16 tokens, 32 input sets) and configs[4] (its two batches rotated; "
-                    "cache strips only); compute-free copies beside the real kernels, graphs of "
-                    "1024 (32 for configs[4]) launches, alternating",
+                    "(1024 BF16 tokens, 32 input sets; the strip writer and the token scatter "
+                    "at one token per strip) and configs[4] (its two batches rotated; cache "
+                    "strips only); compute-free copies beside the real kernels, graphs of 1024 "
+                    "(32 for configs[4]) launches, alternating",
         "library": "libtq4_floor.so"}), flush=True)
 
 

@@ -267,13 +267,14 @@ def test_auto_splits_lens_rule(lib):
 
 def test_floor_library_refuses_other_geometry():
     """libtq4_floor.so (bench.py --floor's compute-free copies) loads, exports
-    its two launchers, and refuses any geometry but the measured rows' before
-    it launches anything."""
+    its launchers, and refuses any geometry but the measured rows' before it
+    launches anything."""
     path = os.path.join(REPO, "ascend-micro-harness_amd", "libtq4_floor.so")
     if not os.path.exists(path):
         pytest.skip("libtq4_floor.so is not built (make -C ascend-micro-harness_amd/csrc floor)")
     fl = C.CDLL(path)
-    for fn in (fl.tq4_floor_decode_launch, fl.tq4_floor_writer_launch):
+    for fn in (fl.tq4_floor_decode_launch, fl.tq4_floor_writer_launch,
+               fl.tq4_floor_scatter_launch):
         fn.argtypes = [C.c_void_p, C.c_void_p]
         fn.restype = C.c_int
 
@@ -297,3 +298,10 @@ def test_floor_library_refuses_other_geometry():
         e = FloorWriter.from_buffer_copy(wp)
         setattr(e, field, bad)
         assert fl.tq4_floor_writer_launch(None, C.addressof(e)) == -1, field
+    # the token scatter's copy shares the writer's argument block
+    sp = FloorWriter(H=8, D=128, S=16, P=4096, tokens=1024, mode=0)
+    for field, bad in (("D", 256), ("S", 64), ("tokens", 0), ("mode", 2)):
+        e = FloorWriter.from_buffer_copy(sp)
+        setattr(e, field, bad)
+        assert fl.tq4_floor_scatter_launch(None, C.addressof(e)) == -1, field
+    assert fl.tq4_floor_scatter_launch(None, None) == -1
